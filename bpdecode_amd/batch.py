@@ -1,0 +1,233 @@
+"""Continuous-batching constraint state (batch.py of the reference).
+
+:class:`ConstraintBatch` keeps one int32 DFA state per slot in a device pool.
+``apply_mask`` and ``commit`` are one kernel launch each: the slot gather
+``pool[slots]`` is fused into the mask kernel, and the commit kernel gathers,
+advances and scatters back in one pass.  Slot writes from ``add`` / ``evict``
+/ ``reset`` are queued on the host and applied in one scatter before the pool
+is next read, so per-request churn costs no launches of its own.
+"""
+
+from __future__ import annotations
+
+from collections import OrderedDict, defaultdict
+from collections.abc import Hashable, Sequence
+
+import torch
+
+from . import ops
+from .ops import FsaTensors, advance_state, apply_mask_, apply_soft_
+from .tokenizer import Vocabulary
+
+FREE = -2  # slot holds no sequence
+BROKEN = -1  # a committed token left the grammar (matches step() == -1)
+
+
+class MaskCache:
+    """LRU of allowed-token ids per DFA state (batch.py:35-86 of the
+    reference); the ids come from the packed allow-bit kernel."""
+
+    def __init__(self, fsa: FsaTensors, max_states: int = 512) -> None:
+        self._fsa = fsa
+        self._vocab = int(fsa.offsets.numel() - 1)
+        self._max = max_states
+        self._allowed: OrderedDict[int, torch.Tensor] = OrderedDict()
+
+    def _compute(self, state: int) -> torch.Tensor:
+        st = torch.tensor([state], dtype=torch.int32, device=self._fsa.device)
+        if state < 0:
+            return torch.empty(0, dtype=torch.long, device=self._fsa.device)
+        bits = ops.compute_mask(self._fsa, st)[0].to(torch.int64) & 0xFFFFFFFF
+        t = torch.arange(self._vocab, device=bits.device)
+        on = (bits[t >> 5] >> (t & 31)) & 1
+        return on.nonzero(as_tuple=False).squeeze(1).to(torch.long)
+
+    def allowed_ids(self, state: int) -> torch.Tensor:
+        hit = self._allowed.get(state)
+        if hit is not None:
+            self._allowed.move_to_end(state)
+            return hit
+        ids = self._compute(state)
+        self._allowed[state] = ids
+        if len(self._allowed) > self._max:
+            self._allowed.popitem(last=False)
+        return ids
+
+    def __len__(self) -> int:
+        return len(self._allowed)
+
+    def apply(self, states: torch.Tensor, logits: torch.Tensor, neg_inf: float = float("-inf")):
+        """In place: mask ``logits`` [n, vocab] given one state per row."""
+        by_state: dict[int, list[int]] = defaultdict(list)
+        for i, s in enumerate(states.tolist()):
+            by_state[s].append(i)
+        for state, rows in by_state.items():
+            allowed = self.allowed_ids(state).to(logits.device)
+            r = torch.tensor(rows, device=logits.device)
+            keep = logits.index_select(0, r).index_select(1, allowed)
+            logits[r] = neg_inf
+            logits[r.unsqueeze(1), allowed] = keep
+        return logits
+
+
+class GrammarCache:
+    """LRU of compiled grammars for one vocabulary and device."""
+
+    def __init__(self, vocab: Vocabulary, device: torch.device | str = "cpu", max_size: int = 128) -> None:
+        self._vocab = vocab
+        self._device = torch.device(device)
+        self._max = max_size
+        self._cache: OrderedDict[str, FsaTensors] = OrderedDict()
+
+    def get(self, pattern: str) -> FsaTensors:
+        hit = self._cache.get(pattern)
+        if hit is not None:
+            self._cache.move_to_end(pattern)
+            return hit
+        fsa = FsaTensors.build(pattern, self._vocab).to(self._device)
+        if fsa.tok_next is None and self._device.type == "cuda":
+            fsa = fsa.densify()  # built on the device by the table-builder kernel
+        self._cache[pattern] = fsa
+        if len(self._cache) > self._max:
+            self._cache.popitem(last=False)
+        return fsa
+
+    def __len__(self) -> int:
+        return len(self._cache)
+
+
+def index_tensor(values: Sequence[int], device: torch.device) -> torch.Tensor:
+    """int64 tensor of ``values`` on ``device`` (pinned staging for a device)."""
+    if device.type != "cuda":
+        return torch.tensor(values, dtype=torch.long)
+    host = torch.empty(len(values), dtype=torch.long, pin_memory=True)
+    host.numpy()[:] = values
+    return host.to(device, non_blocking=True)
+
+
+class ConstraintBatch:
+    """Fixed-capacity pool of grammar states sharing one :class:`FsaTensors`
+    (batch.py:118-226 of the reference)."""
+
+    def __init__(self, fsa: FsaTensors, capacity: int, device=None,
+                 mask_cache: bool | MaskCache = False) -> None:
+        self.fsa = fsa if device is None else fsa.to(device)
+        self.device = self.fsa.device
+        self.capacity = capacity
+        self._pool = torch.full((capacity,), FREE, dtype=torch.int32, device=self.device)
+        self._pending: dict[int, int] = {}
+        self._slot_of: dict[Hashable, int] = {}
+        self._free: list[int] = list(reversed(range(capacity)))
+        self._version = 0
+        self._slot_key: tuple | None = None
+        self._slot_tensor: torch.Tensor | None = None
+        self._err = torch.zeros(1, dtype=torch.int32, device=self.device) if self.device.type == "cuda" else None
+        if mask_cache is True:
+            mask_cache = MaskCache(self.fsa)
+        self.cache: MaskCache | None = mask_cache or None
+
+    # --- pool -----------------------------------------------------------
+    def _flush(self) -> None:
+        if self._pending:
+            idx = index_tensor(list(self._pending.keys()), self.device)
+            val = torch.tensor(list(self._pending.values()), dtype=torch.int32)
+            self._pool.index_put_((idx,), val.to(self.device, non_blocking=True))
+            self._pending.clear()
+
+    @property
+    def _state(self) -> torch.Tensor:
+        """The state pool (pending slot writes applied)."""
+        self._flush()
+        return self._pool
+
+    # --- lifecycle -------------------------------------------------------
+    def add(self, seq_id: Hashable) -> int:
+        if seq_id in self._slot_of:
+            raise KeyError(f"sequence {seq_id!r} already in the batch")
+        if not self._free:
+            raise RuntimeError("ConstraintBatch is at capacity")
+        slot = self._free.pop()
+        self._slot_of[seq_id] = slot
+        self._pending[slot] = self.fsa.start
+        self._version += 1
+        return slot
+
+    def evict(self, seq_id: Hashable) -> None:
+        slot = self._slot_of.pop(seq_id)
+        self._pending[slot] = FREE
+        self._free.append(slot)
+        self._version += 1
+
+    def reset(self, seq_id: Hashable) -> None:
+        self._pending[self._slot_of[seq_id]] = self.fsa.start
+
+    def __len__(self) -> int:
+        return len(self._slot_of)
+
+    def __contains__(self, seq_id: Hashable) -> bool:
+        return seq_id in self._slot_of
+
+    # --- per step ----------------------------------------------------------
+    def _slots(self, seq_ids: Sequence[Hashable]) -> torch.Tensor:
+        key = (self._version, tuple(seq_ids))
+        if key != self._slot_key:
+            slot_of = self._slot_of
+            self._slot_tensor = index_tensor([slot_of[s] for s in seq_ids], self.device)
+            self._slot_key = key
+        return self._slot_tensor
+
+    def apply_mask(self, seq_ids: Sequence[Hashable], logits: torch.Tensor,
+                   neg_inf: float = float("-inf")) -> torch.Tensor:
+        """In place: every grammar-disallowed logit of ``logits``
+        [len(seq_ids), vocab] becomes ``neg_inf``."""
+        slots = self._slots(seq_ids)
+        pool = self._state
+        if self.cache is not None:
+            self.cache.apply(pool[slots], logits, neg_inf)
+        elif self.fsa.tok_next is not None:
+            ops.dense_mask_(logits, self.fsa.tok_next, pool, slots, neg_inf, self._err)
+        else:
+            apply_mask_(logits, self.fsa, pool[slots], neg_inf)
+        return logits
+
+    def apply_soft(self, seq_ids: Sequence[Hashable], logits: torch.Tensor, alpha: float = 1.0):
+        """In place: ``logits += alpha * lookahead[state]`` (and mask)."""
+        if self.fsa.lookahead is None:
+            raise ValueError("fsa has no lookahead table; build with dense + with_lookahead")
+        slots = self._slots(seq_ids)
+        ops.soft_apply_(logits, self.fsa.lookahead, self._state, slots, alpha)
+        return logits
+
+    def commit(self, seq_ids: Sequence[Hashable], tokens: torch.Tensor) -> torch.Tensor:
+        """Advance each sequence by its sampled token; returns the new states
+        (``BROKEN`` where the token was off a valid path)."""
+        slots = self._slots(seq_ids)
+        pool = self._state
+        if self.fsa.tok_next is not None:
+            return ops.dense_advance(self.fsa.tok_next, pool, tokens, slots, True, self._err)
+        nxt = advance_state(self.fsa, pool[slots], tokens.to(torch.int32))
+        pool[slots] = nxt
+        return nxt
+
+    def check_errors(self) -> None:
+        """Raise if a device kernel met an out-of-range state or token since
+        the last check (synchronises with the device)."""
+        if self._err is None:
+            return
+        flags = int(self._err.item())
+        if flags:
+            self._err.zero_()
+            raise IndexError(f"out-of-range index in a device constraint kernel (flags {flags})")
+
+    # --- queries -----------------------------------------------------------
+    def state_of(self, seq_id: Hashable) -> int:
+        slot = self._slot_of[seq_id]
+        if slot in self._pending:
+            return self._pending[slot]
+        return int(self._pool[slot])
+
+    def is_complete(self, seq_id: Hashable) -> bool:
+        return self.state_of(seq_id) in self.fsa.accepting
+
+    def is_broken(self, seq_id: Hashable) -> bool:
+        return self.state_of(seq_id) == BROKEN

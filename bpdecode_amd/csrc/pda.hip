@@ -1,0 +1,491 @@
+// Config-set PDA step on gfx950: token mask (fused into the logits or packed
+// bits) and the per-row commit, plus the host forms of both and pda_init.
+//
+// Mask kernel: one wave64 per (row, vocab chunk).  The row's config-set is
+// staged in LDS (int32 layout) and shared by the wave; each lane walks one
+// token at a time through its own two LDS config-sets (LaneView, 16-bit
+// frames, lane-interleaved).  Before walking, the wave evaluates all 256
+// first bytes from the row's set (4 per lane) and packs the survivors into a
+// 256-bit table with ballots, so a token whose first byte empties the set is
+// rejected with one bit test.  Verdicts of the 64 lanes are written as one
+// coalesced store (logits) or packed into two words with a ballot (bits).
+//
+// Commit kernel: one thread per row with two int32 config-sets in LDS; the
+// walk starts from the row's set in global memory and every byte step writes
+// a freshly cleared set, so the 266 words written back on acceptance are
+// exactly those the reference produces.
+#include <vector>
+
+#include "bpd_common.hpp"
+#include "pda_core.hpp"
+
+namespace bpd {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kCommitRows = 16;
+
+struct MaskArgs {
+  PdaTableView g;
+  const int32_t* tok_off;
+  const uint8_t* tok_bytes;
+  int32_t vocab;
+  int32_t eos;
+  const int32_t* configs;
+  const int64_t* slots;
+  const uint8_t* broken;
+  int64_t rows;
+  uint8_t* logits;  // null when writing bits
+  int64_t ld_bytes;
+  int32_t elem;
+  uint32_t fill;
+  uint32_t* bits;  // null when writing logits
+  int64_t words;
+  int32_t chunk_tokens;  // multiple of 64
+  int32_t* err;
+};
+
+// Structural check of a row's config-set before any table lookup with its
+// frames: counts in range and every frame a valid state id.
+__device__ bool config_ok(const int32_t* c, int32_t num_states, int lane) {
+  const int n = c[0];
+  bool ok = n >= 0 && n <= kMaxConfigs;
+  if (lane < kMaxConfigs) {
+    const int d = c[2 + lane];
+    ok = ok && (lane >= n || (d >= 0 && d <= kMaxDepth));
+  }
+  for (int f = lane; f < kMaxConfigs * kMaxDepth; f += kWave) {
+    const int i = f / kMaxDepth, k = f % kMaxDepth;
+    if (i < n && i < kMaxConfigs) {
+      const int d = c[2 + i];
+      if (d >= 0 && d <= kMaxDepth && k < d) {
+        const int v = c[2 + kMaxConfigs + f];
+        ok = ok && v >= 0 && v < num_states;
+      }
+    }
+  }
+  return __ballot(!ok) == 0;
+}
+
+__global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
+  __shared__ int32_t row_cfg[kConfigWords];
+  __shared__ uint32_t lane_sets[2 * kLaneWords * kWave];
+  __shared__ uint32_t first_ok[8];
+
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t row = a.slots ? a.slots[b] : b;
+  for (int k = lane; k < kConfigWords; k += kWave) row_cfg[k] = a.configs[row * kConfigWords + k];
+  __syncthreads();
+
+  bool dead_row = a.broken != nullptr && a.broken[row] != 0;
+  if (!config_ok(row_cfg, a.g.num_states, lane)) {
+    if (lane == 0 && blockIdx.x == 0 && a.err) atomicOr(a.err, BPD_FLAG_STATE_RANGE);
+    dead_row = true;
+  }
+  const ConstFlatView C{row_cfg};
+  LaneView A{lane_sets + lane};
+  LaneView Bv{lane_sets + kLaneWords * kWave + lane};
+
+  if (!dead_row) {
+    for (int q = 0; q < 4; ++q) {
+      A.reset();
+      const bool ok = advance_byte(a.g, C, A, q * kWave + lane);
+      const uint64_t m = __ballot(ok);
+      if (lane == 0) {
+        first_ok[2 * q] = uint32_t(m);
+        first_ok[2 * q + 1] = uint32_t(m >> 32);
+      }
+    }
+  }
+  __syncthreads();
+  const bool complete = !dead_row && is_complete(a.g, C);
+  const bool nonempty = !dead_row && C.n() > 0;
+
+  const int64_t t_begin = int64_t(blockIdx.x) * a.chunk_tokens;
+  const int64_t t_end = t_begin + a.chunk_tokens < a.vocab ? t_begin + a.chunk_tokens : a.vocab;
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kWave) {
+    const int64_t t = t0 + lane;
+    bool allow = false;
+    if (!dead_row && t < t_end) {
+      if (t == a.eos) {
+        allow = complete;
+      } else {
+        const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
+        if (s == e) {
+          allow = nonempty;
+        } else {
+          const int b0 = a.tok_bytes[s];
+          if ((first_ok[b0 >> 5] >> (b0 & 31)) & 1u) {
+            LaneView cur = A, nxt = Bv;
+            cur.reset();
+            allow = advance_byte(a.g, C, cur, b0);
+            for (int32_t i = s + 1; i < e && allow; ++i) {
+              nxt.reset();
+              allow = advance_byte(a.g, cur, nxt, a.tok_bytes[i]);
+              const LaneView tmp = cur;
+              cur = nxt;
+              nxt = tmp;
+            }
+          }
+        }
+      }
+    }
+    if (a.logits) {
+      if (t < t_end && !allow) {
+        uint8_t* p = a.logits + b * a.ld_bytes + t * a.elem;
+        if (a.elem == 2)
+          *reinterpret_cast<uint16_t*>(p) = uint16_t(a.fill);
+        else
+          *reinterpret_cast<uint32_t*>(p) = a.fill;
+      }
+    } else {
+      const uint64_t m = __ballot(allow);
+      if (lane == 0) {
+        const int64_t w0 = t0 >> 5;
+        if (w0 < a.words) a.bits[b * a.words + w0] = uint32_t(m);
+        if (w0 + 1 < a.words) a.bits[b * a.words + w0 + 1] = uint32_t(m >> 32);
+      }
+    }
+  }
+}
+
+struct AdvanceArgs {
+  PdaTableView g;
+  const int32_t* tok_off;
+  const uint8_t* tok_bytes;
+  int32_t vocab;
+  int32_t eos;
+  int32_t* configs;
+  const int64_t* slots;
+  const void* tokens;
+  int tok_dtype;
+  int64_t rows;
+  uint8_t* ok;
+  uint8_t* broken;
+  int32_t* status;
+  int32_t* err;
+};
+
+__device__ bool flat_config_ok(const int32_t* c, int32_t num_states) {
+  const int n = c[0];
+  if (n < 0 || n > kMaxConfigs) return false;
+  for (int i = 0; i < n; ++i) {
+    const int d = c[2 + i];
+    if (d < 0 || d > kMaxDepth) return false;
+    for (int k = 0; k < d; ++k) {
+      const int v = c[2 + kMaxConfigs + i * kMaxDepth + k];
+      if (v < 0 || v >= num_states) return false;
+    }
+  }
+  return true;
+}
+
+__global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a) {
+  __shared__ int32_t bufs[kCommitRows][2][kConfigWords];
+  const int64_t b = int64_t(blockIdx.x) * kCommitRows + threadIdx.x;
+  if (b >= a.rows) return;
+  const int64_t row = a.slots ? a.slots[b] : b;
+  int32_t* cfg = a.configs + row * kConfigWords;
+  const int64_t t = a.tok_dtype == BPD_INDEX_I64
+                        ? int64_t(int32_t(static_cast<const int64_t*>(a.tokens)[b]))
+                        : int64_t(static_cast<const int32_t*>(a.tokens)[b]);
+  bool ok;
+  if (t < 0 || t >= a.vocab) {
+    if (a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
+    ok = false;
+  } else if (!flat_config_ok(cfg, a.g.num_states)) {
+    if (a.err) atomicOr(a.err, BPD_FLAG_STATE_RANGE);
+    ok = false;
+  } else if (t == a.eos) {
+    ok = is_complete(a.g, ConstFlatView{cfg});
+  } else {
+    const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
+    ok = true;
+    if (s < e) {
+      FlatView x{bufs[threadIdx.x][0]}, y{bufs[threadIdx.x][1]};
+      x.reset_all();
+      ok = advance_byte(a.g, ConstFlatView{cfg}, x, a.tok_bytes[s]);
+      for (int32_t i = s + 1; i < e && ok; ++i) {
+        y.reset_all();
+        ok = advance_byte(a.g, x, y, a.tok_bytes[i]);
+        const FlatView tmp = x;
+        x = y;
+        y = tmp;
+      }
+      if (ok)
+        for (int k = 0; k < kConfigWords; ++k) cfg[k] = x.w[k];
+    }
+  }
+  if (a.ok) a.ok[b] = ok ? 1 : 0;
+  if (a.broken) {
+    if (!ok) a.broken[row] = 1;
+    if (a.status) a.status[b] = a.broken[row] ? -1 : 1;
+  } else if (a.status) {
+    a.status[b] = ok ? 1 : -1;
+  }
+}
+
+int check_tables(const BpdPdaTable* g, const BpdTokenBytes* toks) {
+  BPD_REQUIRE(g && toks, "null table argument");
+  BPD_REQUIRE(g->num_states > 0, "empty PDA table");
+  BPD_REQUIRE(g->num_states <= 65536, "PDA tables above 65536 states are not supported");
+  BPD_REQUIRE(g->root_start >= 0 && g->root_start < g->num_states, "root_start out of range");
+  BPD_REQUIRE(toks->vocab_size >= 0, "negative vocab size");
+  return BPD_OK;
+}
+
+// ---------------------------------------------------------------- host --
+bool host_try_token(const PdaTableView& g, const BpdTokenBytes& tk, const int32_t* cfg,
+                    int32_t t, int32_t* x, int32_t* y) {
+  if (t == tk.eos_id) return is_complete(g, ConstFlatView{cfg});
+  const int32_t s = tk.offsets[t], e = tk.offsets[t + 1];
+  if (s == e) return cfg[0] > 0;
+  FlatView cur{x}, nxt{y};
+  cur.reset_all();
+  if (!advance_byte(g, ConstFlatView{cfg}, cur, tk.bytes[s])) return false;
+  for (int32_t i = s + 1; i < e; ++i) {
+    nxt.reset_all();
+    if (!advance_byte(g, cur, nxt, tk.bytes[i])) return false;
+    const FlatView tmp = cur;
+    cur = nxt;
+    nxt = tmp;
+  }
+  return cur.n() > 0;
+}
+
+bool host_config_ok(const int32_t* c, int32_t num_states) {
+  const int n = c[0];
+  if (n < 0 || n > kMaxConfigs) return false;
+  for (int i = 0; i < n; ++i) {
+    const int d = c[2 + i];
+    if (d < 0 || d > kMaxDepth) return false;
+    for (int k = 0; k < d; ++k) {
+      const int v = c[2 + kMaxConfigs + i * kMaxDepth + k];
+      if (v < 0 || v >= num_states) return false;
+    }
+  }
+  return true;
+}
+
+}  // namespace
+}  // namespace bpd
+
+using namespace bpd;
+
+extern "C" size_t bpd_pda_workspace_bytes(int64_t rows, int32_t vocab) {
+  (void)rows;
+  (void)vocab;
+  return 0;
+}
+
+extern "C" int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out) {
+  BPD_REQUIRE(g && config_out, "null argument");
+  BPD_REQUIRE(g->num_states > 0, "empty PDA table");
+  BPD_REQUIRE(g->root_start >= 0 && g->root_start < g->num_states, "root_start out of range");
+  init_config(table_view(*g), FlatView{config_out});
+  return BPD_OK;
+}
+
+static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, const int32_t* configs,
+                           const int64_t* slots, const uint8_t* broken, int64_t rows,
+                           void* logits, int dtype, int64_t ld, double neg_inf, uint32_t* bits,
+                           void* stream) {
+  if (int rc = check_tables(g, toks)) return rc;
+  BPD_REQUIRE(rows >= 0 && rows < 65536, "rows must lie in [0, 65535]");
+  MaskArgs a{};
+  a.g = table_view(*g);
+  a.tok_off = toks->offsets;
+  a.tok_bytes = toks->bytes;
+  a.vocab = toks->vocab_size;
+  a.eos = toks->eos_id;
+  a.configs = configs;
+  a.slots = slots;
+  a.broken = broken;
+  a.rows = rows;
+  if (logits) {
+    a.elem = elem_bytes(dtype);
+    BPD_REQUIRE(a.elem != 0, "unknown logits dtype code %d", dtype);
+    BPD_REQUIRE(ld >= toks->vocab_size, "ld smaller than vocab");
+    uint32_t fill = 0;
+    if (int rc = fill_bits(dtype, neg_inf, &fill)) return rc;
+    a.fill = fill;
+    a.logits = static_cast<uint8_t*>(logits);
+    a.ld_bytes = ld * a.elem;
+  } else {
+    a.bits = bits;
+    a.words = (int64_t(toks->vocab_size) + 31) / 32;
+  }
+  if (rows == 0 || toks->vocab_size == 0) return BPD_OK;
+  // ~16 waves per row keeps >= 4096 waves in flight at serving batch sizes
+  const int64_t per_wave_min = 1024;
+  int64_t chunks = (int64_t(toks->vocab_size) + per_wave_min - 1) / per_wave_min;
+  if (chunks > 16) chunks = 16;
+  int64_t per = (int64_t(toks->vocab_size) + chunks - 1) / chunks;
+  per = (per + kWave - 1) / kWave * kWave;
+  chunks = (int64_t(toks->vocab_size) + per - 1) / per;
+  a.chunk_tokens = int32_t(per);
+  a.err = nullptr;
+  pda_mask_kernel<<<dim3(unsigned(chunks), unsigned(rows)), dim3(kWave), 0, as_stream(stream)>>>(a);
+  BPD_LAUNCHED();
+  return BPD_OK;
+}
+
+extern "C" int bpd_pda_apply_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                                  const int32_t* configs, const int64_t* slots,
+                                  const uint8_t* broken, int64_t rows, void* logits, int dtype,
+                                  int64_t ld, double neg_inf, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  BPD_REQUIRE(logits || rows == 0, "null logits");
+  return launch_pda_mask(g, toks, configs, slots, broken, rows, logits, dtype, ld, neg_inf,
+                         nullptr, stream);
+}
+
+extern "C" int bpd_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                                    const int32_t* configs, const int64_t* slots, int64_t rows,
+                                    uint32_t* bits, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  BPD_REQUIRE(bits || rows == 0, "null bits");
+  return launch_pda_mask(g, toks, configs, slots, nullptr, rows, nullptr, 0, 0, 0.0, bits,
+                         stream);
+}
+
+extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,
+                               const int64_t* slots, const void* tokens, int token_dtype,
+                               int64_t rows, uint8_t* ok, uint8_t* broken, int32_t* status,
+                               int32_t* err, void* stream) {
+  if (int rc = check_tables(g, toks)) return rc;
+  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64,
+              "unknown token dtype code %d", token_dtype);
+  BPD_REQUIRE(rows >= 0, "negative row count");
+  if (rows == 0) return BPD_OK;
+  AdvanceArgs a{};
+  a.g = table_view(*g);
+  a.tok_off = toks->offsets;
+  a.tok_bytes = toks->bytes;
+  a.vocab = toks->vocab_size;
+  a.eos = toks->eos_id;
+  a.configs = configs;
+  a.slots = slots;
+  a.tokens = tokens;
+  a.tok_dtype = token_dtype;
+  a.rows = rows;
+  a.ok = ok;
+  a.broken = broken;
+  a.status = status;
+  a.err = err;
+  const unsigned blocks = unsigned((rows + kCommitRows - 1) / kCommitRows);
+  pda_advance_kernel<<<blocks, kCommitRows, 0, as_stream(stream)>>>(a);
+  BPD_LAUNCHED();
+  return BPD_OK;
+}
+
+static int host_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, const int32_t* configs,
+                         const int64_t* slots, const uint8_t* broken, int64_t rows, void* logits,
+                         int dtype, int64_t ld, double neg_inf, uint32_t* bits) {
+  if (int rc = check_tables(g, toks)) return rc;
+  const PdaTableView gv = table_view(*g);
+  const int E = logits ? elem_bytes(dtype) : 0;
+  uint32_t fill = 0;
+  if (logits) {
+    BPD_REQUIRE(E != 0, "unknown logits dtype code %d", dtype);
+    if (int rc = fill_bits(dtype, neg_inf, &fill)) return rc;
+  }
+  const int64_t words = (int64_t(toks->vocab_size) + 31) / 32;
+  std::vector<int32_t> x(kConfigWords), y(kConfigWords);
+  for (int64_t b = 0; b < rows; ++b) {
+    const int64_t row = slots ? slots[b] : b;
+    const int32_t* cfg = configs + row * kConfigWords;
+    BPD_REQUIRE(host_config_ok(cfg, g->num_states), "config-set of row %lld is malformed",
+                (long long)b);
+    const bool dead = broken && broken[row];
+    if (bits) std::fill(bits + b * words, bits + (b + 1) * words, 0u);
+    for (int32_t t = 0; t < toks->vocab_size; ++t) {
+      const bool allow = !dead && host_try_token(gv, *toks, cfg, t, x.data(), y.data());
+      if (bits) {
+        if (allow) bits[b * words + (t >> 5)] |= 1u << (t & 31);
+      } else if (!allow) {
+        uint8_t* p = static_cast<uint8_t*>(logits) + (b * ld + t) * E;
+        if (E == 2)
+          *reinterpret_cast<uint16_t*>(p) = uint16_t(fill);
+        else
+          *reinterpret_cast<uint32_t*>(p) = fill;
+      }
+    }
+  }
+  return BPD_OK;
+}
+
+extern "C" int bpd_host_pda_apply_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                                       const int32_t* configs, const int64_t* slots,
+                                       const uint8_t* broken, int64_t rows, void* logits,
+                                       int dtype, int64_t ld, double neg_inf) {
+  return host_pda_mask(g, toks, configs, slots, broken, rows, logits, dtype, ld, neg_inf, nullptr);
+}
+
+extern "C" int bpd_host_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                                         const int32_t* configs, const int64_t* slots,
+                                         int64_t rows, uint32_t* bits) {
+  return host_pda_mask(g, toks, configs, slots, nullptr, rows, nullptr, 0, 0, 0.0, bits);
+}
+
+extern "C" int bpd_host_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                                    int32_t* configs, const int64_t* slots, const void* tokens,
+                                    int token_dtype, int64_t rows, uint8_t* ok, uint8_t* broken,
+                                    int32_t* status) {
+  if (int rc = check_tables(g, toks)) return rc;
+  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64,
+              "unknown token dtype code %d", token_dtype);
+  const PdaTableView gv = table_view(*g);
+  auto token_at = [&](int64_t b) -> int64_t {
+    return token_dtype == BPD_INDEX_I64 ? int64_t(int32_t(static_cast<const int64_t*>(tokens)[b]))
+                                        : int64_t(static_cast<const int32_t*>(tokens)[b]);
+  };
+  for (int64_t b = 0; b < rows; ++b) {
+    const int64_t t = token_at(b);
+    BPD_REQUIRE(t >= 0 && t < toks->vocab_size,
+                "index %lld is out of bounds for dimension 0 with size %d", (long long)t,
+                toks->vocab_size);
+    const int64_t row = slots ? slots[b] : b;
+    BPD_REQUIRE(host_config_ok(configs + row * kConfigWords, g->num_states),
+                "config-set of row %lld is malformed", (long long)b);
+  }
+  std::vector<int32_t> x(kConfigWords), y(kConfigWords);
+  for (int64_t b = 0; b < rows; ++b) {
+    const int64_t row = slots ? slots[b] : b;
+    int32_t* cfg = configs + row * kConfigWords;
+    const int32_t t = int32_t(token_at(b));
+    bool accepted;
+    if (t == toks->eos_id) {
+      accepted = is_complete(gv, ConstFlatView{cfg});
+    } else {
+      const int32_t s = toks->offsets[t], e = toks->offsets[t + 1];
+      accepted = true;
+      if (s < e) {
+        FlatView cur{x.data()}, nxt{y.data()};
+        cur.reset_all();
+        accepted = advance_byte(gv, ConstFlatView{cfg}, cur, toks->bytes[s]);
+        for (int32_t i = s + 1; i < e && accepted; ++i) {
+          nxt.reset_all();
+          accepted = advance_byte(gv, cur, nxt, toks->bytes[i]);
+          const FlatView tmp = cur;
+          cur = nxt;
+          nxt = tmp;
+        }
+        if (accepted) std::copy(cur.w, cur.w + kConfigWords, cfg);
+      }
+    }
+    if (ok) ok[b] = accepted ? 1 : 0;
+    if (broken) {
+      if (!accepted) broken[row] = 1;
+      if (status) status[b] = broken[row] ? -1 : 1;
+    } else if (status) {
+      status[b] = accepted ? 1 : -1;
+    }
+  }
+  return BPD_OK;
+}

@@ -1,0 +1,355 @@
+"""Operator layer of the constraint step (ops.py of the reference).
+
+:class:`FsaTensors` is the grammar bundle; the functions below are the
+reference's operator API with the same signatures and results.  Every
+computation runs in ``libbpdecode_hip.so``: device tensors go to its HIP
+kernels on torch's current stream, CPU tensors to its host entry points.
+torch only allocates outputs and supplies the stream.
+
+Dense ``tok_next`` semantics (ops.py:143-197, 262-311):
+
+* ``tok_next[s, t]`` is the state after token ``t`` from ``s`` or ``-1`` (the
+  walk reaches ``dead`` or ends in a non-live state); the EOS column holds
+  ``s`` for an accepting ``s`` and ``-1`` otherwise.
+* ``apply_mask_``: ``logits[b, t] = neg_inf`` iff ``states[b] < 0`` or
+  ``tok_next[states[b], t] == -1``; all other entries keep their bits.
+* ``advance_state``: ``-1`` for a negative state, else ``tok_next[s, t]``
+  (a negative ``t`` indexes from the end, as torch indexing does).
+
+A bundle without ``tok_next`` gets the rows it needs walked on the fly by the
+table-builder kernel, which computes ``step`` entry for entry.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, replace
+
+import torch
+
+from . import _lib
+from ._lib import check, lib, ptr
+from .fsa import FsaTable, TokenSymbols, fsa_from_dfa, token_symbols
+from .regex import compile_regex
+from .regex.compile import DFA
+from .tokenizer import Vocabulary
+
+HAVE_NATIVE = True  # the library is required; loading failures raise at first use
+
+DENSE_AUTO_LIMIT = 32_000_000  # S * V at or below which build() densifies (ops.py:137-139)
+
+
+@dataclass
+class FsaTensors:
+    """FSA + token tables as tensors (field-for-field the reference's bundle)."""
+
+    trans: torch.Tensor  # int32 [num_states * num_symbols]
+    accept: torch.Tensor  # uint8 [num_states]
+    live: torch.Tensor  # uint8 [num_states]
+    num_symbols: int
+    dead: int
+    offsets: torch.Tensor  # int32 [vocab_size + 1]
+    symbols: torch.Tensor  # int32 [offsets[-1]]
+    eos_id: int
+    start: int = 0
+    accepting: frozenset = frozenset()
+    tok_next: torch.Tensor | None = None  # int32 [num_states, vocab]
+    lookahead: torch.Tensor | None = None  # float32 [num_states, vocab]
+
+    @property
+    def device(self) -> torch.device:
+        return self.trans.device
+
+    @property
+    def num_states(self) -> int:
+        return int(self.accept.numel())
+
+    @property
+    def vocab_size(self) -> int:
+        return int(self.offsets.numel() - 1)
+
+    def to(self, device) -> FsaTensors:
+        if self.trans.device == torch.device(device):
+            return self
+        mv = lambda t: None if t is None else t.to(device)  # noqa: E731
+        return FsaTensors(
+            mv(self.trans), mv(self.accept), mv(self.live), self.num_symbols, self.dead,
+            mv(self.offsets), mv(self.symbols), self.eos_id, self.start, self.accepting,
+            mv(self.tok_next), mv(self.lookahead),
+        )
+
+    def densify(self) -> FsaTensors:
+        if self.tok_next is not None:
+            return self
+        return replace(self, tok_next=build_token_transitions(self))
+
+    def with_lookahead(self, k: int = 3) -> FsaTensors:
+        base = self.densify()
+        return replace(base, lookahead=build_lookahead(base, k))
+
+    @classmethod
+    def from_tables(cls, fsa: FsaTable, toks: TokenSymbols) -> FsaTensors:
+        return cls(
+            trans=torch.tensor(fsa.trans, dtype=torch.int32),
+            accept=torch.tensor(fsa.accept, dtype=torch.uint8),
+            live=torch.tensor(fsa.live, dtype=torch.uint8),
+            num_symbols=fsa.num_symbols,
+            dead=fsa.dead,
+            offsets=torch.tensor(toks.offsets, dtype=torch.int32),
+            symbols=torch.frombuffer(bytearray(toks.symbols or b"\x00"), dtype=torch.uint8)[
+                : len(toks.symbols)
+            ].to(torch.int32),
+            eos_id=toks.eos_id,
+            start=fsa.start,
+            accepting=frozenset(i for i, a in enumerate(fsa.accept) if a),
+        )
+
+    @classmethod
+    def build(cls, pattern: str | DFA, vocab: Vocabulary, *, dense: bool | str = "auto") -> FsaTensors:
+        dfa = pattern if isinstance(pattern, DFA) else compile_regex(pattern)
+        fsa = cls.from_tables(fsa_from_dfa(dfa), token_symbols(dfa, vocab))
+        want = dense is True or (dense == "auto" and fsa.num_states * fsa.vocab_size <= DENSE_AUTO_LIMIT)
+        return fsa.densify() if want else fsa
+
+
+# --------------------------------------------------------------- helpers --
+def _same_device(*ts: torch.Tensor | None) -> torch.device:
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) != 1:
+        raise RuntimeError(f"all tensors of one call must be on the same device, got {sorted(map(str, devs))}")
+    return devs.pop()
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    t = t if t.dtype == torch.int32 else t.to(torch.int32)
+    return t.contiguous()
+
+
+def _unit_stride_rows(logits: torch.Tensor) -> tuple[torch.Tensor, bool]:
+    """A view with unit column stride (a copy when needed, flagged)."""
+    if logits.dim() != 2:
+        raise RuntimeError("logits must be [batch, vocab]")
+    if logits.stride(1) == 1 and logits.stride(0) >= max(logits.size(1), 1):
+        return logits, False
+    return logits.contiguous(), True
+
+
+def _symbols_u8(fsa: FsaTensors) -> torch.Tensor:
+    sym = fsa.symbols
+    if sym.numel() and (int(sym.min()) < 0 or int(sym.max()) > 255):
+        raise RuntimeError("symbol-class ids must lie in [0, 255]")
+    return sym.to(torch.uint8).contiguous() if sym.numel() else torch.zeros(1, dtype=torch.uint8, device=sym.device)
+
+
+def build_token_transitions(fsa: FsaTensors, rows=None) -> torch.Tensor:
+    """Dense ``[num_states, vocab]`` int32 next-state table (``[len(rows), vocab]``
+    for the given start states), built by the table-builder kernel / host
+    routine (ops.py:143-197)."""
+    S, M, V = fsa.num_states, fsa.num_symbols, fsa.vocab_size
+    dev = fsa.device
+    row_states = None
+    n = S
+    if rows is not None:
+        row_states = torch.as_tensor(rows, dtype=torch.int32, device=dev).contiguous()
+        n = int(row_states.numel())
+        if dev.type != "cuda" and n and (int(row_states.min()) < 0 or int(row_states.max()) >= S):
+            raise IndexError(f"row state out of range [0, {S})")
+    out = torch.empty((n, V), dtype=torch.int32, device=dev)
+    if n == 0 or V == 0:
+        return out
+    trans = _i32(fsa.trans)
+    acc = fsa.accept.contiguous()
+    live = fsa.live.contiguous()
+    offs = _i32(fsa.offsets)
+    sym = _symbols_u8(fsa)
+    eos = fsa.eos_id if fsa.eos_id is not None else -1
+    args = (ptr(trans), S, M, fsa.dead, ptr(acc), ptr(live), ptr(offs), ptr(sym), V, eos,
+            ptr(row_states), n, ptr(out))
+    if dev.type == "cuda":
+        check(lib().bpd_build_tok_next(*args, _lib.stream_of(dev)))
+    else:
+        check(lib().bpd_host_build_tok_next(*args))
+    return out
+
+
+def build_lookahead(fsa: FsaTensors, k: int) -> torch.Tensor:
+    """Uniform-count soft-lookahead table ``[num_states, vocab]`` float32
+    (ops.py:200-236): ``out[s, t] = logZ_{k-1}(tok_next[s, t])`` with the
+    backward recurrence ``logZ_{j+1}(s) = logsumexp_t logZ_j(tok_next[s, t])``
+    (``⊕ 0`` for accepting ``s``, ``-inf`` off the live set), ``-inf`` on
+    rejected tokens and 0 / ``-inf`` in the EOS column."""
+    if fsa.tok_next is None:
+        fsa = fsa.densify()
+    tn = fsa.tok_next.contiguous()
+    S, V = tn.shape
+    dev = tn.device
+    out = torch.empty((S, V), dtype=torch.float32, device=dev)
+    eos = fsa.eos_id if fsa.eos_id is not None and 0 <= fsa.eos_id < V else -1
+    acc, live = fsa.accept.contiguous(), fsa.live.contiguous()
+    if dev.type == "cuda":
+        ws_bytes = int(lib().bpd_soft_workspace_bytes(0, S, 0))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        check(lib().bpd_soft_build_lookahead(ptr(tn), S, V, ptr(acc), ptr(live), eos, int(k),
+                                             ptr(out), ptr(ws), ws_bytes, _lib.stream_of(dev)))
+    else:
+        check(lib().bpd_host_soft_build_lookahead(ptr(tn), S, V, ptr(acc), ptr(live), eos, int(k),
+                                                  ptr(out)))
+    return out
+
+
+# ------------------------------------------------- dense kernels (+slots) --
+def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err=None):
+    """``logits`` masked in place against ``tok_next`` rows; the state of row
+    b is ``states[slots[b]]`` when ``slots`` is given (int64), else
+    ``states[b]``."""
+    dev = _same_device(logits, tok_next, states, slots)
+    work, copied = _unit_stride_rows(logits)
+    B, V = work.shape
+    S, TV = tok_next.shape
+    if TV != V:
+        raise RuntimeError(f"logits have {V} columns but tok_next has {TV}")
+    nb = B if slots is None else slots.numel()
+    if nb != B:
+        raise RuntimeError("one slot per logits row")
+    st = _i32(states)
+    if slots is None and st.numel() != B:
+        raise RuntimeError(f"one state per logits row (got {st.numel()} states for {B} rows)")
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    tn = tok_next if tok_next.dtype == torch.int32 and tok_next.is_contiguous() else _i32(tok_next)
+    code = _lib.dtype_code(work.dtype)
+    ld = work.stride(0) if B > 1 else V
+    if dev.type == "cuda":
+        check(lib().bpd_dense_apply_mask(ptr(work), code, B, V, ld, ptr(tn), S, ptr(st), ptr(sl),
+                                         float(neg_inf), ptr(err), _lib.stream_of(dev)))
+    else:
+        check(lib().bpd_host_dense_apply_mask(ptr(work), code, B, V, ld, ptr(tn), S, ptr(st),
+                                              ptr(sl), float(neg_inf)))
+    if copied:
+        logits.copy_(work)
+    return logits
+
+
+def dense_advance(tok_next, states, tokens, slots=None, write_back=False, err=None):
+    """Next state per row; with ``write_back`` the pool ``states`` is updated
+    at the rows' slots as well.  Host-side token ids for a device table are
+    range-checked on the host (raising as torch indexing does) and copied
+    over; device-side ids out of range yield ``-1`` and set
+    ``BPD_FLAG_TOKEN_RANGE`` in ``err``."""
+    S, V = tok_next.shape
+    tk = tokens.contiguous()
+    if tk.dtype not in (torch.int32, torch.int64):
+        tk = tk.to(torch.int64)
+    if tk.device != tok_next.device and tk.device.type == "cpu":
+        if tk.numel():
+            lo, hi = int(tk.to(torch.int32).min()), int(tk.to(torch.int32).max())
+            bad = hi if hi >= V else (lo if lo < -V else None)
+            if bad is not None:
+                raise IndexError(f"index {bad} is out of bounds for dimension 1 with size {V}")
+        tk = tk.to(tok_next.device, non_blocking=True)
+    dev = _same_device(tok_next, states, tk, slots)
+    B = tk.numel()
+    if slots is None and states.numel() != B:
+        raise RuntimeError("one token id per state")
+    if slots is not None and slots.numel() != B:
+        raise RuntimeError("one token id per slot")
+    if write_back and (states.dtype != torch.int32 or not states.is_contiguous()):
+        raise RuntimeError("write_back needs a contiguous int32 state pool")
+    st = states if write_back else _i32(states)
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    tn = tok_next if tok_next.dtype == torch.int32 and tok_next.is_contiguous() else _i32(tok_next)
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    code = _lib.index_code(tk.dtype)
+    if dev.type == "cuda":
+        check(lib().bpd_dense_advance(ptr(tn), S, V, ptr(st), ptr(sl), ptr(tk), code, B, ptr(out),
+                                      int(write_back), ptr(err), _lib.stream_of(dev)))
+    else:
+        check(lib().bpd_host_dense_advance(ptr(tn), S, V, ptr(st), ptr(sl), ptr(tk), code, B,
+                                           ptr(out), int(write_back)))
+    return out.view(tokens.shape) if tokens.dim() else out.reshape(())
+
+
+def dense_compute_mask(tok_next, states, slots=None, err=None):
+    dev = _same_device(tok_next, states, slots)
+    S, V = tok_next.shape
+    st = _i32(states)
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    B = st.numel() if sl is None else sl.numel()
+    out = torch.empty((B, (V + 31) // 32), dtype=torch.int32, device=dev)
+    tn = _i32(tok_next)
+    if dev.type == "cuda":
+        check(lib().bpd_dense_compute_mask(ptr(tn), S, V, ptr(st), ptr(sl), B, ptr(out), ptr(err),
+                                           _lib.stream_of(dev)))
+    else:
+        check(lib().bpd_host_dense_compute_mask(ptr(tn), S, V, ptr(st), ptr(sl), B, ptr(out)))
+    return out
+
+
+def _walked_rows(fsa: FsaTensors, states: torch.Tensor):
+    """For a bundle without ``tok_next``: each row's table row, walked now,
+    plus the per-row state index into it (negative states kept)."""
+    st = _i32(states).view(-1)
+    if st.numel() and int(st.max()) >= fsa.num_states:
+        raise IndexError(f"index {int(st.max())} is out of bounds for dimension 0 with size {fsa.num_states}")
+    rows = build_token_transitions(fsa, rows=st.clamp(min=0))
+    idx = torch.where(st < 0, st, torch.arange(st.numel(), dtype=torch.int32, device=st.device))
+    return rows, idx
+
+
+# ------------------------------------------------------------- public API --
+def apply_soft_(logits: torch.Tensor, fsa: FsaTensors, states: torch.Tensor, alpha: float = 1.0):
+    """In place: ``logits += alpha * lookahead[states]`` on the finite part,
+    ``-inf`` where the lookahead is ``-inf`` or the state is negative
+    (ops.py:239-259)."""
+    if fsa.lookahead is None:
+        raise ValueError("fsa has no lookahead table; build with dense + with_lookahead")
+    return soft_apply_(logits, fsa.lookahead, states, alpha=alpha)
+
+
+def soft_apply_(logits, lookahead, states, slots=None, alpha: float = 1.0):
+    dev = _same_device(logits, lookahead, states, slots)
+    work, copied = _unit_stride_rows(logits)
+    B, V = work.shape
+    S, LV = lookahead.shape
+    if LV != V:
+        raise RuntimeError(f"logits have {V} columns but the lookahead table has {LV}")
+    st = _i32(states)
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    la = lookahead.contiguous()
+    code = _lib.dtype_code(work.dtype)
+    ld = work.stride(0) if B > 1 else V
+    if dev.type == "cuda":
+        check(lib().bpd_soft_apply(ptr(work), code, B, V, ld, ptr(la), S, ptr(st), ptr(sl),
+                                   float(alpha), None, _lib.stream_of(dev)))
+    else:
+        check(lib().bpd_host_soft_apply(ptr(work), code, B, V, ld, ptr(la), S, ptr(st), ptr(sl),
+                                        float(alpha)))
+    if copied:
+        logits.copy_(work)
+    return logits
+
+
+def apply_mask_(logits: torch.Tensor, fsa: FsaTensors, states: torch.Tensor,
+                neg_inf: float = float("-inf")) -> torch.Tensor:
+    """In place: every disallowed logit of ``logits`` [batch, vocab] becomes
+    ``neg_inf``, one grammar state per row (ops.py:262-281)."""
+    if fsa.tok_next is not None:
+        return dense_mask_(logits, fsa.tok_next, states, neg_inf=neg_inf)
+    rows, idx = _walked_rows(fsa, states)
+    return dense_mask_(logits, rows, idx, neg_inf=neg_inf)
+
+
+def compute_mask(fsa: FsaTensors, states: torch.Tensor) -> torch.Tensor:
+    """Packed allow-mask, uint32 bits in an int32 tensor [batch, ceil(vocab/32)],
+    LSB-first (ops.py:284-292)."""
+    if fsa.tok_next is not None:
+        return dense_compute_mask(fsa.tok_next, states)
+    rows, idx = _walked_rows(fsa, states)
+    return dense_compute_mask(rows, idx)
+
+
+def advance_state(fsa: FsaTensors, states: torch.Tensor, token_ids: torch.Tensor) -> torch.Tensor:
+    """Next state per request after ``token_ids``; ``-1`` off a valid path
+    (ops.py:295-311)."""
+    if fsa.tok_next is not None:
+        return dense_advance(fsa.tok_next, states, token_ids)
+    rows, idx = _walked_rows(fsa, states)
+    return dense_advance(rows, idx, token_ids)

@@ -1,0 +1,197 @@
+/*
+ * bpdecode_hip.h -- C ABI of libbpdecode_hip.so, the MI355X (gfx950) library
+ * behind bpdecode_amd's batched constraint step.
+ *
+ * Plain pointers and sizes only.  Every entry point returns BPD_OK (0) or an
+ * error code; bpd_last_error() then describes the failure (thread-local).
+ * Device entry points take device pointers and a hipStream_t (as void*),
+ * enqueue work on that stream and return without synchronising.  Host entry
+ * points (bpd_host_*) take host pointers and run on the calling thread; they
+ * serve the CPU-tensor side of the same operator set.  The library allocates
+ * no device memory: buffers an operation needs beyond its inputs and outputs
+ * are passed in as a workspace whose size the matching *_workspace_bytes
+ * function reports.
+ *
+ * Layouts (identical to the reference's tensor bundles):
+ *   tok_next  int32 [num_states, vocab] row-major; -1 = token rejected.
+ *   states    int32 pool; FREE = -2, BROKEN = -1.  With `slots` non-NULL the
+ *             state of row b is states[slots[b]] (slots int64), otherwise
+ *             states[b].
+ *   logits    [rows, ld] elements of `dtype`, unit column stride.
+ *   configs   int32 [*, BPD_PDA_CONFIG_WORDS] = {num_configs, saturated,
+ *             depth[8], stack[8][32]} (padding-free PdaConfigSet).
+ *   bits      uint32 [rows, ceil(vocab/32)], LSB-first.
+ */
+#ifndef BPDECODE_HIP_H_
+#define BPDECODE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BPD_OK 0
+#define BPD_ERR_INVALID 1     /* bad argument: shape, dtype, range, alignment */
+#define BPD_ERR_HIP 2         /* HIP runtime / launch failure */
+#define BPD_ERR_OVERFLOW 3    /* fill value not representable in the logits dtype */
+#define BPD_ERR_UNSUPPORTED 4 /* table too large for a kernel's encoding */
+
+#define BPD_DTYPE_F32 0
+#define BPD_DTYPE_F16 1
+#define BPD_DTYPE_BF16 2
+
+#define BPD_INDEX_I32 0
+#define BPD_INDEX_I64 1
+
+/* Bits OR-ed into the optional `err` word by kernels (device int32). */
+#define BPD_FLAG_STATE_RANGE 1 /* a state >= num_states was read */
+#define BPD_FLAG_TOKEN_RANGE 2 /* a token outside [-vocab, vocab) was read */
+
+#define BPD_PDA_MAX_CONFIGS 8
+#define BPD_PDA_MAX_DEPTH 32
+#define BPD_PDA_CONFIG_WORDS (2 + BPD_PDA_MAX_CONFIGS + BPD_PDA_MAX_CONFIGS * BPD_PDA_MAX_DEPTH)
+
+#define BPD_PDA_EDGE_EPS 0
+#define BPD_PDA_EDGE_BYTE 1
+#define BPD_PDA_EDGE_CALL 2
+
+const char* bpd_last_error(void);
+int bpd_abi_version(void);
+
+/* ---------------------------------------------------------------- dense --
+ * bpd_dense_apply_mask: logits[b, t] = neg_inf (converted to dtype as ATen's
+ * checked scalar conversion does) iff state(b) < 0 or
+ * tok_next[state(b), t] == -1; other entries are left bit-identical.
+ * Replaces the tok_next branch of ops.apply_mask_ (ops.py:271-276), which
+ * ConstraintBatch.apply_mask (batch.py:176-190) calls after gathering
+ * states = _state[slots]; the gather is fused here via `slots`.
+ */
+int bpd_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                         const int32_t* tok_next, int32_t num_states,
+                         const int32_t* states, const int64_t* slots, double neg_inf,
+                         int32_t* err, void* stream);
+
+/* bpd_dense_advance: nxt = state(b) < 0 ? -1 : tok_next[state(b), t(b)], where
+ * t(b) = (int32)tokens[b] and a negative t indexes from the end as torch
+ * advanced indexing does.  Writes next_out[b] (if non-NULL) and, with
+ * write_back, stores nxt into the pool slot it was read from; all reads
+ * happen before any write-back.  Replaces ops.advance_state's tok_next branch
+ * (ops.py:301-306) plus ConstraintBatch.commit's scatter (batch.py:206-215).
+ */
+int bpd_dense_advance(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                      int32_t* states, const int64_t* slots, const void* tokens,
+                      int token_dtype, int64_t rows, int32_t* next_out, int write_back,
+                      int32_t* err, void* stream);
+
+/* bpd_dense_compute_mask: packed allow bits from tok_next (bit t of row b set
+ * iff state(b) >= 0 and tok_next[state(b), t] != -1).  Dense counterpart of
+ * compute_mask_batch (mask.hpp:55-57, torch_ops.cpp:154-189). */
+int bpd_dense_compute_mask(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                           const int32_t* states, const int64_t* slots, int64_t rows,
+                           uint32_t* bits, int32_t* err, void* stream);
+
+/* bpd_build_tok_next: the dense table of build_token_transitions
+ * (ops.py:143-197) on the device: tok_next[r, t] = walk of token t's symbol
+ * classes from row_states[r] (every state 0..num_states-1 when row_states is
+ * NULL), -1 on reaching `dead` or ending in a non-live state; the EOS column
+ * is s for an accepting s and -1 otherwise. */
+int bpd_build_tok_next(const int32_t* trans, int32_t num_states, int32_t num_symbols,
+                       int32_t dead, const uint8_t* accept, const uint8_t* live,
+                       const int32_t* tok_offsets, const uint8_t* tok_symbols,
+                       int64_t vocab, int32_t eos_id, const int32_t* row_states,
+                       int32_t num_rows, int32_t* out, void* stream);
+
+/* Host (CPU-tensor) forms of the dense entry points. */
+int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                              const int32_t* tok_next, int32_t num_states,
+                              const int32_t* states, const int64_t* slots, double neg_inf);
+int bpd_host_dense_advance(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                           int32_t* states, const int64_t* slots, const void* tokens,
+                           int token_dtype, int64_t rows, int32_t* next_out, int write_back);
+int bpd_host_dense_compute_mask(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                                const int32_t* states, const int64_t* slots, int64_t rows,
+                                uint32_t* bits);
+int bpd_host_build_tok_next(const int32_t* trans, int32_t num_states, int32_t num_symbols,
+                            int32_t dead, const uint8_t* accept, const uint8_t* live,
+                            const int32_t* tok_offsets, const uint8_t* tok_symbols,
+                            int64_t vocab, int32_t eos_id, const int32_t* row_states,
+                            int32_t num_rows, int32_t* out);
+
+/* ------------------------------------------------------------------ PDA --
+ * Flattened grammar (grammar/device.py:79-158, pda.hpp:46-69): every rule's
+ * NFA in one global state space plus a CSR edge list.  The same struct
+ * carries host pointers for bpd_host_* / bpd_pda_init and device pointers for
+ * the device entry points.
+ */
+typedef struct BpdPdaTable {
+  int32_t num_states;
+  int32_t root_start;
+  int32_t root_accept;
+  int32_t num_edges;
+  const uint8_t* accept;       /* [num_states] */
+  const uint8_t* live;         /* [num_states] */
+  const int32_t* edge_offsets; /* [num_states + 1] */
+  const int32_t* edge_kind;    /* [num_edges] BPD_PDA_EDGE_* */
+  const int32_t* edge_lo;      /* [num_edges] */
+  const int32_t* edge_hi;      /* [num_edges] */
+  const int32_t* edge_dst;     /* [num_edges] */
+  const int32_t* edge_callee;  /* [num_edges] */
+} BpdPdaTable;
+
+typedef struct BpdTokenBytes {
+  int32_t vocab_size;
+  int32_t eos_id;
+  const int32_t* offsets; /* [vocab_size + 1] */
+  const uint8_t* bytes;   /* [offsets[vocab_size]] */
+} BpdTokenBytes;
+
+/* bpd_pda_init: the closed initial config-set (pda.hpp:200-207), host only,
+ * as the reference's pda_init op (torch_ops.cpp:307-324). */
+int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out);
+
+/* bpd_pda_apply_mask: logits[b, t] = neg_inf unless token t is accepted from
+ * config-set configs[row(b)] (pda_try_token, pda.hpp:248-258), or for every t
+ * when broken[row(b)] != 0 (broken may be NULL).  row(b) = slots ? slots[b]
+ * : b.  Replaces pda_apply_mask_op (torch_ops.cpp:326-376) and the broken-row
+ * fill of CFGConstraintBatch.apply_mask (device.py:252-266). */
+size_t bpd_pda_workspace_bytes(int64_t rows, int32_t vocab);
+int bpd_pda_apply_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                       const int32_t* configs, const int64_t* slots, const uint8_t* broken,
+                       int64_t rows, void* logits, int dtype, int64_t ld, double neg_inf,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* bpd_pda_compute_mask: packed allow bits (compute_mask_pda_batch,
+ * pda_cpu.cpp:7-21). */
+int bpd_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                         const int32_t* configs, const int64_t* slots, int64_t rows,
+                         uint32_t* bits, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* bpd_pda_advance: advance configs[row(b)] in place by tokens[b]; ok[b] = 0 and
+ * the config-set untouched when the token is rejected; EOS only tests
+ * completeness (advance_state_pda_batch, pda_cpu.cpp:35-54).  With broken
+ * non-NULL, broken[row(b)] |= !ok[b] and status[b] = broken[row(b)] ? -1 : 1
+ * (CFGConstraintBatch.commit, device.py:268-283); without it status[b] =
+ * ok[b] ? 1 : -1.  ok, broken and status may each be NULL. */
+int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,
+                    const int64_t* slots, const void* tokens, int token_dtype, int64_t rows,
+                    uint8_t* ok, uint8_t* broken, int32_t* status, int32_t* err, void* stream);
+
+int bpd_host_pda_apply_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                            const int32_t* configs, const int64_t* slots,
+                            const uint8_t* broken, int64_t rows, void* logits, int dtype,
+                            int64_t ld, double neg_inf);
+int bpd_host_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
+                              const int32_t* configs, const int64_t* slots, int64_t rows,
+                              uint32_t* bits);
+int bpd_host_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,
+                         const int64_t* slots, const void* tokens, int token_dtype,
+                         int64_t rows, uint8_t* ok, uint8_t* broken, int32_t* status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BPDECODE_HIP_H_ */
