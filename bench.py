@@ -1,0 +1,248 @@
+"""Benchmark of the batched constraint step on one MI355X.
+
+Default workload (serving scale, dense tok_next): the email regex
+``[a-z0-9._]{1,32}@[a-z0-9-]{1,24}\\.(com|org|net|io)`` compiled to a byte DFA
+over a seeded synthetic vocabulary of V = 151,936 tokens; B = 256 rows;
+bf16 logits N(0, 3); continuous batching that evicts 10% of the rows and adds
+as many fresh ones every step; tokens sampled from the masked softmax.
+
+One step = ``ConstraintBatch.apply_mask`` + ``ConstraintBatch.commit``.  Each
+step starts from cold caches: a 512 MB scratch buffer is read before it (no
+dirty lines left behind), so logits and tok_next rows come from HBM.  The two
+calls are bracketed by HIP events on the stream they launch on; logits
+generation, the flush, sampling and churn sit outside those brackets.
+
+Roofline (dominant kernel = the dense mask): algorithmic bytes per launch
+``D = B*V*2e + U*V*4`` (read + write of every logit, one int32 tok_next row per
+distinct live state U of that step), divided by the kernel's event-timed
+duration, against the 8 TB/s HBM3E peak.  The commit kernel adds 16 B per row.
+
+CPU baseline: the oracle's numpy restatement of the reference dense path
+timed on the host over a bounded replay of the first recorded steps.
+
+Prints one JSON line.  ``--gpus N`` with N > 1 is refused: this build
+measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=128)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--batch", type=int, default=256)
+    p.add_argument("--vocab", type=int, default=151_936)
+    p.add_argument("--churn", type=float, default=0.10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-steps", type=int, default=8, help="recorded steps replayed on the CPU")
+    p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                   help="instead: run a plain device copy of MB megabytes 20 times (PMC scale check)")
+    return p.parse_args(argv)
+
+
+def calibrate_copy(mb: int) -> None:
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = mb * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(20):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 20}))
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(rows shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return 0
+
+    import numpy as np
+    import torch
+
+    from bpdecode_amd import synth
+    from bpdecode_amd.batch import ConstraintBatch
+    from bpdecode_amd.ops import FsaTensors
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, V = args.batch, args.vocab
+    t0 = time.perf_counter()
+    vocab = synth.serving_vocab(V, seed=1)
+    fsa = FsaTensors.build(synth.EMAIL, vocab, dense=False).to(dev).densify()
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    S = fsa.num_states
+    e = 2  # bf16
+
+    batch = ConstraintBatch(fsa, capacity=2 * B, device=dev)
+    rng = np.random.default_rng(2)
+    next_id = 0
+    active: list[int] = []
+    for _ in range(B):
+        batch.add(next_id)
+        active.append(next_id)
+        next_id += 1
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    logits = torch.empty((B, V), dtype=torch.bfloat16, device=dev)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    flush.zero_()
+    flush64 = flush.view(torch.int64)
+    stream = torch.cuda.current_stream(dev)
+
+    n_total = args.warmup + args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_total)]
+    distinct: list[int] = []
+    host_api_s: list[float] = []
+    recorded = []  # (logits bits, states, tokens, masked bits) of the first timed steps
+    n_cpu = 0 if args.no_cpu else min(args.cpu_steps, args.steps)
+
+    torch.cuda.synchronize()
+    wall0 = None
+    for k in range(n_total):
+        if k == args.warmup:
+            torch.cuda.synchronize()
+            wall0 = time.perf_counter()
+        ids = list(active)
+        logits.copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
+        slots = batch._slots(ids)
+        pool = batch._state  # applies queued slot writes before the timed region
+        states_now = pool[slots].cpu().numpy()
+        live = states_now[states_now >= 0]
+        distinct.append(int(np.unique(live).size))
+        keep = k >= args.warmup and len(recorded) < n_cpu
+        if keep:
+            rec_logits = logits.cpu()
+        if not args.no_flush:
+            flush64.sum()
+        h0 = time.perf_counter()
+        ev[k][0].record(stream)
+        batch.apply_mask(ids, logits)
+        ev[k][1].record(stream)
+        h1 = time.perf_counter()
+        probs = torch.softmax(logits.float(), dim=-1)
+        toks = torch.multinomial(probs, 1, generator=gen).view(-1)
+        h2 = time.perf_counter()
+        ev[k][2].record(stream)
+        batch.commit(ids, toks)
+        ev[k][3].record(stream)
+        h3 = time.perf_counter()
+        host_api_s.append((h1 - h0) + (h3 - h2))
+        if keep:
+            recorded.append((rec_logits, states_now.copy(), toks.cpu().numpy(), logits.cpu()))
+        # continuous batching: evict 10% of the rows, add as many fresh ones
+        n_churn = int(round(args.churn * B))
+        for i in rng.choice(len(active), size=n_churn, replace=False).tolist():
+            batch.evict(active[i])
+            active[i] = next_id
+            batch.add(next_id)
+            next_id += 1
+    torch.cuda.synchronize()
+    wall1 = time.perf_counter()
+
+    mask_ms = [ev[k][0].elapsed_time(ev[k][1]) for k in range(args.warmup, n_total)]
+    commit_ms = [ev[k][2].elapsed_time(ev[k][3]) for k in range(args.warmup, n_total)]
+    step_ms = [a + b for a, b in zip(mask_ms, commit_ms)]
+    U = distinct[args.warmup:]
+    d_bytes = [B * V * 2 * e + u * V * 4 for u in U]
+    achieved_gbs = sum(d_bytes) / (sum(mask_ms) * 1e-3) / 1e9
+    mean_step_ms = statistics.fmean(step_ms)
+
+    out = {
+        "metric": "µs/step apply_mask+commit & GB/s (% HBM roofline), B=256 V=151936 bf16",
+        "value": round(mean_step_ms * 1e3, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_step_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "dense tok_next apply_mask+commit, email-regex DFA, continuous batching 10% churn",
+            "batch_rows": B,
+            "vocab": V,
+            "dfa_states": S,
+            "logits": "bf16 N(0,3)",
+            "cache_flush": "512 MB read before each step" if not args.no_flush else "none",
+        },
+        "median_us_per_step": round(statistics.median(step_ms) * 1e3, 3),
+        "mask_us": round(statistics.fmean(mask_ms) * 1e3, 3),
+        "commit_us": round(statistics.fmean(commit_ms) * 1e3, 3),
+        "row_vocab_entries_per_s": round(B * V / (mean_step_ms * 1e-3), 1),
+        "distinct_live_states_mean": round(statistics.fmean(U), 2),
+        "api_host_us_per_step": round(statistics.fmean(host_api_s[args.warmup:]) * 1e6, 2),
+        "wall_ms_per_step_incl_setup_work": round((wall1 - wall0) * 1e3 / args.steps, 4),
+        "setup_s": round(setup_s, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": "dense_mask_vec_kernel<2>",
+            "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1),
+        },
+    }
+
+    if n_cpu:
+        from oracle import dense as OD
+
+        tn_host = fsa.tok_next.cpu().numpy()
+        fill = OD.fill_bits(torch.bfloat16, float("-inf"))
+        parity = True
+        times = []
+        for _ in range(args.cpu_repeats):
+            for lg, st, tk, masked in recorded:
+                bits = lg.view(torch.int16).numpy().view(np.uint16).copy()
+                c0 = time.perf_counter()
+                OD.apply_mask_bits(bits, tn_host, st, fill)
+                nxt = OD.advance(tn_host, st, tk)
+                times.append(time.perf_counter() - c0)
+                parity &= bool(np.array_equal(bits, masked.view(torch.int16).numpy().view(np.uint16)))
+                del nxt
+        out["cpu_baseline"] = {
+            "value": round(statistics.fmean(times) * 1e6, 1),
+            "unit": "us/step",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{len(recorded)} recorded steps of the same workload (B={B}, V={V}, bf16), "
+                      f"replayed {args.cpu_repeats}x through oracle/dense.py (numpy, one thread)",
+            "host_cpus": os.cpu_count(),
+        }
+        out["parity_vs_oracle"] = parity
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -267,8 +267,10 @@ __global__ __launch_bounds__(256) void build_tok_next_kernel(
   const int32_t r = blockIdx.y;
   if (t >= vocab || r >= num_rows) return;
   const int32_t s0 = row_states ? row_states[r] : r;
-  int32_t res;
-  if (t == eos_id) {
+  int32_t res = -1;
+  if (s0 < 0 || s0 >= num_states) {
+    res = -1;
+  } else if (t == eos_id) {
     res = accept[s0] ? s0 : -1;
   } else {
     int32_t cur = s0;
@@ -281,6 +283,10 @@ __global__ __launch_bounds__(256) void build_tok_next_kernel(
         break;
       }
       cur = trans[int64_t(cur) * num_symbols + k];
+      if (cur < 0 || cur >= num_states) {
+        ok = false;
+        break;
+      }
     }
     res = (ok && live[cur]) ? cur : -1;
   }

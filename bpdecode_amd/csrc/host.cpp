@@ -153,6 +153,10 @@ extern "C" int bpd_host_build_tok_next(const int32_t* trans, int32_t num_states,
           break;
         }
         cur = trans[int64_t(cur) * num_symbols + k];
+        if (cur < 0 || cur >= num_states) {
+          ok = false;
+          break;
+        }
       }
       o[t] = (ok && live[cur]) ? cur : -1;
     }

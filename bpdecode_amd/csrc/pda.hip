@@ -279,6 +279,26 @@ extern "C" size_t bpd_pda_workspace_bytes(int64_t rows, int32_t vocab) {
   return 0;
 }
 
+extern "C" int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data,
+                            int64_t n) {
+  BPD_REQUIRE(g && config, "null argument");
+  BPD_REQUIRE(g->num_states > 0, "empty PDA table");
+  BPD_REQUIRE(host_config_ok(config, g->num_states), "config-set is malformed");
+  const PdaTableView gv = table_view(*g);
+  std::vector<int32_t> x(kConfigWords), y(kConfigWords);
+  FlatView cur{x.data()}, nxt{y.data()};
+  std::copy(config, config + kConfigWords, x.data());
+  for (int64_t i = 0; i < n; ++i) {
+    nxt.reset_all();
+    if (!advance_byte(gv, cur, nxt, data[i])) return 0;
+    const FlatView tmp = cur;
+    cur = nxt;
+    nxt = tmp;
+  }
+  std::copy(cur.w, cur.w + kConfigWords, config);
+  return 1;
+}
+
 extern "C" int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out) {
   BPD_REQUIRE(g && config_out, "null argument");
   BPD_REQUIRE(g->num_states > 0, "empty PDA table");

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kSoftThreads) void soft_round_kernel(
   Lse acc{-INFINITY, 0.0f};
   for (int64_t t = threadIdx.x; t < V; t += kSoftThreads) {
     const int32_t d = row[t];
-    if (d >= 0) acc = lse_push(acc, lz[d]);
+    if (d >= 0 && d < S) acc = lse_push(acc, lz[d]);
   }
   red_m[threadIdx.x] = acc.m;
   red_s[threadIdx.x] = acc.s;
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void soft_table_kernel(const int32_t* __restri
     v = accept[s] ? 0.0f : -INFINITY;
   } else {
     const int32_t d = tok_next[int64_t(s) * V + t];
-    v = d >= 0 ? lz[d] : -INFINITY;
+    v = (d >= 0 && d < S) ? lz[d] : -INFINITY;
   }
   out[int64_t(s) * V + t] = v;
 }

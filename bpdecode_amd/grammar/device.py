@@ -130,6 +130,17 @@ class PdaTensors:
             self._c["init"] = out
         return out.clone()
 
+    def feed(self, config: torch.Tensor, data: bytes) -> bool:
+        """Consume raw bytes into one host config-set in place; False (config
+        untouched) when a byte empties it."""
+        if config.device.type != "cpu" or config.dtype != torch.int32 or not config.is_contiguous():
+            raise RuntimeError("feed works on a contiguous int32 CPU config-set")
+        host = self if self.device.type == "cpu" else self.to("cpu")
+        rc = lib().bpd_pda_feed(host.c_table(), ptr(config), bytes(data), len(data))
+        if rc < 0:
+            check(-rc)
+        return rc == 1
+
     def init_batch(self, batch: int) -> torch.Tensor:
         return self.init_config().unsqueeze(0).expand(batch, -1).contiguous()
 

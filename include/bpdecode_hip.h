@@ -151,6 +151,14 @@ typedef struct BpdTokenBytes {
  * as the reference's pda_init op (torch_ops.cpp:307-324). */
 int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out);
 
+/* bpd_pda_feed: host only; consume `n` raw bytes into one config-set in place
+ * (pda_advance_byte per byte, pda.hpp:211-236).  Returns 1 when every byte
+ * kept the set non-empty (config updated), 0 when a byte emptied it (config
+ * untouched), or a negative error code.  Seeds a row with a known prefix; no
+ * single reference entry point corresponds (the reference's tests feed bytes
+ * through pda_advance_byte directly, test_pda.cpp:46-51). */
+int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data, int64_t n);
+
 /* bpd_pda_apply_mask: logits[b, t] = neg_inf unless token t is accepted from
  * config-set configs[row(b)] (pda_try_token, pda.hpp:248-258), or for every t
  * when broken[row(b)] != 0 (broken may be NULL).  row(b) = slots ? slots[b]
@@ -189,6 +197,34 @@ int bpd_host_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
 int bpd_host_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,
                          const int64_t* slots, const void* tokens, int token_dtype,
                          int64_t rows, uint8_t* ok, uint8_t* broken, int32_t* status);
+
+/* ----------------------------------------------------------------- soft --
+ * bpd_soft_build_lookahead: the uniform-count bias table of build_lookahead
+ * (ops.py:200-236), float32 [num_states, vocab]: k-1 rounds of
+ * logZ(s) = logsumexp_t logZ(tok_next[s, t]) (logaddexp with 0 for accepting
+ * s, -inf off the live set), then out[s, t] = logZ(tok_next[s, t]), -inf on
+ * rejected tokens, 0 / -inf in the EOS column.  Workspace:
+ * bpd_soft_workspace_bytes(0, num_states, k).
+ */
+size_t bpd_soft_workspace_bytes(int64_t rows, int32_t num_states, int32_t k);
+int bpd_soft_build_lookahead(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                             const uint8_t* accept, const uint8_t* live, int32_t eos_id, int32_t k,
+                             float* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* bpd_soft_apply: logits[b, t] += alpha * lookahead[state(b), t] on finite
+ * entries (float arithmetic, stored in the logits dtype) and -inf where the
+ * lookahead is -inf or state(b) < 0 (apply_soft_, ops.py:239-259, called by
+ * ConstraintBatch.apply_soft, batch.py:192-204). */
+int bpd_soft_apply(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                   const float* lookahead, int32_t num_states, const int32_t* states,
+                   const int64_t* slots, float alpha, int32_t* err, void* stream);
+
+int bpd_host_soft_build_lookahead(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                                  const uint8_t* accept, const uint8_t* live, int32_t eos_id,
+                                  int32_t k, float* out);
+int bpd_host_soft_apply(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                        const float* lookahead, int32_t num_states, const int32_t* states,
+                        const int64_t* slots, float alpha);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,7 @@ _TORCH_BITS = {torch.float32: (torch.int32, np.uint32), torch.float16: (torch.in
 def fill_bits(dtype: torch.dtype, value: float) -> int:
     """Bit pattern ATen stores for ``value`` in a ``dtype`` tensor."""
     ibits, npt = _TORCH_BITS[dtype]
-    t = torch.full((1,), value, dtype=dtype)  # raises exactly as masked_fill_ does
+    t = torch.zeros(1, dtype=dtype).masked_fill_(torch.ones(1, dtype=torch.bool), value)
     return int(t.view(ibits).numpy().astype(npt)[0])
 
 

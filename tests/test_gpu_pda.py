@@ -1,0 +1,139 @@
+"""PDA step on the device (HIP kernels through the C ABI) against the C
+oracle: masks, ok flags, status and raw 266-word config-sets, on the
+reference's toy grammars (saturating flattening included) and on the
+recursive JSON grammar at V = 151,936."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from bpdecode_amd import synth
+from bpdecode_amd.grammar.device import (
+    CFGConstraintBatch, build_pda_tensors, pda_compute_mask, pda_mask_, pda_step,
+)
+from bpdecode_amd.grammar.gbnf import parse_gbnf
+from bpdecode_amd.grammar.pda import CompiledGrammar
+from oracle import pda as OP
+from tests._util import PDA_VOCAB as VOCAB
+from tests.golden.cases import GRAMMARS
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("idx", range(len(GRAMMARS)))
+@pytest.mark.parametrize("reduce", [False, True])
+def test_toy_trajectories_match_oracle(dev, idx, reduce):
+    _log(f"case toy grammar {idx} reduce={reduce}")
+    g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(GRAMMARS[idx])), VOCAB, eps_reduce=reduce)
+    t = OP.Table(g)
+    gd = g.to(dev)
+    rng = np.random.default_rng(idx)
+    cap, B = 12, 7
+    pool = gd.init_batch(cap)
+    broken = torch.zeros(cap, dtype=torch.bool, device=dev)
+    mirror = pool.cpu().numpy().copy()
+    mbroken = np.zeros(cap, dtype=bool)
+    for step in range(20):
+        sl = rng.choice(cap, size=B, replace=False)
+        slots = torch.from_numpy(sl).to(dev)
+        sub = mirror[sl]
+        bits = pda_compute_mask(gd, pool, slots).cpu().numpy().view(np.uint32)
+        assert np.array_equal(bits, OP.compute_mask(t, sub)), step
+        for dtype in (torch.float32, torch.bfloat16, torch.float16):
+            lg = torch.randn(B, VOCAB.size).to(dtype)
+            want = lg.clone()
+            ref = lg.float().numpy().copy()
+            OP.apply_mask(t, sub, ref)
+            ref[mbroken[sl]] = -np.inf
+            want[torch.from_numpy(np.isneginf(ref))] = float("-inf")
+            got = lg.to(dev)
+            pda_mask_(got, gd, pool, slots, broken)
+            assert torch.equal(got.cpu().view(torch.uint8), want.view(torch.uint8)), (step, dtype)
+        toks = []
+        for r in range(B):
+            allowed = [k for k in range(VOCAB.size) if bits[r, k >> 5] >> (k & 31) & 1]
+            toks.append(int(rng.choice(allowed)) if allowed and rng.random() < 0.85
+                        else int(rng.integers(VOCAB.size)))
+        ok, status = pda_step(pool, gd, torch.tensor(toks, dtype=torch.int32, device=dev), slots, broken)
+        sub2 = sub.copy()
+        ok_o = OP.advance(t, sub2, toks)
+        mirror[sl] = sub2
+        mbroken[sl] |= ok_o == 0
+        assert ok.cpu().tolist() == ok_o.tolist(), step
+        assert status.cpu().tolist() == [-1 if mbroken[s] else 1 for s in sl.tolist()]
+        assert np.array_equal(pool.cpu().numpy(), mirror), step
+        assert np.array_equal(broken.cpu().numpy(), mbroken)
+
+
+@pytest.fixture(scope="module")
+def json_case():
+    vocab = synth.serving_vocab(151_936, seed=1)
+    comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
+    g = build_pda_tensors(comp, vocab, eps_reduce=True)
+    return vocab, g, OP.Table(g)
+
+
+def _json_configs(g, n, seed):
+    rng = np.random.default_rng(seed)
+    rows = []
+    while len(rows) < n:
+        c = g.init_config()
+        if g.feed(c, synth.json_prefix(rng, int(rng.integers(0, 9)))):
+            rows.append(c)
+    return torch.stack(rows)
+
+
+def test_json_full_vocab_masks_and_commits(dev, json_case):
+    vocab, g, t = json_case
+    _log("case json V=151936 B=12 mask+commit 4 steps")
+    cfgs = _json_configs(g, 12, seed=3)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    mirror = cfgs.numpy().copy()
+    gen = torch.Generator().manual_seed(0)
+    for step in range(4):
+        bits = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+        want = OP.compute_mask(t, mirror)
+        assert np.array_equal(bits, want), step
+        lg = synth.logits(12, vocab.size, 3.0, torch.float32, seed=step)
+        got = lg.to(dev)
+        pda_mask_(got, gd, pool)
+        ref = lg.numpy().copy()
+        OP.apply_mask(t, mirror, ref)
+        assert np.array_equal(got.cpu().numpy(), ref), step
+        probs = torch.softmax(torch.from_numpy(ref), dim=-1)
+        toks = torch.multinomial(probs, 1, generator=gen).view(-1).to(torch.int32)
+        ok, _ = pda_step(pool, gd, toks.to(dev))
+        ok_o = OP.advance(t, mirror, toks.numpy())
+        assert ok.cpu().tolist() == ok_o.tolist() and ok_o.all()
+        assert np.array_equal(pool.cpu().numpy(), mirror), step
+
+
+def test_json_batch_api_b64(dev, json_case):
+    vocab, g, t = json_case
+    _log("case json CFGConstraintBatch B=64 2 steps")
+    cfgs = _json_configs(g, 64, seed=9)
+    batch = CFGConstraintBatch(g, capacity=64, device=dev)
+    for i in range(64):
+        batch.add(i)
+    batch._configs.copy_(cfgs.to(dev))
+    mirror = cfgs.numpy().copy()
+    ids = list(range(64))
+    for step in range(2):
+        lg = torch.zeros(64, vocab.size, device=dev)
+        batch.apply_mask(ids, lg)
+        ref = np.zeros((64, vocab.size), np.float32)
+        OP.apply_mask(t, mirror, ref)
+        assert np.array_equal(lg.cpu().numpy(), ref), step
+        toks = [int(np.nonzero(ref[r] == 0)[0][step % max(1, np.count_nonzero(ref[r] == 0))])
+                for r in range(64)]
+        status = batch.commit(ids, torch.tensor(toks, device=dev))
+        OP.advance(t, mirror, toks)
+        assert status.cpu().tolist() == [1] * 64
+        assert np.array_equal(batch._configs.cpu().numpy(), mirror)
