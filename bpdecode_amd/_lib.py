@@ -49,6 +49,7 @@ _SIGNATURES = {
     "bpd_last_error": (C.c_char_p, []),
     "bpd_abi_version": (cint, []),
     "bpd_dense_apply_mask": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f64, vp, vp]),
+    "bpd_dense_apply_mask_bits": (cint, [vp, cint, i64, i64, i64, vp, i64, i32, vp, vp, f64, vp, vp]),
     "bpd_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, cint, i64, vp, cint, vp, vp]),
     "bpd_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp, vp, vp]),
     "bpd_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp, vp]),

@@ -125,6 +125,8 @@ class ConstraintBatch:
         if mask_cache is True:
             mask_cache = MaskCache(self.fsa)
         self.cache: MaskCache | None = mask_cache or None
+        if self.device.type == "cuda" and self.fsa.tok_next is not None:
+            self.fsa.ensure_allow_bits()
 
     # --- pool -----------------------------------------------------------
     def _flush(self) -> None:
@@ -184,6 +186,8 @@ class ConstraintBatch:
         pool = self._state
         if self.cache is not None:
             self.cache.apply(pool[slots], logits, neg_inf)
+        elif self.fsa.allow_bits is not None and logits.device.type == "cuda":
+            ops.dense_mask_bits_(logits, self.fsa.allow_bits, pool, slots, neg_inf, self._err)
         elif self.fsa.tok_next is not None:
             ops.dense_mask_(logits, self.fsa.tok_next, pool, slots, neg_inf, self._err)
         else:

@@ -4,14 +4,21 @@
 //
 // apply_mask is HBM-bound integer work: per row it streams the logits row
 // once (read + write, unit stride) and the int32 tok_next row of that row's
-// state.  A 256-thread block owns a 2048-column slab of kRows rows; each lane
+// state.  A 256-thread block owns a 2048-column slab of a few rows; each lane
 // handles 8 consecutive columns with 16-byte vector accesses, issuing all
-// loads of its kRows rows before any store.  Logits use non-temporal
-// accesses (streamed once) so the L2 keeps tok_next rows, which are shared by
-// every row in the same DFA state.  Blocks are numbered so that all row-slabs
-// of one column slab run on the same XCD (workgroups are dealt round-robin
-// to the 8 XCDs), so each (state, column slab) tile of tok_next is fetched
-// from HBM into one L2 and re-read from there by the other rows in that state.
+// loads of its rows before any store.  Blocks are numbered so that all
+// row-slabs of one column slab run on the same XCD (workgroups are dealt
+// round-robin to the 8 XCDs), so each (state, column slab) tile of the table
+// is fetched from HBM into one L2 and re-read from there by the other rows in
+// that state.
+//
+// The mask only needs "tok_next[s, t] != -1", so the serving path masks from
+// a packed allow-bit table (1 bit per (state, token), LSB-first uint32 words,
+// built once per grammar from tok_next by the bit kernel below): a lane's 8
+// verdicts are one byte, and table traffic drops 32x against the int32 rows.
+// Measured on MI355X the logits stream then sets the pace; plain (temporal)
+// global loads/stores beat non-temporal ones for this read-modify-write
+// pattern.
 #include <algorithm>
 
 #include "bpd_common.hpp"
@@ -25,7 +32,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kVec = 8;                          // columns per lane
 constexpr int64_t kSlab = int64_t(kThreads) * kVec;  // columns per block
-constexpr int kRows = 4;                         // rows per block
+constexpr int kRows = 2;                         // rows per block (int32 table)
+constexpr int kBitRows = 4;                      // rows per block (bit table)
 constexpr int kXcds = 8;
 
 __device__ __forceinline__ int32_t row_state(const int32_t* __restrict__ states,
@@ -75,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void dense_mask_vec_kernel(
     if (r < rows) {
       const u32x4* p = reinterpret_cast<const u32x4*>(logits + r * ld_bytes + col * E);
 #pragma unroll
-      for (int k = 0; k < E / 2; ++k) lg[i][k] = __builtin_nontemporal_load(p + k);
+      for (int k = 0; k < E / 2; ++k) lg[i][k] = p[k];
     }
   }
 #pragma unroll
@@ -105,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void dense_mask_vec_kernel(
                                        fill | (fill << 16), fill | (fill << 16)}
                                : u32x4{fill, fill, fill, fill};
 #pragma unroll
-      for (int k = 0; k < E / 2; ++k) __builtin_nontemporal_store(f, p + k);
+      for (int k = 0; k < E / 2; ++k) p[k] = f;
       continue;
     }
     if (E == 2) {
@@ -114,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void dense_mask_vec_kernel(
       v.y = pick16(v.y, tn[i][0].z, tn[i][0].w, fill);
       v.z = pick16(v.z, tn[i][1].x, tn[i][1].y, fill);
       v.w = pick16(v.w, tn[i][1].z, tn[i][1].w, fill);
-      __builtin_nontemporal_store(v, p);
+      *p = v;
     } else {
       u32x4 a = lg[i][0], b = lg[i][E / 2 - 1];
       a.x = tn[i][0].x == -1 ? fill : a.x;
@@ -125,8 +133,100 @@ __global__ __launch_bounds__(kThreads) void dense_mask_vec_kernel(
       b.y = tn[i][1].y == -1 ? fill : b.y;
       b.z = tn[i][1].z == -1 ? fill : b.z;
       b.w = tn[i][1].w == -1 ? fill : b.w;
-      __builtin_nontemporal_store(a, p);
-      __builtin_nontemporal_store(b, p + 1);
+      p[0] = a;
+      p[1] = b;
+    }
+  }
+}
+
+// Mask from the packed allow-bit table: byte (col / 8) of a state's bit row
+// holds the verdicts of the lane's 8 columns.
+template <int E>
+__global__ __launch_bounds__(kThreads) void dense_mask_bits_kernel(
+    uint8_t* __restrict__ logits, int64_t ld_bytes, const uint8_t* __restrict__ bits,
+    int64_t row_bytes, int64_t vocab, int32_t num_states, const int32_t* __restrict__ states,
+    const int64_t* __restrict__ slots, int64_t rows, uint32_t row_slabs, uint32_t col_slabs,
+    uint32_t fill, int32_t* __restrict__ err) {
+  const uint32_t lb = logical_block();
+  const uint32_t cs = lb / row_slabs;
+  const uint32_t rs = lb - cs * row_slabs;
+  if (cs >= col_slabs) return;
+  const int64_t col = int64_t(cs) * kSlab + int64_t(threadIdx.x) * kVec;
+  if (col >= vocab) return;  // vocab % kVec == 0 on this path
+  const int64_t r0 = int64_t(rs) * kBitRows;
+  u32x4 lg[kBitRows][E / 2];
+  int64_t slot[kBitRows];
+  int32_t st[kBitRows];
+  uint32_t m[kBitRows];
+#pragma unroll
+  for (int i = 0; i < kBitRows; ++i) {
+    const int64_t r = r0 + i;
+    if (r < rows) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(logits + r * ld_bytes + col * E);
+#pragma unroll
+      for (int k = 0; k < E / 2; ++k) lg[i][k] = p[k];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kBitRows; ++i) {
+    const int64_t r = r0 + i;
+    slot[i] = (r < rows) ? (slots ? slots[r] : r) : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kBitRows; ++i) st[i] = (slot[i] >= 0) ? states[slot[i]] : -1;
+#pragma unroll
+  for (int i = 0; i < kBitRows; ++i)
+    m[i] = (st[i] >= 0 && st[i] < num_states) ? uint32_t(bits[int64_t(st[i]) * row_bytes + (col >> 3)]) : 0u;
+#pragma unroll
+  for (int i = 0; i < kBitRows; ++i) {
+    const int64_t r = r0 + i;
+    if (r >= rows) break;
+    if (st[i] >= num_states && err && threadIdx.x == 0 && cs == 0) atomicOr(err, BPD_FLAG_STATE_RANGE);
+    u32x4* p = reinterpret_cast<u32x4*>(logits + r * ld_bytes + col * E);
+    const uint32_t mm = m[i];
+    if (E == 2) {
+      u32x4 v = lg[i][0];
+      v.x = ((mm & 1u) ? (v.x & 0xFFFFu) : fill) | (((mm & 2u) ? (v.x >> 16) : fill) << 16);
+      v.y = ((mm & 4u) ? (v.y & 0xFFFFu) : fill) | (((mm & 8u) ? (v.y >> 16) : fill) << 16);
+      v.z = ((mm & 16u) ? (v.z & 0xFFFFu) : fill) | (((mm & 32u) ? (v.z >> 16) : fill) << 16);
+      v.w = ((mm & 64u) ? (v.w & 0xFFFFu) : fill) | (((mm & 128u) ? (v.w >> 16) : fill) << 16);
+      *p = v;
+    } else {
+      u32x4 a = lg[i][0], b = lg[i][E / 2 - 1];
+      a.x = (mm & 1u) ? a.x : fill;
+      a.y = (mm & 2u) ? a.y : fill;
+      a.z = (mm & 4u) ? a.z : fill;
+      a.w = (mm & 8u) ? a.w : fill;
+      b.x = (mm & 16u) ? b.x : fill;
+      b.y = (mm & 32u) ? b.y : fill;
+      b.z = (mm & 64u) ? b.z : fill;
+      b.w = (mm & 128u) ? b.w : fill;
+      p[0] = a;
+      p[1] = b;
+    }
+  }
+}
+
+// Any alignment / vocab, bit table: one element per lane per step.
+template <int E>
+__global__ __launch_bounds__(kThreads) void dense_mask_bits_scalar_kernel(
+    uint8_t* __restrict__ logits, int64_t ld_bytes, const uint32_t* __restrict__ bits,
+    int64_t words, int64_t vocab, int32_t num_states, const int32_t* __restrict__ states,
+    const int64_t* __restrict__ slots, int64_t rows, uint32_t fill, int32_t* __restrict__ err) {
+  const int64_t r = blockIdx.y;
+  if (r >= rows) return;
+  const int32_t s = row_state(states, slots, r);
+  const bool whole = s < 0 || s >= num_states;
+  if (s >= num_states && err && threadIdx.x == 0 && blockIdx.x == 0) atomicOr(err, BPD_FLAG_STATE_RANGE);
+  uint8_t* row = logits + r * ld_bytes;
+  const uint32_t* bw = bits + (whole ? 0 : int64_t(s) * words);
+  for (int64_t t = int64_t(blockIdx.x) * kThreads + threadIdx.x; t < vocab;
+       t += int64_t(gridDim.x) * kThreads) {
+    if (whole || !((bw[t >> 5] >> (t & 31)) & 1u)) {
+      if (E == 2)
+        *reinterpret_cast<uint16_t*>(row + t * 2) = static_cast<uint16_t>(fill);
+      else
+        *reinterpret_cast<uint32_t*>(row + t * 4) = fill;
     }
   }
 }
@@ -406,6 +506,57 @@ extern "C" int bpd_build_tok_next(const int32_t* trans, int32_t num_states, int3
   build_tok_next_kernel<<<grid, 256, 0, as_stream(stream)>>>(
       trans, num_states, num_symbols, dead, accept, live, tok_offsets, tok_symbols, vocab,
       eos_id, row_states, num_rows, out);
+  BPD_LAUNCHED();
+  return BPD_OK;
+}
+
+extern "C" int bpd_dense_apply_mask_bits(void* logits, int dtype, int64_t rows, int64_t vocab,
+                                         int64_t ld, const uint32_t* allow_bits, int64_t words,
+                                         int32_t num_states, const int32_t* states,
+                                         const int64_t* slots, double neg_inf, int32_t* err,
+                                         void* stream) {
+  const int E = elem_bytes(dtype);
+  BPD_REQUIRE(E != 0, "unknown logits dtype code %d", dtype);
+  BPD_REQUIRE(rows >= 0 && vocab >= 0 && ld >= vocab, "bad logits shape rows=%lld vocab=%lld ld=%lld",
+              (long long)rows, (long long)vocab, (long long)ld);
+  BPD_REQUIRE(num_states > 0, "empty allow-bit table");
+  BPD_REQUIRE(words == (vocab + 31) / 32, "allow-bit rows must hold ceil(vocab/32) words");
+  uint32_t fill = 0;
+  if (int rc = fill_bits(dtype, neg_inf, &fill)) return rc;
+  if (rows == 0 || vocab == 0) return BPD_OK;
+  BPD_REQUIRE(logits && allow_bits && states, "null pointer argument");
+  hipStream_t s = as_stream(stream);
+  const int64_t ld_bytes = ld * E;
+  const bool aligned = (vocab % kVec == 0) && (ld_bytes % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(logits) % 16 == 0);
+  if (aligned) {
+    const int64_t col_slabs = (vocab + kSlab - 1) / kSlab;
+    const int64_t row_slabs = (rows + kBitRows - 1) / kBitRows;
+    int64_t blocks = col_slabs * row_slabs;
+    blocks = (blocks + kXcds - 1) / kXcds * kXcds;
+    BPD_REQUIRE(blocks < (int64_t(1) << 31), "batch too large for one launch");
+    const uint8_t* b8 = reinterpret_cast<const uint8_t*>(allow_bits);
+    if (E == 2)
+      dense_mask_bits_kernel<2><<<dim3(unsigned(blocks)), dim3(kThreads), 0, s>>>(
+          static_cast<uint8_t*>(logits), ld_bytes, b8, words * 4, vocab, num_states, states, slots,
+          rows, uint32_t(row_slabs), uint32_t(col_slabs), fill, err);
+    else
+      dense_mask_bits_kernel<4><<<dim3(unsigned(blocks)), dim3(kThreads), 0, s>>>(
+          static_cast<uint8_t*>(logits), ld_bytes, b8, words * 4, vocab, num_states, states, slots,
+          rows, uint32_t(row_slabs), uint32_t(col_slabs), fill, err);
+  } else {
+    BPD_REQUIRE(rows < 65536, "unaligned path supports at most 65535 rows");
+    const int64_t gx = std::min<int64_t>((vocab + kThreads - 1) / kThreads, 1024);
+    const dim3 grid = dim3(unsigned(gx), unsigned(rows));
+    if (E == 2)
+      dense_mask_bits_scalar_kernel<2><<<grid, dim3(kThreads), 0, s>>>(
+          static_cast<uint8_t*>(logits), ld_bytes, allow_bits, words, vocab, num_states, states,
+          slots, rows, fill, err);
+    else
+      dense_mask_bits_scalar_kernel<4><<<grid, dim3(kThreads), 0, s>>>(
+          static_cast<uint8_t*>(logits), ld_bytes, allow_bits, words, vocab, num_states, states,
+          slots, rows, fill, err);
+  }
   BPD_LAUNCHED();
   return BPD_OK;
 }

@@ -54,6 +54,9 @@ class FsaTensors:
     accepting: frozenset = frozenset()
     tok_next: torch.Tensor | None = None  # int32 [num_states, vocab]
     lookahead: torch.Tensor | None = None  # float32 [num_states, vocab]
+    # packed allow bits derived from tok_next: int32 [num_states, ceil(vocab/32)],
+    # bit t of row s set iff tok_next[s, t] != -1 (the device mask reads these)
+    allow_bits: torch.Tensor | None = None
 
     @property
     def device(self) -> torch.device:
@@ -74,13 +77,23 @@ class FsaTensors:
         return FsaTensors(
             mv(self.trans), mv(self.accept), mv(self.live), self.num_symbols, self.dead,
             mv(self.offsets), mv(self.symbols), self.eos_id, self.start, self.accepting,
-            mv(self.tok_next), mv(self.lookahead),
+            mv(self.tok_next), mv(self.lookahead), mv(self.allow_bits),
         )
 
     def densify(self) -> FsaTensors:
         if self.tok_next is not None:
             return self
         return replace(self, tok_next=build_token_transitions(self))
+
+    def ensure_allow_bits(self) -> torch.Tensor:
+        """The packed allow-bit table (built once from tok_next and kept on
+        this bundle; derived data, so sharing bundles is unaffected)."""
+        if self.allow_bits is None:
+            base = self.densify()
+            st = torch.arange(base.num_states, dtype=torch.int32, device=base.device)
+            self.tok_next = base.tok_next
+            self.allow_bits = dense_compute_mask(base.tok_next, st)
+        return self.allow_bits
 
     def with_lookahead(self, k: int = 3) -> FsaTensors:
         base = self.densify()
@@ -228,6 +241,32 @@ def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err
     return logits
 
 
+def dense_mask_bits_(logits, allow_bits, states, slots=None, neg_inf=float("-inf"), err=None):
+    """Device mask from the packed allow-bit table (same result as
+    :func:`dense_mask_`)."""
+    dev = _same_device(logits, allow_bits, states, slots)
+    if dev.type != "cuda":
+        raise RuntimeError("the allow-bit mask runs on the device; use dense_mask_ on the host")
+    work, copied = _unit_stride_rows(logits)
+    B, V = work.shape
+    S, W = allow_bits.shape
+    if W != (V + 31) // 32:
+        raise RuntimeError(f"logits have {V} columns but the allow-bit table has {W} words per row")
+    if slots is not None and slots.numel() != B:
+        raise RuntimeError("one slot per logits row")
+    st = _i32(states)
+    if slots is None and st.numel() != B:
+        raise RuntimeError(f"one state per logits row (got {st.numel()} states for {B} rows)")
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    code = _lib.dtype_code(work.dtype)
+    ld = work.stride(0) if B > 1 else V
+    check(lib().bpd_dense_apply_mask_bits(ptr(work), code, B, V, ld, ptr(allow_bits), W, S, ptr(st),
+                                          ptr(sl), float(neg_inf), ptr(err), _lib.stream_of(dev)))
+    if copied:
+        logits.copy_(work)
+    return logits
+
+
 def dense_advance(tok_next, states, tokens, slots=None, write_back=False, err=None):
     """Next state per row; with ``write_back`` the pool ``states`` is updated
     at the rows' slots as well.  Host-side token ids for a device table are
@@ -332,6 +371,8 @@ def apply_mask_(logits: torch.Tensor, fsa: FsaTensors, states: torch.Tensor,
     """In place: every disallowed logit of ``logits`` [batch, vocab] becomes
     ``neg_inf``, one grammar state per row (ops.py:262-281)."""
     if fsa.tok_next is not None:
+        if logits.device.type == "cuda":
+            return dense_mask_bits_(logits, fsa.ensure_allow_bits(), states, neg_inf=neg_inf)
         return dense_mask_(logits, fsa.tok_next, states, neg_inf=neg_inf)
     rows, idx = _walked_rows(fsa, states)
     return dense_mask_(logits, rows, idx, neg_inf=neg_inf)

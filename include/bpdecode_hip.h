@@ -73,6 +73,17 @@ int bpd_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, i
                          const int32_t* states, const int64_t* slots, double neg_inf,
                          int32_t* err, void* stream);
 
+/* bpd_dense_apply_mask_bits: the same mask from the packed allow-bit table
+ * (uint32 [num_states, words], words = ceil(vocab/32), bit t of row s set iff
+ * tok_next[s, t] != -1 -- bpd_dense_compute_mask over every state builds it).
+ * Results are identical to bpd_dense_apply_mask; the table read per row is
+ * vocab/8 bytes instead of 4*vocab.  Serves the same reference entry points
+ * (ops.py:271-276 via batch.py:176-190). */
+int bpd_dense_apply_mask_bits(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                              const uint32_t* allow_bits, int64_t words, int32_t num_states,
+                              const int32_t* states, const int64_t* slots, double neg_inf,
+                              int32_t* err, void* stream);
+
 /* bpd_dense_advance: nxt = state(b) < 0 ? -1 : tok_next[state(b), t(b)], where
  * t(b) = (int32)tokens[b] and a negative t indexes from the end as torch
  * advanced indexing does.  Writes next_out[b] (if non-NULL) and, with

@@ -168,7 +168,10 @@ def test_edge_cases(dev, dtype, neg_inf, shape):
         assert torch.equal(wide[:, :8].cpu(), torch.zeros(B, 8, dtype=dtype))
     else:
         got = base.to(dev)
-        ops.apply_mask_(got, fdev, torch.from_numpy(st).to(dev), neg_inf)
+        ops.apply_mask_(got, fdev, torch.from_numpy(st).to(dev), neg_inf)  # allow-bit kernel
+        got32 = base.to(dev)
+        ops.dense_mask_(got32, fdev.tok_next, torch.from_numpy(st).to(dev), neg_inf=neg_inf)  # int32 table
+        assert np.array_equal(bits_of(got32), bits_of(want))
     assert np.array_equal(bits_of(got), bits_of(want))
     bits = ops.compute_mask(fdev, torch.from_numpy(st).to(dev))
     assert np.array_equal(bits.cpu().numpy().view(np.uint32), OD.compute_mask_bits(tn, st))
