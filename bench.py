@@ -89,11 +89,15 @@ def parse_args(argv=None):
     p.add_argument("--cpu-steps", type=int, default=8, help="recorded steps replayed on the CPU")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
-    p.add_argument("--workload", choices=["dense", "pda"], default="dense",
+    p.add_argument("--workload", choices=["dense", "pda", "soft"], default="dense",
                    help="dense: email-regex tok_next step (the headline); pda: recursive-JSON PDA step")
     p.add_argument("--pda-rows", type=int, default=256)
     p.add_argument("--pda-steps", type=int, default=64)
     p.add_argument("--pda-cpu-rows", type=int, default=4, help="rows of one step replayed on the CPU oracle")
+    p.add_argument("--soft-rows", type=int, default=128)
+    p.add_argument("--soft-k", type=int, default=4)
+    p.add_argument("--soft-steps", type=int, default=64)
+    p.add_argument("--soft-cpu-rows", type=int, default=2, help="rows replayed on the float64 oracle")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="instead: run a plain device copy of MB megabytes 20 times (PMC scale check)")
     return p.parse_args(argv)
@@ -123,6 +127,8 @@ def main(argv=None) -> int:
         return 0
     if args.workload == "pda":
         return bench_pda(args)
+    if args.workload == "soft":
+        return bench_soft(args)
 
     import numpy as np
     import torch
@@ -403,6 +409,101 @@ def bench_pda(args) -> int:
             "host_cpus": os.cpu_count(),
         }
         out["parity_vs_oracle_sampled_rows"] = bool(np.array_equal(lg, masked[:n].numpy()))
+    print(json.dumps(out))
+    return 0
+
+
+def bench_soft(args) -> int:
+    """Prior-weighted soft lookahead over the email DFA: B rows at random
+    reachable states, fp32 logits N(0, 3), k-step lookahead with the row's
+    softmax as the token prior; one step = one in-place rewrite of the
+    [B, V] logits."""
+    import numpy as np
+    import torch
+
+    from bpdecode_amd import ops, synth
+    from bpdecode_amd.ops import FsaTensors
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, V, K = args.soft_rows, args.vocab, args.soft_k
+    vocab = synth.serving_vocab(V, seed=1)
+    fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
+    S = fsa.num_states
+    states = synth.random_walk_states(fsa.tok_next, fsa.start, fsa.eos_id, B, 40, seed=5).to(torch.int32)
+    fd = fsa.to(dev)
+    sc = fd.ensure_soft_classes()
+    st = states.to(dev)
+    src = synth.logits(B, V, std=3.0, dtype=torch.float32, seed=11, device=dev)
+    work = torch.empty_like(src)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if not args.no_flush else None
+    flush64 = flush.view(torch.int64) if flush is not None else None
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    n_total = args.warmup + args.soft_steps
+    kev = HipEvents(2 * n_total)
+    for k in range(n_total):
+        work.copy_(src)
+        if flush64 is not None:
+            flush64.sum()
+        kev.record(2 * k, sh)
+        ops.apply_soft_prior_(work, fd, st, K, 1.0)
+        kev.record(2 * k + 1, sh)
+    torch.cuda.synchronize()
+    times = [kev.elapsed_ms(2 * k, 2 * k + 1) for k in range(args.warmup, n_total)]
+    step_ms = statistics.fmean(times)
+    U = int(torch.unique(states[states >= 0]).numel())
+    members = int(sc.class_tok.numel())
+    # algorithmic bytes of one step: the stats kernel reads the logits and
+    # gathers the class members' logits; the output kernel reads the logits
+    # and the token -> class map and writes the logits
+    d_bytes = 3 * B * V * 4 + B * members * 4 + V * 4
+    out = {
+        "metric": "µs/step prior-weighted soft lookahead (k=4), email DFA, B=128 V=151936 fp32",
+        "value": round(step_ms * 1e3, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.soft_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": False,
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "soft lookahead with the row softmax as token prior, email DFA",
+                   "batch_rows": B, "vocab": V, "k": K, "dfa_states": S,
+                   "token_classes": sc.num_classes, "class_members": members,
+                   "distinct_row_states": U, "logits": "fp32 N(0,3)"},
+        "roofline": {"bound": "hbm", "achieved": round(d_bytes / (step_ms * 1e-3) / 1e9, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(d_bytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "scope": "whole step (3 kernels)",
+                     "algorithmic_bytes": d_bytes},
+        "row_vocab_entries_per_s": round(B * V / (step_ms * 1e-3), 1),
+    }
+    if not args.no_cpu and args.soft_cpu_rows:
+        from oracle import soft as OS
+
+        n = min(args.soft_cpu_rows, B)
+        x = src[:n].double().cpu().numpy()
+        tn = fsa.tok_next.numpy()
+        c0 = time.perf_counter()
+        want = OS.prior_lookahead(x, tn, fsa.live.numpy(), fsa.accept.numpy(), fsa.eos_id,
+                                  states[:n].numpy(), K, 1.0)
+        cpu_s = time.perf_counter() - c0
+        got = work[:n].double().cpu().numpy()
+        fin = np.isfinite(want)
+        ok = np.array_equal(np.isneginf(got), np.isneginf(want)) and bool(
+            np.all(np.abs(got[fin] - want[fin]) <= 1e-5 * np.abs(want[fin]) + 1e-5))
+        out["cpu_baseline"] = {
+            "value": round(cpu_s / n * B * 1e6, 1),
+            "unit": "us/step",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{n} rows through oracle/soft.py prior_lookahead (float64 numpy, dense "
+                      f"[S, V] gathers per round), scaled to B={B}",
+            "host_cpus": os.cpu_count(),
+        }
+        out["parity_vs_oracle_sampled_rows"] = ok
     print(json.dumps(out))
     return 0
 

@@ -45,6 +45,14 @@ class TokenBytesC(C.Structure):
     _fields_ = [("vocab_size", i32), ("eos_id", i32), ("offsets", vp), ("bytes", vp)]
 
 
+class SoftClassesC(C.Structure):
+    _fields_ = [
+        ("num_classes", i32), ("num_members", i32), ("num_pieces", i32), ("num_pairs", i32),
+        ("class_off", vp), ("class_tok", vp), ("class_piece", vp), ("piece_off", vp),
+        ("state_off", vp), ("pair_class", vp), ("pair_next", vp), ("token_class", vp),
+    ]
+
+
 _SIGNATURES = {
     "bpd_last_error": (C.c_char_p, []),
     "bpd_abi_version": (cint, []),
@@ -75,8 +83,11 @@ _SIGNATURES = {
     "bpd_soft_workspace_bytes": (sz, [i64, i32, i32]),
     "bpd_soft_build_lookahead": (cint, [vp, i32, i64, vp, vp, i32, i32, vp, vp, sz, vp]),
     "bpd_soft_apply": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f32, vp, vp]),
-    "bpd_soft_prior": (cint, [vp, i64, i64, i64, vp, i32, vp, vp, i32, vp, vp, vp, i32, f32,
-                              vp, sz, vp]),
+    "bpd_host_soft_classes": (cint, [vp, i32, i64, C.POINTER(SoftClassesC)]),
+    "bpd_soft_prior_workspace_bytes": (sz, [i64, i64, i32, i32]),
+    "bpd_soft_prior": (cint, [vp, i64, i64, i64, i32, vp, vp, i32, vp, vp, C.POINTER(SoftClassesC),
+                              i32, f32, vp, sz, vp, vp]),
+    "bpd_host_soft_prior": (cint, [vp, i64, i64, i64, vp, i32, vp, vp, i32, vp, vp, i32, f32]),
     "bpd_host_soft_build_lookahead": (cint, [vp, i32, i64, vp, vp, i32, i32, vp]),
     "bpd_host_soft_apply": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f32]),
 }

@@ -202,6 +202,16 @@ class ConstraintBatch:
         ops.soft_apply_(logits, self.fsa.lookahead, self._state, slots, alpha)
         return logits
 
+    def apply_soft_prior(self, seq_ids: Sequence[Hashable], logits: torch.Tensor, k: int = 4,
+                         alpha: float = 1.0) -> torch.Tensor:
+        """In place, float32 ``logits``: each row becomes its log-softmax
+        plus ``alpha`` times the log-probability, under the row's own
+        softmax, of staying on a live path for ``k - 1`` further tokens
+        (``-inf`` on grammar-disallowed tokens)."""
+        slots = self._slots(seq_ids)
+        ops.apply_soft_prior_(logits, self.fsa, self._state, k, alpha, slots=slots, err=self._err)
+        return logits
+
     def commit(self, seq_ids: Sequence[Hashable], tokens: torch.Tensor) -> torch.Tensor:
         """Advance each sequence by its sampled token; returns the new states
         (``BROKEN`` where the token was off a valid path)."""

@@ -9,6 +9,9 @@
 // the gather is an LDS read.  Rounds ping-pong two logZ vectors in the
 // caller's workspace.  A last pass writes out[s, t] = logZ(tok_next[s, t]).
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <unordered_map>
 #include <vector>
 
 #include "bpd_common.hpp"
@@ -312,6 +315,816 @@ extern "C" int bpd_host_soft_apply(void* logits, int dtype, int64_t rows, int64_
         std::memcpy(p, &ninf, size_t(E));
       else if (alpha != 0.0f)
         host_store(p, dtype, std::fmaf(alpha, bias, host_load(p, dtype)));
+    }
+  }
+  return BPD_OK;
+}
+
+// ------------------------------------------------------- prior-weighted --
+// Soft lookahead weighted by each row's own model prior.  With
+// logpi_b = log_softmax(logits_b) and k-1 rounds of
+//   logZ_0(s)     = 0 on live s, -inf elsewhere
+//   logZ_{j+1}(s) = logsumexp_t [logpi_b(t) + logZ_j(tok_next[s, t])]
+//                   (logaddexp with logpi_b(eos) for accepting s), -inf off live
+// the output is out[b, t] = logpi_b(t) + alpha * logZ_{k-1}(tok_next[s_b, t])
+// on allowed tokens, logpi_b(eos) / -inf in the EOS column, -inf elsewhere.
+// With logpi == 0 the recurrence is the uniform one above.  Logits are
+// expected finite or -inf.
+//
+// Token classes make the per-row work independent of the vocab size: tokens
+// whose tok_next columns are equal behave identically in every state, so a
+// round needs only logsumexp_{t in class} logpi_b(t) per class.  Classes are
+// built once per grammar on the host (bpd_host_soft_classes).  One call is
+// three kernels:
+//   stats:  grid (G, rows), block g streams tokens [8192 g, 8192 (g+1)) of
+//           its row with their class ids and leaves the chunk's logsumexp
+//           and, per class, (max, sum exp(x - max)) of its members: a
+//           class-max pass and a class-sum pass through LDS atomics.  Above
+//           kLdsClasses classes the class sums come from gathers over class
+//           pieces of <= 256 members instead (one wave per piece).
+//   rounds: one block per row merges the partials, runs the k-1 rounds with
+//           logZ, the class sums and the (class, next) pairs in LDS, and
+//           writes zcls[b, c] = logZ(next of class c from s_b) and lse[b].
+//   out:    one streaming pass, out = x - lse + alpha * zcls[b, class(t)].
+// The kernel boundaries order the cross-block hand-offs; an in-kernel
+// last-block hand-off needs agent-scope release fences, which write back the
+// whole L2 of each XCD on this part and cost far more than a launch.
+namespace bpd {
+namespace {
+
+constexpr int kPriorThreads = 512;
+constexpr int kPriorOutThreads = 256;
+constexpr int kPriorMaxStates = 4096;
+constexpr int kPieceMembers = 256;
+constexpr int kLdsClasses = 1024;                          // class-atomic stats up to this many classes
+constexpr int kStatLoads = 4;                              // float4 loads per thread (class-atomic stats)
+constexpr int64_t kStatChunk = kPriorThreads * 4 * kStatLoads;  // tokens per block
+constexpr size_t kPriorMaxLds = 60 * 1024;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x by the hardware exponential (v_exp_f32); used for x <= 0.
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// exp(x - m) for x <= m
+__device__ inline float exp_shift(float x, float m_log2e) { return exp2_fast(fmaf(x, kLog2e, -m_log2e)); }
+
+// Order-preserving int image of a float (and back: the map is an involution).
+__device__ inline int32_t ord_of(float x) {
+  const int32_t i = __float_as_int(x);
+  return i >= 0 ? i : i ^ 0x7FFFFFFF;
+}
+__device__ inline float float_of_ord(int32_t i) { return __int_as_float(i >= 0 ? i : i ^ 0x7FFFFFFF); }
+
+__device__ inline Lse wave_lse(Lse a) {
+  for (int o = 32; o > 0; o >>= 1) {
+    Lse b;
+    b.m = __shfl_xor(a.m, o);
+    b.s = __shfl_xor(a.s, o);
+    a = lse_merge(a, b);
+  }
+  return a;
+}
+
+// Block-wide merge of one Lse per thread; the result is valid in every thread.
+template <int kThreads>
+__device__ inline Lse block_lse(Lse a) {
+  __shared__ float wm[kThreads / 64];
+  __shared__ float ws[kThreads / 64];
+  a = wave_lse(a);
+  const int w = threadIdx.x / 64;
+  if ((threadIdx.x & 63) == 0) {
+    wm[w] = a.m;
+    ws[w] = a.s;
+  }
+  __syncthreads();
+  Lse r{-INFINITY, 0.0f};
+  for (int i = 0; i < kThreads / 64; ++i) r = lse_merge(r, Lse{wm[i], ws[i]});
+  __syncthreads();
+  return r;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Launch geometry of one call.
+struct PriorPlan {
+  bool class_stats;  // class-atomic stats (else pieces)
+  int G;             // chunk blocks per row
+  int Gp;            // piece blocks per row (pieces path)
+};
+
+PriorPlan prior_plan(int64_t rows, int64_t vocab, int32_t C, int32_t P, bool force_pieces) {
+  PriorPlan pl;
+  pl.class_stats = !force_pieces && C <= kLdsClasses;
+  if (pl.class_stats) {
+    pl.G = int((vocab + kStatChunk - 1) / kStatChunk);
+    pl.Gp = 0;
+  } else {
+    const int64_t g = rows > 0 ? (1024 + rows - 1) / rows : 1;
+    pl.G = int(g < 1 ? 1 : (g > 64 ? 64 : g));
+    pl.Gp = (P + 2 * (kPriorThreads / 64) - 1) / (2 * (kPriorThreads / 64));
+  }
+  return pl;
+}
+
+struct PriorWs {
+  float* part;   // [rows, G, 2] chunk logsumexp partials
+  float* mid;    // class-atomic: [rows, G, C, 2] class partials; pieces: [rows, P, 2]
+  float* lse;    // [rows]
+  float* zcls;   // [rows, C]
+};
+
+size_t prior_mid_floats(int64_t rows, const PriorPlan& pl, int32_t C, int32_t P) {
+  return pl.class_stats ? size_t(rows) * pl.G * C * 2 : size_t(rows) * P * 2;
+}
+
+PriorWs prior_ws(void* base, int64_t rows, const PriorPlan& pl, int32_t C, int32_t P) {
+  char* p = static_cast<char*>(base);
+  PriorWs w;
+  w.part = reinterpret_cast<float*>(p);
+  p += align256(size_t(rows) * pl.G * 8);
+  w.mid = reinterpret_cast<float*>(p);
+  p += align256(prior_mid_floats(rows, pl, C, P) * 4);
+  w.lse = reinterpret_cast<float*>(p);
+  p += align256(size_t(rows) * 4);
+  w.zcls = reinterpret_cast<float*>(p);
+  return w;
+}
+
+size_t prior_ws_bytes(int64_t rows, const PriorPlan& pl, int32_t C, int32_t P) {
+  return align256(size_t(rows) * pl.G * 8) + align256(prior_mid_floats(rows, pl, C, P) * 4) +
+         align256(size_t(rows) * 4) + align256(size_t(rows) * C * 4);
+}
+
+size_t prior_lds_bytes(int32_t S, int32_t C, int32_t P, int64_t pairs, bool pairs_in_lds, bool pieces) {
+  size_t n = size_t(C) * 4 + size_t(S) * 8 + size_t(S + 3) / 4 * 4 + size_t(S + 1) * 4;
+  if (pairs_in_lds) n += size_t(pairs) * 4;
+  n = (n + 7) / 8 * 8;
+  return pieces ? n + size_t(P) * 8 : n;
+}
+
+// Class-atomic stats, grid (G, rows): block g takes tokens
+// [kStatChunk g, kStatChunk (g+1)) of its row.
+template <bool Vec>
+__global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
+    const float* __restrict__ logits, int64_t ld, int64_t V, const int32_t* __restrict__ token_class,
+    int32_t C, PriorWs ws) {
+  __shared__ int32_t cmax[kLdsClasses];
+  __shared__ float csum[kLdsClasses];
+  constexpr int kE = 4 * kStatLoads;
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const float* row = logits + b * ld;
+  const int64_t base = int64_t(g) * kStatChunk;
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    cmax[c] = ord_of(-INFINITY);
+    csum[c] = 0.0f;
+  }
+  float x[kE];
+  int32_t k[kE];
+  if (Vec) {
+#pragma unroll
+    for (int u = 0; u < kStatLoads; ++u) {
+      const int64_t t = base + (int64_t(u) * kPriorThreads + threadIdx.x) * 4;
+      float4 xv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      int4 kv = make_int4(-1, -1, -1, -1);
+      if (t < V) {
+        xv = *reinterpret_cast<const float4*>(row + t);
+        kv = *reinterpret_cast<const int4*>(token_class + t);
+      }
+      x[4 * u] = xv.x;
+      x[4 * u + 1] = xv.y;
+      x[4 * u + 2] = xv.z;
+      x[4 * u + 3] = xv.w;
+      k[4 * u] = kv.x;
+      k[4 * u + 1] = kv.y;
+      k[4 * u + 2] = kv.z;
+      k[4 * u + 3] = kv.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kE; ++e) {
+      const int64_t t = base + int64_t(e) * kPriorThreads + threadIdx.x;
+      x[e] = t < V ? row[t] : -INFINITY;
+      k[e] = t < V ? token_class[t] : -1;
+    }
+  }
+  // chunk logsumexp
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < kE; ++e) m = fmaxf(m, x[e]);
+  Lse acc{-INFINITY, 0.0f};
+  if (m != -INFINITY) {
+    const float mb = m * kLog2e;
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kE; ++e) sum += exp_shift(x[e], mb);
+    acc = Lse{m, sum};
+  }
+  acc = block_lse<kPriorThreads>(acc);  // its barriers also publish the LDS init
+  if (threadIdx.x == 0) {
+    ws.part[(b * G + g) * 2] = acc.m;
+    ws.part[(b * G + g) * 2 + 1] = acc.s;
+  }
+  // per-class max, then per-class sum of exp(x - max)
+#pragma unroll
+  for (int e = 0; e < kE; ++e)
+    if (k[e] >= 0 && x[e] != -INFINITY) atomicMax(&cmax[k[e]], ord_of(x[e]));
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    if (k[e] >= 0 && x[e] != -INFINITY) {
+      const float cm = float_of_ord(cmax[k[e]]);
+      atomicAdd(&csum[k[e]], exp_shift(x[e], cm * kLog2e));
+    }
+  }
+  __syncthreads();
+  float* out = ws.mid + (b * G + g) * int64_t(C) * 2;
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    out[2 * c] = float_of_ord(cmax[c]);
+    out[2 * c + 1] = csum[c];
+  }
+}
+
+// Pieces stats, grid (G + Gp, rows): block g < G takes vocab chunk g
+// (partial row logsumexp), blocks G.. the class pieces (one wave per piece,
+// unnormalised piece logsumexp).
+template <bool Vec>
+__global__ __launch_bounds__(kPriorThreads) void prior_stats_pieces_kernel(
+    const float* __restrict__ logits, int64_t ld, int64_t V, int64_t chunk, int G,
+    BpdSoftClasses cls, PriorWs ws) {
+  const int g = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int32_t P = cls.num_pieces;
+  const float* row = logits + b * ld;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x / 64;
+  constexpr int kWaves = kPriorThreads / 64;
+  if (g >= G) {
+    const int nw = (int(gridDim.x) - G) * kWaves;
+    for (int32_t p = (g - G) * kWaves + wave; p < P; p += nw) {
+      const int32_t m0 = cls.piece_off[p], m1 = cls.piece_off[p + 1];
+      int32_t idx[kPieceMembers / 64];
+#pragma unroll
+      for (int j = 0; j < kPieceMembers / 64; ++j) {
+        const int32_t i = m0 + lane + 64 * j;
+        idx[j] = i < m1 ? cls.class_tok[i] : -1;
+      }
+      float v[kPieceMembers / 64];
+#pragma unroll
+      for (int j = 0; j < kPieceMembers / 64; ++j) v[j] = idx[j] >= 0 ? row[idx[j]] : -INFINITY;
+      Lse a{-INFINITY, 0.0f};
+#pragma unroll
+      for (int j = 0; j < kPieceMembers / 64; ++j) a = lse_push(a, v[j]);
+      a = wave_lse(a);
+      if (lane == 0) {
+        ws.mid[(b * P + p) * 2] = a.m;
+        ws.mid[(b * P + p) * 2 + 1] = a.s;
+      }
+    }
+    return;
+  }
+  const int64_t lo = g * chunk;
+  const int64_t hi = lo + chunk < V ? lo + chunk : V;
+  Lse acc{-INFINITY, 0.0f};
+  if (Vec) {
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    const int64_t q1 = hi / 4;
+    for (int64_t q = lo / 4 + threadIdx.x; q < q1; q += int64_t(kPriorThreads) * kStatLoads) {
+      float4 x[kStatLoads];
+#pragma unroll
+      for (int u = 0; u < kStatLoads; ++u) {
+        const int64_t qq = q + int64_t(u) * kPriorThreads;
+        x[u] = qq < q1 ? row4[qq] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      }
+      float m = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kStatLoads; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
+      if (m != -INFINITY) {
+        const float mb = m * kLog2e;
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kStatLoads; ++u)
+          sum += (exp_shift(x[u].x, mb) + exp_shift(x[u].y, mb)) + (exp_shift(x[u].z, mb) + exp_shift(x[u].w, mb));
+        acc = lse_merge(acc, Lse{m, sum});
+      }
+    }
+  } else {
+    for (int64_t t = lo + threadIdx.x; t < hi; t += kPriorThreads) acc = lse_push(acc, row[t]);
+  }
+  acc = block_lse<kPriorThreads>(acc);
+  if (threadIdx.x == 0) {
+    ws.part[(b * G + g) * 2] = acc.m;
+    ws.part[(b * G + g) * 2 + 1] = acc.s;
+  }
+}
+
+// One block per row: merge the partials into lse[b] and the class sums, run
+// the k-1 rounds with logZ, the class sums and (when they fit) the
+// (class, next) pairs in LDS, and write zcls[b, c] = logZ(next state of
+// class c from s_b) and lse[b].
+template <bool PairsInLds, bool ClassStats>
+__global__ __launch_bounds__(kPriorThreads) void prior_rounds_kernel(
+    const float* __restrict__ logits, int64_t ld, int32_t S, int G, BpdSoftClasses cls,
+    const uint8_t* __restrict__ accept, const uint8_t* __restrict__ live, int32_t eos,
+    const int32_t* __restrict__ states, const int64_t* __restrict__ slots, int32_t rounds,
+    PriorWs ws) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ float lse_sh;
+  const int64_t b = blockIdx.x;
+  const int32_t C = cls.num_classes, P = cls.num_pieces;
+  if (threadIdx.x < 64) {
+    Lse r{-INFINITY, 0.0f};
+    for (int i = threadIdx.x; i < G; i += 64)
+      r = lse_merge(r, Lse{ws.part[(b * G + i) * 2], ws.part[(b * G + i) * 2 + 1]});
+    r = wave_lse(r);
+    if (threadIdx.x == 0) lse_sh = lse_value(r);
+  }
+  float* lc = lds;           // [C] class logsumexp (unnormalised), later zcls
+  float* z0 = lc + C;        // [S]
+  float* z1 = z0 + S;        // [S]
+  uint8_t* flag = reinterpret_cast<uint8_t*>(z1 + S);  // [S] bit 0 live, bit 1 accept
+  int32_t* so = reinterpret_cast<int32_t*>(z1 + S + (S + 3) / 4);  // [S + 1]
+  uint32_t* pr = reinterpret_cast<uint32_t*>(so + S + 1);  // [pairs] class << 16 | next (PairsInLds)
+  if (ClassStats) {
+    // class c: merge of the G chunk partials (loads issued 4 at a time)
+    for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+      Lse a{-INFINITY, 0.0f};
+      const float* src = ws.mid + (b * G) * int64_t(C) * 2 + 2 * c;
+      int i = 0;
+      for (; i + 4 <= G; i += 4) {
+        float2 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float2*>(src + int64_t(i + u) * C * 2);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a = lse_merge(a, Lse{v[u].x, v[u].y});
+      }
+      for (; i < G; ++i) {
+        const float2 v = *reinterpret_cast<const float2*>(src + int64_t(i) * C * 2);
+        a = lse_merge(a, Lse{v.x, v.y});
+      }
+      lc[c] = lse_value(a);
+    }
+  } else {
+    // [P] piece (max, sum) pairs, 8-byte aligned after the pairs
+    const uintptr_t pc_at = reinterpret_cast<uintptr_t>(pr + (PairsInLds ? cls.num_pairs : 0));
+    float2* pc = reinterpret_cast<float2*>((pc_at + 7) & ~uintptr_t(7));
+    for (int32_t p = threadIdx.x; p < P; p += kPriorThreads)
+      pc[p] = make_float2(ws.mid[(b * P + p) * 2], ws.mid[(b * P + p) * 2 + 1]);
+    __syncthreads();
+    for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+      Lse a{-INFINITY, 0.0f};
+      for (int32_t p = cls.class_piece[c]; p < cls.class_piece[c + 1]; ++p) a = lse_merge(a, Lse{pc[p].x, pc[p].y});
+      lc[c] = lse_value(a);
+    }
+  }
+  for (int32_t s = threadIdx.x; s < S; s += kPriorThreads) {
+    const bool lv = live[s] != 0;
+    flag[s] = uint8_t((lv ? 1 : 0) | (accept[s] ? 2 : 0));
+    z0[s] = lv ? 0.0f : -INFINITY;
+  }
+  for (int32_t s = threadIdx.x; s <= S; s += kPriorThreads) so[s] = cls.state_off[s];
+  if (PairsInLds) {
+    constexpr int kU = 8;
+    for (int32_t i = threadIdx.x; i < cls.num_pairs; i += kPriorThreads * kU) {
+      int32_t pc_[kU], pn_[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int32_t j = i + u * kPriorThreads;
+        pc_[u] = j < cls.num_pairs ? cls.pair_class[j] : 0;
+        pn_[u] = j < cls.num_pairs ? cls.pair_next[j] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int32_t j = i + u * kPriorThreads;
+        if (j < cls.num_pairs) pr[j] = (uint32_t(pc_[u]) << 16) | uint32_t(pn_[u]);
+      }
+    }
+  }
+  __syncthreads();
+  const float lse = lse_sh;
+  const float lp_eos = eos >= 0 ? logits[b * ld + eos] - lse : -INFINITY;
+
+  // k-1 rounds; a group of Q lanes (a power of two dividing 64) per state,
+  // each lane taking every Q-th pair of the state: a max pass, then a sum of
+  // exp(v - max) pass, each closed by a Q-lane reduction
+  int Q = 1;
+  while (Q < 64 && 2 * Q * S <= kPriorThreads) Q *= 2;
+  const int groups = kPriorThreads / Q;
+  const int sub = threadIdx.x & (Q - 1);
+  const int passes = (S + groups - 1) / groups;
+  float* zc = z0;
+  float* zn = z1;
+  for (int32_t j = 0; j < rounds; ++j) {
+    for (int pass = 0; pass < passes; ++pass) {
+      const int32_t s = pass * groups + int32_t(threadIdx.x) / Q;
+      const bool on = s < S;
+      const int32_t i0 = on ? so[s] : 0;
+      const int32_t i1 = on ? so[s + 1] : 0;
+      float mx = -INFINITY;
+      for (int32_t i = i0 + sub; i < i1; i += Q) {
+        int32_t c, d;
+        if (PairsInLds) {
+          c = int32_t(pr[i] >> 16);
+          d = int32_t(pr[i] & 0xFFFFu);
+        } else {
+          c = cls.pair_class[i];
+          d = cls.pair_next[i];
+        }
+        mx = fmaxf(mx, lc[c] + zc[d]);
+      }
+      for (int o = Q / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      float sm = 0.0f;
+      if (mx != -INFINITY) {
+        const float mb = mx * kLog2e;
+        for (int32_t i = i0 + sub; i < i1; i += Q) {
+          int32_t c, d;
+          if (PairsInLds) {
+            c = int32_t(pr[i] >> 16);
+            d = int32_t(pr[i] & 0xFFFFu);
+          } else {
+            c = cls.pair_class[i];
+            d = cls.pair_next[i];
+          }
+          sm += exp_shift(lc[c] + zc[d], mb);
+        }
+      }
+      for (int o = Q / 2; o > 0; o >>= 1) sm += __shfl_xor(sm, o);
+      if (sub == 0 && on) {
+        const uint8_t f = flag[s];
+        float v = mx == -INFINITY ? -INFINITY : mx + logf(sm) - lse;
+        if (f & 2) v = log_add_exp(v, lp_eos);
+        zn[s] = (f & 1) ? v : -INFINITY;
+      }
+    }
+    __syncthreads();
+    float* t = zc;
+    zc = zn;
+    zn = t;
+  }
+
+  // zcls[b, c] = logZ(next state of class c from s_b), -inf when rejected
+  const int32_t sb = states[slots ? slots[b] : b];
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) lc[c] = -INFINITY;
+  __syncthreads();
+  if (sb >= 0 && sb < S) {
+    for (int32_t i = so[sb] + threadIdx.x; i < so[sb + 1]; i += kPriorThreads) {
+      const int32_t c = PairsInLds ? int32_t(pr[i] >> 16) : cls.pair_class[i];
+      const int32_t d = PairsInLds ? int32_t(pr[i] & 0xFFFFu) : cls.pair_next[i];
+      lc[c] = zc[d];
+    }
+  }
+  __syncthreads();
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) ws.zcls[b * C + c] = lc[c];
+  if (threadIdx.x == 0) ws.lse[b] = lse;
+}
+
+__device__ inline float prior_value(float x, float lse, int64_t t, float z, bool acc_s, int32_t eos,
+                                    float alpha) {
+  const float lp = x - lse;
+  if (t == eos) return acc_s ? lp : -INFINITY;
+  if (z == -INFINITY) return -INFINITY;
+  return alpha != 0.0f ? fmaf(alpha, z, lp) : lp;
+}
+
+constexpr int kOutLoads = 4;          // float4 loads in flight per thread
+constexpr int kOutLdsClasses = 4096;  // zcls rows up to this size are staged in LDS
+
+// grid (ceil(V / (16 * 256)), rows); each thread rewrites 16 tokens, four
+// float4 groups 256 * 4 tokens apart (coalesced per group).
+template <bool Vec, bool ZInLds>
+__global__ __launch_bounds__(kPriorOutThreads) void prior_out_kernel(
+    float* __restrict__ logits, int64_t ld, int64_t V, const int32_t* __restrict__ token_class,
+    int32_t C, const float* __restrict__ lse_in, const float* __restrict__ zcls, int32_t S,
+    const uint8_t* __restrict__ accept, int32_t eos, const int32_t* __restrict__ states,
+    const int64_t* __restrict__ slots, float alpha, int32_t* __restrict__ err) {
+  __shared__ float zs[ZInLds ? kOutLdsClasses : 1];
+  const int64_t b = blockIdx.y;
+  const int64_t base = int64_t(blockIdx.x) * kPriorOutThreads * 4 * kOutLoads;
+  const int32_t s = states[slots ? slots[b] : b];
+  float* row = logits + b * ld;
+  if (s < 0 || s >= S) {
+    if (s >= S && err && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, BPD_FLAG_STATE_RANGE);
+    for (int u = 0; u < 4 * kOutLoads; ++u) {
+      const int64_t t = base + int64_t(u) * kPriorOutThreads + threadIdx.x;
+      if (t < V) row[t] = -INFINITY;
+    }
+    return;
+  }
+  const float* zrow = zcls + b * C;
+  if (ZInLds) {
+    for (int32_t c = threadIdx.x; c < C; c += kPriorOutThreads) zs[c] = zrow[c];
+    __syncthreads();
+  }
+  const float* z = ZInLds ? zs : zrow;
+  const float lse = lse_in[b];
+  const bool acc_s = accept[s] != 0;
+  auto zof = [&](int32_t c) { return c >= 0 ? z[c] : -INFINITY; };
+  if (Vec) {
+    float4 x[kOutLoads];
+    int4 c[kOutLoads];
+#pragma unroll
+    for (int u = 0; u < kOutLoads; ++u) {
+      const int64_t t = base + (int64_t(u) * kPriorOutThreads + threadIdx.x) * 4;
+      if (t < V) {
+        x[u] = *reinterpret_cast<const float4*>(row + t);
+        c[u] = *reinterpret_cast<const int4*>(token_class + t);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kOutLoads; ++u) {
+      const int64_t t = base + (int64_t(u) * kPriorOutThreads + threadIdx.x) * 4;
+      if (t < V) {
+        float4 o;
+        o.x = prior_value(x[u].x, lse, t, zof(c[u].x), acc_s, eos, alpha);
+        o.y = prior_value(x[u].y, lse, t + 1, zof(c[u].y), acc_s, eos, alpha);
+        o.z = prior_value(x[u].z, lse, t + 2, zof(c[u].z), acc_s, eos, alpha);
+        o.w = prior_value(x[u].w, lse, t + 3, zof(c[u].w), acc_s, eos, alpha);
+        *reinterpret_cast<float4*>(row + t) = o;
+      }
+    }
+  } else {
+    for (int u = 0; u < 4 * kOutLoads; ++u) {
+      const int64_t t = base + int64_t(u) * kPriorOutThreads + threadIdx.x;
+      if (t < V) row[t] = prior_value(row[t], lse, t, zof(token_class[t]), acc_s, eos, alpha);
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool force_pieces() {
+  const char* e = std::getenv("BPD_SOFT_PRIOR_PIECES");
+  return e && *e && std::strcmp(e, "0") != 0;
+}
+
+}  // namespace
+}  // namespace bpd
+
+using namespace bpd;
+
+extern "C" size_t bpd_soft_prior_workspace_bytes(int64_t rows, int64_t vocab, int32_t num_classes,
+                                                 int32_t num_pieces) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  const int32_t C = num_classes > 0 ? num_classes : 0, P = num_pieces > 0 ? num_pieces : 0;
+  // room for either stats path
+  const size_t a = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, false), C, P);
+  const size_t b = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, true), C, P);
+  return a > b ? a : b;
+}
+
+extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld,
+                              int32_t num_states, const uint8_t* accept, const uint8_t* live,
+                              int32_t eos_id, const int32_t* states, const int64_t* slots,
+                              const BpdSoftClasses* classes, int32_t k, float alpha,
+                              void* workspace, size_t workspace_bytes, int32_t* err, void* stream) {
+  BPD_REQUIRE(rows >= 0 && vocab > 0 && ld >= vocab, "bad logits shape");
+  BPD_REQUIRE(num_states > 0 && num_states <= kPriorMaxStates, "1..%d states", kPriorMaxStates);
+  BPD_REQUIRE(classes, "null classes");
+  const BpdSoftClasses cls = *classes;
+  BPD_REQUIRE(cls.num_classes >= 0 && cls.num_pieces >= 0 && cls.num_pairs >= 0, "bad class counts");
+  BPD_REQUIRE(k >= 1, "k must be >= 1");
+  BPD_REQUIRE(eos_id < vocab, "eos id out of range");
+  if (rows == 0) return BPD_OK;
+  BPD_REQUIRE(rows < 65536, "at most 65535 rows");
+  BPD_REQUIRE(workspace_bytes >= bpd_soft_prior_workspace_bytes(rows, vocab, cls.num_classes, cls.num_pieces),
+              "workspace too small");
+  BPD_REQUIRE(logits && accept && live && states && workspace && cls.class_off && cls.class_piece &&
+                  cls.piece_off && cls.state_off && cls.token_class,
+              "null pointer argument");
+  const PriorPlan pl = prior_plan(rows, vocab, cls.num_classes, cls.num_pieces, force_pieces());
+  const bool pieces = !pl.class_stats;
+  const bool pairs_in_lds =
+      cls.num_classes < 65536 &&
+      prior_lds_bytes(num_states, cls.num_classes, cls.num_pieces, cls.num_pairs, true, pieces) <= kPriorMaxLds;
+  const size_t lds = prior_lds_bytes(num_states, cls.num_classes, cls.num_pieces, cls.num_pairs, pairs_in_lds, pieces);
+  BPD_REQUIRE(lds <= kPriorMaxLds, "%d states and %d classes exceed the LDS budget", num_states,
+              cls.num_classes);
+  hipStream_t st = as_stream(stream);
+  const PriorWs ws = prior_ws(workspace, rows, pl, cls.num_classes, cls.num_pieces);
+  const bool vec = vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) && aligned16(cls.token_class);
+  if (pl.class_stats) {
+    const dim3 grid = dim3(unsigned(pl.G), unsigned(rows));
+    if (vec) {
+      prior_stats_classes_kernel<true><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab, cls.token_class,
+                                                                      cls.num_classes, ws);
+    } else {
+      prior_stats_classes_kernel<false><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab, cls.token_class,
+                                                                       cls.num_classes, ws);
+    }
+  } else {
+    int64_t chunk = (vocab + pl.G - 1) / pl.G;
+    chunk = (chunk + 3) / 4 * 4;
+    const dim3 grid = dim3(unsigned(pl.G + pl.Gp), unsigned(rows));
+    if (vec) {
+      prior_stats_pieces_kernel<true><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab, chunk, pl.G, cls, ws);
+    } else {
+      prior_stats_pieces_kernel<false><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab, chunk, pl.G, cls, ws);
+    }
+  }
+  BPD_LAUNCHED();
+#define BPD_PRIOR_ROUNDS(LDSP, CLS)                                                                  \
+  prior_rounds_kernel<LDSP, CLS><<<unsigned(rows), kPriorThreads, lds, st>>>(                       \
+      logits, ld, num_states, pl.G, cls, accept, live, eos_id, states, slots, k - 1, ws)
+  if (pairs_in_lds && pl.class_stats) BPD_PRIOR_ROUNDS(true, true);
+  else if (pairs_in_lds) BPD_PRIOR_ROUNDS(true, false);
+  else if (pl.class_stats) BPD_PRIOR_ROUNDS(false, true);
+  else BPD_PRIOR_ROUNDS(false, false);
+#undef BPD_PRIOR_ROUNDS
+  BPD_LAUNCHED();
+  const dim3 ogrid = dim3(unsigned((vocab + 4 * kOutLoads * kPriorOutThreads - 1) /
+                                   (4 * kOutLoads * kPriorOutThreads)),
+                          unsigned(rows));
+  const bool z_lds = cls.num_classes <= kOutLdsClasses;
+#define BPD_PRIOR_OUT(VEC, ZL)                                                                   \
+  prior_out_kernel<VEC, ZL><<<ogrid, kPriorOutThreads, 0, st>>>(                               \
+      logits, ld, vocab, cls.token_class, cls.num_classes, ws.lse, ws.zcls, num_states, accept, \
+      eos_id, states, slots, alpha, err)
+  if (vec && z_lds) BPD_PRIOR_OUT(true, true);
+  else if (vec) BPD_PRIOR_OUT(true, false);
+  else if (z_lds) BPD_PRIOR_OUT(false, true);
+  else BPD_PRIOR_OUT(false, false);
+#undef BPD_PRIOR_OUT
+  BPD_LAUNCHED();
+  return BPD_OK;
+}
+
+// Token classes of the prior recurrence (once per grammar, host side).
+// Class c holds the tokens whose tok_next columns are equal once every entry
+// outside [0, S) reads as "rejected"; tokens rejected in every state form no
+// class (token_class -1).  Classes are numbered by their smallest token,
+// members are listed in increasing token order and cut into pieces of at most
+// 256 members; the (class, next) pairs of state s are listed in class order.
+extern "C" int bpd_host_soft_classes(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                                     BpdSoftClasses* out) {
+  BPD_REQUIRE(tok_next && out, "null pointer argument");
+  BPD_REQUIRE(num_states > 0 && vocab > 0 && vocab < (int64_t(1) << 31), "bad table shape");
+  const int32_t S = num_states;
+  const int64_t V = vocab;
+  auto norm = [&](int32_t d) { return (d >= 0 && d < S) ? d : -1; };
+  std::vector<uint64_t> h(size_t(V), 1469598103934665603ull);
+  std::vector<uint8_t> any(size_t(V), 0);
+  for (int32_t s = 0; s < S; ++s) {
+    const int32_t* r = tok_next + int64_t(s) * V;
+    for (int64_t t = 0; t < V; ++t) {
+      const int32_t d = norm(r[t]);
+      h[size_t(t)] = (h[size_t(t)] ^ uint32_t(d)) * 1099511628211ull;
+      any[size_t(t)] |= uint8_t(d >= 0);
+    }
+  }
+  std::unordered_map<uint64_t, std::vector<int32_t>> by_hash;
+  std::vector<int32_t> rep, cls(size_t(V), -1);
+  for (int64_t t = 0; t < V; ++t) {
+    if (!any[size_t(t)]) continue;
+    auto& cands = by_hash[h[size_t(t)]];
+    int32_t found = -1;
+    for (const int32_t c : cands) {
+      const int64_t u = rep[size_t(c)];
+      bool same = true;
+      for (int32_t s = 0; s < S && same; ++s)
+        same = norm(tok_next[int64_t(s) * V + t]) == norm(tok_next[int64_t(s) * V + u]);
+      if (same) {
+        found = c;
+        break;
+      }
+    }
+    if (found < 0) {
+      found = int32_t(rep.size());
+      rep.push_back(int32_t(t));
+      cands.push_back(found);
+    }
+    cls[size_t(t)] = found;
+  }
+  const int64_t C = int64_t(rep.size());
+  std::vector<int64_t> size(size_t(C), 0);
+  for (int64_t t = 0; t < V; ++t)
+    if (cls[size_t(t)] >= 0) ++size[size_t(cls[size_t(t)])];
+  int64_t members = 0, pieces = 0, pairs = 0;
+  for (int64_t c = 0; c < C; ++c) {
+    members += size[size_t(c)];
+    pieces += (size[size_t(c)] + kPieceMembers - 1) / kPieceMembers;
+  }
+  for (int32_t s = 0; s < S; ++s)
+    for (int64_t c = 0; c < C; ++c) pairs += norm(tok_next[int64_t(s) * V + rep[size_t(c)]]) >= 0;
+  BPD_REQUIRE(pairs < (int64_t(1) << 31), "too many (class, next) pairs");
+  const bool fill = out->class_off && out->class_tok && out->class_piece && out->piece_off &&
+                    out->state_off && out->pair_class && out->pair_next && out->token_class;
+  if (fill) {
+    BPD_REQUIRE(out->num_classes == C && out->num_members == members && out->num_pieces == pieces &&
+                    out->num_pairs == pairs,
+                "class buffers were sized for another table (counts differ)");
+  }
+  out->num_classes = int32_t(C);
+  out->num_members = int32_t(members);
+  out->num_pieces = int32_t(pieces);
+  out->num_pairs = int32_t(pairs);
+  if (!fill) return BPD_OK;
+  int64_t m = 0, p = 0;
+  std::vector<int64_t> pos(size_t(C), 0);
+  for (int64_t c = 0; c < C; ++c) {
+    out->class_off[c] = int32_t(m);
+    out->class_piece[c] = int32_t(p);
+    pos[size_t(c)] = m;
+    for (int64_t i = 0; i < size[size_t(c)]; i += kPieceMembers) out->piece_off[p++] = int32_t(m + i);
+    m += size[size_t(c)];
+  }
+  out->class_off[C] = int32_t(m);
+  out->class_piece[C] = int32_t(p);
+  out->piece_off[p] = int32_t(m);
+  for (int64_t t = 0; t < V; ++t) {
+    out->token_class[t] = cls[size_t(t)];
+    if (cls[size_t(t)] >= 0) out->class_tok[pos[size_t(cls[size_t(t)])]++] = int32_t(t);
+  }
+  int64_t q = 0;
+  for (int32_t s = 0; s < S; ++s) {
+    out->state_off[s] = int32_t(q);
+    for (int64_t c = 0; c < C; ++c) {
+      const int32_t d = norm(tok_next[int64_t(s) * V + rep[size_t(c)]]);
+      if (d >= 0) {
+        out->pair_class[q] = int32_t(c);
+        out->pair_next[q] = d;
+        ++q;
+      }
+    }
+  }
+  out->state_off[S] = int32_t(q);
+  return BPD_OK;
+}
+
+// Host form of bpd_soft_prior: direct sums over the vocab, accumulated in
+// double (float32 logits in and out).
+namespace {
+struct LseD {
+  double m, s;
+};
+inline LseD lse_push_d(LseD a, double x) {
+  if (x == -INFINITY) return a;
+  if (x > a.m) {
+    a.s = (a.m == -INFINITY ? 0.0 : a.s * std::exp(a.m - x)) + 1.0;
+    a.m = x;
+  } else {
+    a.s += std::exp(x - a.m);
+  }
+  return a;
+}
+inline double lse_value_d(LseD a) { return a.m == -INFINITY ? -INFINITY : a.m + std::log(a.s); }
+inline double log_add_exp_d(double a, double b) {
+  if (a == b && (a == INFINITY || a == -INFINITY)) return a;
+  return std::fmax(a, b) + std::log1p(std::exp(-std::fabs(a - b)));
+}
+}  // namespace
+
+extern "C" int bpd_host_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld,
+                                   const int32_t* tok_next, int32_t num_states,
+                                   const uint8_t* accept, const uint8_t* live, int32_t eos_id,
+                                   const int32_t* states, const int64_t* slots, int32_t k,
+                                   float alpha) {
+  BPD_REQUIRE(rows >= 0 && vocab > 0 && ld >= vocab, "bad logits shape");
+  BPD_REQUIRE(num_states > 0 && k >= 1 && eos_id < vocab, "bad arguments");
+  const int32_t S = num_states;
+  std::vector<double> cur(static_cast<size_t>(S)), nxt(static_cast<size_t>(S));
+  for (int64_t b = 0; b < rows; ++b) {
+    const int32_t s_b = states[slots ? slots[b] : b];
+    if (s_b >= S) BPD_FAIL(BPD_ERR_INVALID, "index %d is out of bounds for dimension 0 with size %d", s_b, S);
+  }
+  for (int64_t b = 0; b < rows; ++b) {
+    float* row = logits + b * ld;
+    LseD r{-INFINITY, 0.0};
+    for (int64_t t = 0; t < vocab; ++t) r = lse_push_d(r, row[t]);
+    const double lse = lse_value_d(r);
+    const double lp_eos = eos_id >= 0 ? row[eos_id] - lse : -INFINITY;
+    for (int32_t s = 0; s < S; ++s) cur[size_t(s)] = live[s] ? 0.0 : -INFINITY;
+    for (int32_t j = 0; j + 1 < k; ++j) {
+      for (int32_t s = 0; s < S; ++s) {
+        LseD a{-INFINITY, 0.0};
+        const int32_t* tn = tok_next + int64_t(s) * vocab;
+        for (int64_t t = 0; t < vocab; ++t) {
+          const int32_t d = tn[t];
+          if (d >= 0 && d < S && cur[size_t(d)] != -INFINITY) a = lse_push_d(a, row[t] + cur[size_t(d)]);
+        }
+        double v = lse_value_d(a);
+        v = v == -INFINITY ? v : v - lse;
+        if (accept[s]) v = log_add_exp_d(v, lp_eos);
+        nxt[size_t(s)] = live[s] ? v : -INFINITY;
+      }
+      cur.swap(nxt);
+    }
+    const int32_t s_b = states[slots ? slots[b] : b];
+    for (int64_t t = 0; t < vocab; ++t) {
+      if (s_b < 0) {
+        row[t] = -INFINITY;
+        continue;
+      }
+      const double lp = row[t] - lse;
+      double v;
+      if (t == eos_id) {
+        v = accept[s_b] ? lp : -INFINITY;
+      } else {
+        const int32_t d = tok_next[int64_t(s_b) * vocab + t];
+        const double z = (d >= 0 && d < S) ? cur[size_t(d)] : -INFINITY;
+        v = z == -INFINITY ? -INFINITY : (alpha != 0.0f ? lp + double(alpha) * z : lp);
+      }
+      row[t] = float(v);
     }
   }
   return BPD_OK;

@@ -22,6 +22,7 @@ table-builder kernel, which computes ``step`` entry for entry.
 
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass, replace
 
 import torch
@@ -36,6 +37,83 @@ from .tokenizer import Vocabulary
 HAVE_NATIVE = True  # the library is required; loading failures raise at first use
 
 DENSE_AUTO_LIMIT = 32_000_000  # S * V at or below which build() densifies (ops.py:137-139)
+
+
+_SOFT_ARRAYS = ("class_off", "class_tok", "class_piece", "piece_off", "state_off", "pair_class",
+                "pair_next", "token_class")
+
+
+@dataclass
+class SoftClasses:
+    """Tokens grouped by equal ``tok_next`` columns, for the prior-weighted
+    lookahead: class ``c`` is ``class_tok[class_off[c]:class_off[c + 1]]``
+    (cut into pieces of at most 256 members, ``piece_off``, the pieces of
+    ``c`` being ``class_piece[c]:class_piece[c + 1]``); the (class, next
+    state) pairs of state ``s`` are
+    ``pair_class/pair_next[state_off[s]:state_off[s + 1]]``; ``token_class``
+    maps each token to its class (-1: rejected in every state)."""
+
+    class_off: torch.Tensor
+    class_tok: torch.Tensor
+    class_piece: torch.Tensor
+    piece_off: torch.Tensor
+    state_off: torch.Tensor
+    pair_class: torch.Tensor
+    pair_next: torch.Tensor
+    token_class: torch.Tensor
+    num_members: int = 0
+    num_pairs: int = 0
+
+    def __post_init__(self) -> None:
+        self._c: _lib.SoftClassesC | None = None
+        self._ws: dict = {}
+
+    @property
+    def num_classes(self) -> int:
+        return int(self.class_off.numel() - 1)
+
+    @property
+    def num_pieces(self) -> int:
+        return int(self.piece_off.numel() - 1)
+
+    def to(self, device) -> SoftClasses:
+        return SoftClasses(*(getattr(self, n).to(device) for n in _SOFT_ARRAYS),
+                           num_members=self.num_members, num_pairs=self.num_pairs)
+
+    def c_struct(self) -> _lib.SoftClassesC:
+        if self._c is None:
+            self._c = _lib.SoftClassesC(self.num_classes, self.num_members, self.num_pieces,
+                                        self.num_pairs, *(ptr(getattr(self, n)) for n in _SOFT_ARRAYS))
+        return self._c
+
+    def workspace(self, rows: int, device: torch.device, stream: int) -> tuple[torch.Tensor, int]:
+        """Workspace for ``rows`` rows, kept per stream so a step allocates
+        nothing once it has run at this size."""
+        vocab = int(self.token_class.numel())
+        need = int(lib().bpd_soft_prior_workspace_bytes(rows, vocab, self.num_classes, self.num_pieces))
+        key = (device, stream)
+        ws = self._ws.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+            self._ws[key] = ws
+        return ws, need
+
+    @classmethod
+    def build(cls, tok_next: torch.Tensor) -> SoftClasses:
+        tn = tok_next.to("cpu", torch.int32).contiguous()
+        S, V = tn.shape
+        c = _lib.SoftClassesC()
+        check(lib().bpd_host_soft_classes(ptr(tn), S, V, C.byref(c)))
+        sizes = {"class_off": c.num_classes + 1, "class_tok": c.num_members,
+                 "class_piece": c.num_classes + 1, "piece_off": c.num_pieces + 1,
+                 "state_off": S + 1, "pair_class": c.num_pairs, "pair_next": c.num_pairs,
+                 "token_class": V}
+        arrays = {n: torch.empty(max(k, 1), dtype=torch.int32) for n, k in sizes.items()}
+        for n in _SOFT_ARRAYS:
+            setattr(c, n, ptr(arrays[n]))
+        check(lib().bpd_host_soft_classes(ptr(tn), S, V, C.byref(c)))
+        return cls(*(arrays[n][:sizes[n]] for n in _SOFT_ARRAYS), num_members=c.num_members,
+                   num_pairs=c.num_pairs)
 
 
 @dataclass
@@ -57,6 +135,8 @@ class FsaTensors:
     # packed allow bits derived from tok_next: int32 [num_states, ceil(vocab/32)],
     # bit t of row s set iff tok_next[s, t] != -1 (the device mask reads these)
     allow_bits: torch.Tensor | None = None
+    # token classes of the prior-weighted lookahead (built once from tok_next)
+    soft_classes: SoftClasses | None = None
 
     @property
     def device(self) -> torch.device:
@@ -78,6 +158,7 @@ class FsaTensors:
             mv(self.trans), mv(self.accept), mv(self.live), self.num_symbols, self.dead,
             mv(self.offsets), mv(self.symbols), self.eos_id, self.start, self.accepting,
             mv(self.tok_next), mv(self.lookahead), mv(self.allow_bits),
+            None if self.soft_classes is None else self.soft_classes.to(device),
         )
 
     def densify(self) -> FsaTensors:
@@ -94,6 +175,15 @@ class FsaTensors:
             self.tok_next = base.tok_next
             self.allow_bits = dense_compute_mask(base.tok_next, st)
         return self.allow_bits
+
+    def ensure_soft_classes(self) -> SoftClasses:
+        """Token classes of the prior-weighted lookahead (built once on the
+        host from tok_next and kept on this bundle, like the allow bits)."""
+        if self.soft_classes is None:
+            base = self.densify()
+            self.tok_next = base.tok_next
+            self.soft_classes = SoftClasses.build(base.tok_next).to(self.device)
+        return self.soft_classes
 
     def with_lookahead(self, k: int = 3) -> FsaTensors:
         base = self.densify()
@@ -361,6 +451,52 @@ def soft_apply_(logits, lookahead, states, slots=None, alpha: float = 1.0):
     else:
         check(lib().bpd_host_soft_apply(ptr(work), code, B, V, ld, ptr(la), S, ptr(st), ptr(sl),
                                         float(alpha)))
+    if copied:
+        logits.copy_(work)
+    return logits
+
+
+def apply_soft_prior_(logits: torch.Tensor, fsa: FsaTensors, states: torch.Tensor, k: int = 4,
+                      alpha: float = 1.0, slots: torch.Tensor | None = None, err=None):
+    """In place, float32 ``logits`` [B, vocab]: the prior-weighted soft
+    lookahead.  ``logpi = log_softmax(logits)`` per row; k-1 rounds of
+    ``logZ(s) = logsumexp_t [logpi(t) + logZ(tok_next[s, t])]`` (``⊕ logpi(eos)``
+    for accepting ``s``, ``-inf`` off the live set) from ``logZ = 0`` on live
+    states; then ``logpi(t) + alpha * logZ(tok_next[s_b, t])`` on allowed
+    tokens, ``logpi(eos)`` in the EOS column of accepting rows and ``-inf``
+    elsewhere.  ``logpi == 0`` gives the uniform recurrence of
+    build_lookahead (ops.py:200-236)."""
+    if logits.dtype != torch.float32:
+        raise TypeError("the prior-weighted lookahead takes float32 logits")
+    if k < 1:
+        raise ValueError("k must be >= 1")
+    base = fsa if fsa.tok_next is not None else fsa.densify()
+    tn = base.tok_next.contiguous()
+    dev = _same_device(logits, tn, states, slots)
+    work, copied = _unit_stride_rows(logits)
+    B, V = work.shape
+    S, TV = tn.shape
+    if TV != V:
+        raise RuntimeError(f"logits have {V} columns but tok_next has {TV}")
+    if slots is not None and slots.numel() != B:
+        raise RuntimeError("one slot per logits row")
+    st = _i32(states)
+    if slots is None and st.numel() != B:
+        raise RuntimeError(f"one state per logits row (got {st.numel()} states for {B} rows)")
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    acc, live = base.accept.contiguous(), base.live.contiguous()
+    eos = base.eos_id if base.eos_id is not None and 0 <= base.eos_id < V else -1
+    ld = work.stride(0) if B > 1 else V
+    if dev.type == "cuda":
+        sc = base.ensure_soft_classes()
+        stream = _lib.stream_of(dev)
+        ws, ws_bytes = sc.workspace(B, dev, stream)
+        check(lib().bpd_soft_prior(ptr(work), B, V, ld, S, ptr(acc), ptr(live), eos, ptr(st),
+                                   ptr(sl), C.byref(sc.c_struct()), int(k), float(alpha), ptr(ws),
+                                   ws_bytes, ptr(err), stream))
+    else:
+        check(lib().bpd_host_soft_prior(ptr(work), B, V, ld, ptr(tn), S, ptr(acc), ptr(live), eos,
+                                        ptr(st), ptr(sl), int(k), float(alpha)))
     if copied:
         logits.copy_(work)
     return logits

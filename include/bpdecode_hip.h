@@ -237,6 +237,60 @@ int bpd_host_soft_apply(void* logits, int dtype, int64_t rows, int64_t vocab, in
                         const float* lookahead, int32_t num_states, const int32_t* states,
                         const int64_t* slots, float alpha);
 
+/* --------------------------------------------------- prior-weighted soft --
+ * The reference's build_lookahead (ops.py:200-236) counts continuations
+ * uniformly; this variant weights them by each row's own model prior
+ * logpi_b = log_softmax(logits_b) and replaces the float32 logits in place:
+ *   logZ_0(s) = 0 on live s; k-1 rounds of
+ *   logZ(s) = logsumexp_t [logpi_b(t) + logZ(tok_next[s, t])]
+ *             (logaddexp with logpi_b(eos) for accepting s), -inf off live;
+ *   out[b, t] = logpi_b(t) + alpha * logZ(tok_next[s_b, t]) on allowed t,
+ *   logpi_b(eos) / -inf in the EOS column for accepting / other s_b, -inf on
+ *   every other entry and on rows with s_b < 0.
+ * With logpi == 0 the rounds are the reference's uniform ones.  The reference
+ * has no such kernel: its model-weighted scoring (lookahead.py:57-70,
+ * logit + alpha * log P(valid continuation)) takes a forward pass per
+ * candidate instead of the current row's prior.
+ *
+ * bpd_host_soft_classes groups tokens with equal tok_next columns (once per
+ * grammar, host memory): class c is class_tok[class_off[c] .. class_off[c+1]),
+ * cut into pieces piece_off[p] .. piece_off[p+1] of at most 256 members, its
+ * pieces being class_piece[c] .. class_piece[c+1]; the (class, next state)
+ * pairs of state s are pair_class / pair_next[state_off[s] .. state_off[s+1]);
+ * token_class[t] is t's class, -1 for tokens rejected in every state.  Called
+ * with any array null it only sets the counts; called again with arrays of
+ * those sizes (counts left in place) it fills them.
+ *
+ * bpd_soft_prior takes the same struct with the arrays copied to the device.
+ * Workspace: bpd_soft_prior_workspace_bytes(rows, vocab, num_classes, num_pieces)
+ * bytes (no initial contents needed; calls that overlap on one workspace race).
+ */
+typedef struct BpdSoftClasses {
+  int32_t num_classes, num_members, num_pieces, num_pairs;
+  int32_t* class_off;   /* [num_classes + 1] */
+  int32_t* class_tok;   /* [num_members] */
+  int32_t* class_piece; /* [num_classes + 1] */
+  int32_t* piece_off;   /* [num_pieces + 1] */
+  int32_t* state_off;   /* [num_states + 1] */
+  int32_t* pair_class;  /* [num_pairs] */
+  int32_t* pair_next;   /* [num_pairs] */
+  int32_t* token_class; /* [vocab] */
+} BpdSoftClasses;
+
+int bpd_host_soft_classes(const int32_t* tok_next, int32_t num_states, int64_t vocab,
+                          BpdSoftClasses* out);
+size_t bpd_soft_prior_workspace_bytes(int64_t rows, int64_t vocab, int32_t num_classes,
+                                      int32_t num_pieces);
+int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld, int32_t num_states,
+                   const uint8_t* accept, const uint8_t* live, int32_t eos_id,
+                   const int32_t* states, const int64_t* slots, const BpdSoftClasses* classes,
+                   int32_t k, float alpha, void* workspace, size_t workspace_bytes, int32_t* err,
+                   void* stream);
+int bpd_host_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld,
+                        const int32_t* tok_next, int32_t num_states, const uint8_t* accept,
+                        const uint8_t* live, int32_t eos_id, const int32_t* states,
+                        const int64_t* slots, int32_t k, float alpha);
+
 #ifdef __cplusplus
 }
 #endif

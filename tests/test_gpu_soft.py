@@ -66,3 +66,116 @@ def test_apply_soft(dev, dtype, alpha):
         assert np.array_equal(np.isneginf(g), np.isneginf(want))
         fin = np.isfinite(want)
         assert np.all(np.abs(g[fin] - want[fin]) <= 1e-2 * np.abs(want[fin]) + 1e-2)
+
+
+# ------------------------------------------------------- prior-weighted --
+@pytest.mark.parametrize("pattern", TOY_PATTERNS)
+@pytest.mark.parametrize("k", [1, 2, 4])
+@pytest.mark.parametrize("alpha", [0.0, 1.0, -0.5])
+def test_prior_toy(dev, pattern, k, alpha):
+    fsa = FsaTensors.build(pattern, TOY_VOCAB).densify()
+    S, V = fsa.tok_next.shape
+    st = torch.tensor(list(range(S)) + [-1, 0], dtype=torch.int32)
+    g = torch.Generator().manual_seed(k * 13 + len(pattern))
+    x = torch.randn(len(st), V, generator=g) * 3
+    got = x.to(dev)
+    ops.apply_soft_prior_(got, fsa.to(dev), st.to(dev), k, alpha)
+    want = OS.prior_lookahead(x.double().numpy(), fsa.tok_next.numpy(), fsa.live.numpy(),
+                              fsa.accept.numpy(), fsa.eos_id, st.numpy(), k, alpha)
+    assert close(got.cpu().double().numpy(), want)
+
+
+def test_prior_batch_slots_and_errors(dev):
+    fsa = FsaTensors.build("a[012]+|b0", TOY_VOCAB).densify().to(dev)
+    S, V = fsa.tok_next.shape
+    batch = ConstraintBatch(fsa, capacity=8, device=dev)
+    for i in range(6):
+        batch.add(i)
+    pool = torch.tensor([0, 1, 2, -1, 0, 2, -2, -2], dtype=torch.int32)
+    batch._state[:] = pool.to(dev)
+    ids = [4, 2, 0, 3, 1]
+    x = torch.randn(5, V) * 3
+    got = x.to(dev)
+    batch.apply_soft_prior(ids, got, k=3, alpha=0.5)
+    want = OS.prior_lookahead(x.double().numpy(), fsa.tok_next.cpu().numpy(), fsa.live.cpu().numpy(),
+                              fsa.accept.cpu().numpy(), fsa.eos_id, pool[ids].numpy(), 3, 0.5)
+    assert close(got.cpu().double().numpy(), want)
+    batch.check_errors()
+    batch._state[0] = S  # out-of-range state: -inf row and the device error flag
+    got = x.to(dev)
+    batch.apply_soft_prior([0], got[:1], k=3, alpha=0.5)
+    assert torch.isneginf(got[0]).all()
+    with pytest.raises(IndexError):
+        batch.check_errors()
+
+
+def test_prior_unaligned_vocab(dev):
+    # V = 17 (not a multiple of 4) and a strided row view take the scalar kernels
+    fsa = FsaTensors.build("[a-c]*", TOY_VOCAB).densify()
+    S, V = fsa.tok_next.shape
+    wide = torch.randn(4, V + 3) * 3
+    st = torch.tensor([0, 0, -1, 0], dtype=torch.int32)
+    want = OS.prior_lookahead(wide[:, :V].double().numpy(), fsa.tok_next.numpy(), fsa.live.numpy(),
+                              fsa.accept.numpy(), fsa.eos_id, st.numpy(), 4, 1.0)
+    w = wide.to(dev)
+    ops.apply_soft_prior_(w[:, :V], fsa.to(dev), st.to(dev), 4, 1.0)
+    assert close(w[:, :V].cpu().double().numpy(), want)
+    assert torch.equal(w[:, V:].cpu(), wide[:, V:])
+
+
+def test_prior_email_serving(dev):
+    """B=128, V=151,936, k=4 over the email DFA: four rows against the
+    oracle, every row against the alpha-free identity (alpha = 0 leaves
+    log_softmax on tokens whose k-1 lookahead is finite)."""
+    vocab = synth.serving_vocab(151_936, seed=1)
+    fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
+    tn = fsa.tok_next.numpy()
+    S, V = tn.shape
+    st = synth.random_walk_states(fsa.tok_next, fsa.start, fsa.eos_id, 128, 40, seed=5).to(torch.int32)
+    x = synth.logits(128, V, std=3.0, dtype=torch.float32, seed=11)
+    fd = fsa.to(dev)
+    got = x.to(dev)
+    ops.apply_soft_prior_(got, fd, st.to(dev), 4, 1.0)
+    got = got.cpu().double().numpy()
+    rows = list(range(0, 128, 32))
+    want = OS.prior_lookahead(x[rows].double().numpy(), tn, fsa.live.numpy(), fsa.accept.numpy(),
+                              fsa.eos_id, st[rows].numpy(), 4, 1.0)
+    assert close(got[rows], want)
+    zero = x.to(dev)
+    ops.apply_soft_prior_(zero, fd, st.to(dev), 4, 0.0)
+    ls = torch.log_softmax(x.double(), dim=1).numpy()
+    fin = np.isfinite(got)
+    assert np.array_equal(np.isfinite(zero.cpu().numpy()), fin)
+    z = zero.cpu().double().numpy()
+    assert np.all(np.abs(z[fin] - ls[fin]) <= RTOL * np.abs(ls[fin]) + ATOL)
+
+
+@pytest.mark.parametrize("pattern", ["a[012]+|b0", "[a-c]*"])
+def test_prior_pieces_path(dev, pattern, monkeypatch):
+    """The gather-over-class-pieces statistics (taken above 1024 token
+    classes; forced here) give the same results."""
+    monkeypatch.setenv("BPD_SOFT_PRIOR_PIECES", "1")
+    fsa = FsaTensors.build(pattern, TOY_VOCAB).densify()
+    S, V = fsa.tok_next.shape
+    st = torch.tensor(list(range(S)) + [-1], dtype=torch.int32)
+    x = torch.randn(len(st), V) * 3
+    got = x.to(dev)
+    ops.apply_soft_prior_(got, fsa.to(dev), st.to(dev), 4, 0.7)
+    want = OS.prior_lookahead(x.double().numpy(), fsa.tok_next.numpy(), fsa.live.numpy(),
+                              fsa.accept.numpy(), fsa.eos_id, st.numpy(), 4, 0.7)
+    assert close(got.cpu().double().numpy(), want)
+
+
+def test_prior_pieces_path_email(dev, monkeypatch):
+    vocab = synth.serving_vocab(151_936, seed=1)
+    fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
+    st = synth.random_walk_states(fsa.tok_next, fsa.start, fsa.eos_id, 16, 40, seed=9).to(torch.int32)
+    x = synth.logits(16, 151_936, std=3.0, dtype=torch.float32, seed=12)
+    fd = fsa.to(dev)
+    a = x.to(dev)
+    ops.apply_soft_prior_(a, fd, st.to(dev), 4, 1.0)
+    monkeypatch.setenv("BPD_SOFT_PRIOR_PIECES", "1")
+    b = x.to(dev)
+    ops.apply_soft_prior_(b, fd, st.to(dev), 4, 1.0)
+    a, b = a.cpu().double().numpy(), b.cpu().double().numpy()
+    assert close(b, a)
