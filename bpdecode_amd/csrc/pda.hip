@@ -14,6 +14,7 @@
 // walk starts from the row's set in global memory and every byte step writes
 // a freshly cleared set, so the 266 words written back on acceptance are
 // exactly those the reference produces.
+#include <cstdlib>
 #include <vector>
 
 #include "bpd_common.hpp"
@@ -43,6 +44,7 @@ struct MaskArgs {
   int64_t words;
   int32_t chunk_tokens;  // multiple of 64
   int32_t* err;
+  const int32_t* only_rows;  // non-null: process only rows b with only_rows[b] != 0
 };
 
 // Structural check of a row's config-set before any table lookup with its
@@ -74,6 +76,7 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
 
   const int64_t b = blockIdx.y;
   const int lane = threadIdx.x;
+  if (a.only_rows && a.only_rows[b] == 0) return;
   const int64_t row = a.slots ? a.slots[b] : b;
   for (int k = lane; k < kConfigWords; k += kWave) row_cfg[k] = a.configs[row * kConfigWords + k];
   __syncthreads();
@@ -148,6 +151,269 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
       }
     }
   }
+}
+
+// ------------------------------------------------------- memoised mask --
+// One workgroup per row.  A token's verdict depends only on the config-sets
+// its bytes walk through, and advance_byte is a pure function of a set's
+// meaningful words (n, saturated, depths, frames below each depth).  The
+// workgroup therefore interns the sets it meets (pool, global workspace) and
+// fills a transition table T[set][byte] in LDS on demand: threads walk their
+// tokens through T; a missing entry pauses the token and is requested; the
+// requests of a round are computed in parallel (one thread each, the set
+// being built in a workspace slot), de-duplicated against the pool and among
+// themselves, and entered in T; then the walks resume.  Every entry is
+// computed by the same advance_byte as the direct walk, so verdicts are
+// identical.  A row that needs more than kMemoSets distinct sets marks the
+// missing entries "overflow", leaves those tokens untouched and is finished
+// by the direct-walk kernel (pda_mask_kernel filtered to flagged rows).
+constexpr int kMemoThreads = 1024;
+constexpr int kMemoSets = 128;
+constexpr int kMemoReq = 256;
+constexpr int kMemoTok = 4;
+constexpr uint8_t kTUnknown = 0xFE;
+constexpr uint8_t kTDead = 0xFF;
+constexpr uint8_t kTOverflow = 0xFD;
+
+struct MemoWs {
+  int32_t* pool;      // [rows, kMemoSets, kConfigWords]
+  int32_t* cand;      // [rows, kMemoReq, kConfigWords]
+  int32_t* overflow;  // [rows]
+};
+
+size_t memo_ws_bytes(int64_t rows) {
+  const size_t r = size_t(rows > 0 ? rows : 0);
+  const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
+  return sets + (r * sizeof(int32_t) + 255) / 256 * 256;
+}
+
+MemoWs memo_ws(void* base, int64_t rows) {
+  MemoWs w;
+  w.pool = static_cast<int32_t*>(base);
+  w.cand = w.pool + size_t(rows) * kMemoSets * kConfigWords;
+  w.overflow = w.cand + size_t(rows) * kMemoReq * kConfigWords;
+  return w;
+}
+
+// FNV-1a over a set's meaningful words.
+template <class V>
+__device__ uint32_t set_hash(const V& c) {
+  uint32_t h = 2166136261u;
+  auto mix = [&](uint32_t x) { h = (h ^ x) * 16777619u; };
+  const int n = c.n();
+  mix(uint32_t(n));
+  mix(uint32_t(c.sat()));
+  for (int i = 0; i < n; ++i) {
+    const int d = c.depth(i);
+    mix(uint32_t(d));
+    for (int k = 0; k < d; ++k) mix(uint32_t(c.frame(i, k)));
+  }
+  return h;
+}
+
+template <class A, class B>
+__device__ bool same_set(const A& x, const B& y) {
+  const int n = x.n();
+  if (n != y.n() || x.sat() != y.sat()) return false;
+  for (int i = 0; i < n; ++i) {
+    const int d = x.depth(i);
+    if (d != y.depth(i)) return false;
+    for (int k = 0; k < d; ++k)
+      if (x.frame(i, k) != y.frame(i, k)) return false;
+  }
+  return true;
+}
+
+__global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets) {
+  __shared__ uint32_t T32[kMemoSets * 256 / 4];
+  __shared__ uint32_t req[kMemoSets * 8];
+  __shared__ uint32_t pool_hash[kMemoSets];
+  __shared__ int32_t req_list[kMemoReq];
+  __shared__ uint32_t cand_hash[kMemoReq];
+  __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new
+  __shared__ int32_t cand_lead[kMemoReq];
+  __shared__ int32_t cand_id[kMemoReq];
+  __shared__ int32_t row_cfg[kConfigWords];
+  __shared__ int pool_count, nreq, row_flags, overflowed;
+  uint8_t* T = reinterpret_cast<uint8_t*>(T32);
+
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t row = a.slots ? a.slots[b] : b;
+  int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
+  int32_t* cand = ws.cand + b * kMemoReq * kConfigWords;
+
+  for (int k = tid; k < kConfigWords; k += kMemoThreads) row_cfg[k] = a.configs[row * kConfigWords + k];
+  for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
+  for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0;
+  if (tid == 0) {
+    pool_count = 1;
+    overflowed = 0;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    bool dead = a.broken != nullptr && a.broken[row] != 0;
+    if (!config_ok(row_cfg, a.g.num_states, tid)) {
+      if (tid == 0 && a.err) atomicOr(a.err, BPD_FLAG_STATE_RANGE);
+      dead = true;
+    }
+    if (tid == 0) {
+      const ConstFlatView C{row_cfg};
+      row_flags = dead ? 1 : ((is_complete(a.g, C) ? 2 : 0) | (C.n() > 0 ? 4 : 0));
+      pool_hash[0] = dead ? 0u : set_hash(C);
+    }
+  }
+  for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
+  __syncthreads();
+  const int flags = row_flags;
+  const bool dead_row = (flags & 1) != 0;
+
+  const int64_t V = a.vocab;
+  for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
+    int32_t pos[kMemoTok], end[kMemoTok];
+    int cur[kMemoTok], st[kMemoTok];  // st: 0 walking, 1 allowed, 2 rejected, 3 overflow, 4 none
+#pragma unroll
+    for (int j = 0; j < kMemoTok; ++j) {
+      const int64_t t = tile + int64_t(j) * kMemoThreads + tid;
+      pos[j] = end[j] = 0;
+      cur[j] = 0;
+      if (t >= V) {
+        st[j] = 4;
+      } else if (dead_row) {
+        st[j] = 2;
+      } else if (t == a.eos) {
+        st[j] = (flags & 2) ? 1 : 2;
+      } else {
+        pos[j] = a.tok_off[t];
+        end[j] = a.tok_off[t + 1];
+        st[j] = pos[j] == end[j] ? ((flags & 4) ? 1 : 2) : 0;
+      }
+    }
+    while (true) {
+      bool waiting = false;
+#pragma unroll
+      for (int j = 0; j < kMemoTok; ++j) {
+        while (st[j] == 0) {
+          if (pos[j] == end[j]) {
+            st[j] = 1;
+            break;
+          }
+          const int byte = a.tok_bytes[pos[j]];
+          const uint8_t nx = T[cur[j] * 256 + byte];
+          if (nx == kTUnknown) {
+            atomicOr(&req[cur[j] * 8 + (byte >> 5)], 1u << (byte & 31));
+            waiting = true;
+            break;
+          }
+          if (nx == kTDead) {
+            st[j] = 2;
+          } else if (nx == kTOverflow) {
+            st[j] = 3;
+          } else {
+            cur[j] = nx;
+            ++pos[j];
+          }
+        }
+      }
+      if (!__syncthreads_or(waiting)) break;
+
+      // resolve the requested transitions
+      if (tid == 0) nreq = 0;
+      __syncthreads();
+      for (int w = tid; w < kMemoSets * 8; w += kMemoThreads) {
+        uint32_t bits = req[w];
+        if (bits) {
+          req[w] = 0;
+          int at = atomicAdd(&nreq, __popc(bits));
+          while (bits) {
+            const int bit = __ffs(bits) - 1;
+            bits &= bits - 1;
+            if (at < kMemoReq) req_list[at] = ((w >> 3) << 8) | ((w & 7) * 32 + bit);
+            ++at;
+          }
+        }
+      }
+      __syncthreads();
+      const int n = nreq < kMemoReq ? nreq : kMemoReq;
+      if (tid < n) {
+        const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
+        FlatView dst{cand + tid * kConfigWords};
+        dst.reset_all();
+        if (!advance_byte(a.g, ConstFlatView{pool + set * kConfigWords}, dst, byte)) {
+          cand_res[tid] = -1;
+        } else {
+          const uint32_t h = set_hash(dst);
+          cand_hash[tid] = h;
+          int found = -2;
+          const int pc = pool_count < max_sets ? pool_count : max_sets;
+          for (int k = 0; k < pc && found < 0; ++k)
+            if (pool_hash[k] == h && same_set(ConstFlatView{pool + k * kConfigWords}, dst)) found = k;
+          cand_res[tid] = found;
+        }
+      }
+      __syncthreads();
+      if (tid < n && cand_res[tid] == -2) {
+        const ConstFlatView mine{cand + tid * kConfigWords};
+        int lead = tid;
+        for (int j = 0; j < tid && lead == tid; ++j)
+          if (cand_res[j] == -2 && cand_hash[j] == cand_hash[tid] &&
+              same_set(ConstFlatView{cand + j * kConfigWords}, mine))
+            lead = j;
+        cand_lead[tid] = lead;
+        if (lead == tid) {
+          const int id = atomicAdd(&pool_count, 1);
+          if (id < max_sets) {
+            for (int k = 0; k < kConfigWords; ++k) pool[id * kConfigWords + k] = mine.w[k];
+            pool_hash[id] = cand_hash[tid];
+            cand_id[tid] = id;
+          } else {
+            cand_id[tid] = -3;
+          }
+        }
+      }
+      __syncthreads();
+      if (tid < n) {
+        const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
+        const int r = cand_res[tid];
+        const int id = r == -2 ? cand_id[cand_lead[tid]] : r;
+        uint8_t e;
+        if (id == -1) {
+          e = kTDead;
+        } else if (id == -3) {
+          e = kTOverflow;
+          overflowed = 1;
+        } else {
+          e = uint8_t(id);
+        }
+        T[set * 256 + byte] = e;
+      }
+      __syncthreads();
+    }
+
+    // verdicts of the tile; overflow tokens are left to the direct walk
+#pragma unroll
+    for (int j = 0; j < kMemoTok; ++j) {
+      const int64_t t = tile + int64_t(j) * kMemoThreads + tid;
+      if (a.logits) {
+        if (st[j] == 2) {
+          uint8_t* p = a.logits + b * a.ld_bytes + t * a.elem;
+          if (a.elem == 2)
+            *reinterpret_cast<uint16_t*>(p) = uint16_t(a.fill);
+          else
+            *reinterpret_cast<uint32_t*>(p) = a.fill;
+        }
+      } else {
+        const uint64_t m = __ballot(st[j] == 1);
+        if ((tid & 63) == 0) {
+          const int64_t w0 = (tile + int64_t(j) * kMemoThreads + tid) >> 5;
+          if (w0 < a.words) a.bits[b * a.words + w0] = uint32_t(m);
+          if (w0 + 1 < a.words) a.bits[b * a.words + w0 + 1] = uint32_t(m >> 32);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) ws.overflow[b] = overflowed;
 }
 
 struct AdvanceArgs {
@@ -274,9 +540,8 @@ bool host_config_ok(const int32_t* c, int32_t num_states) {
 using namespace bpd;
 
 extern "C" size_t bpd_pda_workspace_bytes(int64_t rows, int32_t vocab) {
-  (void)rows;
   (void)vocab;
-  return 0;
+  return memo_ws_bytes(rows);
 }
 
 extern "C" int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data,
@@ -310,7 +575,7 @@ extern "C" int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out) {
 static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, const int32_t* configs,
                            const int64_t* slots, const uint8_t* broken, int64_t rows,
                            void* logits, int dtype, int64_t ld, double neg_inf, uint32_t* bits,
-                           void* stream) {
+                           void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_tables(g, toks)) return rc;
   BPD_REQUIRE(rows >= 0 && rows < 65536, "rows must lie in [0, 65535]");
   MaskArgs a{};
@@ -346,6 +611,21 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
   chunks = (int64_t(toks->vocab_size) + per - 1) / per;
   a.chunk_tokens = int32_t(per);
   a.err = nullptr;
+  a.only_rows = nullptr;
+  if (workspace) {
+    BPD_REQUIRE(workspace_bytes >= memo_ws_bytes(rows), "workspace too small (%zu < %zu bytes)",
+                workspace_bytes, memo_ws_bytes(rows));
+    const MemoWs ws = memo_ws(workspace, rows);
+    // BPD_PDA_MEMO_SETS lowers the interned-set limit (tests of the overflow path)
+    int max_sets = kMemoSets;
+    if (const char* e = std::getenv("BPD_PDA_MEMO_SETS")) {
+      const int v = std::atoi(e);
+      if (v >= 1 && v < kMemoSets) max_sets = v;
+    }
+    pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, 0, as_stream(stream)>>>(a, ws, max_sets);
+    BPD_LAUNCHED();
+    a.only_rows = ws.overflow;  // rows that ran out of interned sets
+  }
   pda_mask_kernel<<<dim3(unsigned(chunks), unsigned(rows)), dim3(kWave), 0, as_stream(stream)>>>(a);
   BPD_LAUNCHED();
   return BPD_OK;
@@ -356,22 +636,18 @@ extern "C" int bpd_pda_apply_mask(const BpdPdaTable* g, const BpdTokenBytes* tok
                                   const uint8_t* broken, int64_t rows, void* logits, int dtype,
                                   int64_t ld, double neg_inf, void* workspace,
                                   size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   BPD_REQUIRE(logits || rows == 0, "null logits");
   return launch_pda_mask(g, toks, configs, slots, broken, rows, logits, dtype, ld, neg_inf,
-                         nullptr, stream);
+                         nullptr, workspace, workspace_bytes, stream);
 }
 
 extern "C" int bpd_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
                                     const int32_t* configs, const int64_t* slots, int64_t rows,
                                     uint32_t* bits, void* workspace, size_t workspace_bytes,
                                     void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   BPD_REQUIRE(bits || rows == 0, "null bits");
   return launch_pda_mask(g, toks, configs, slots, nullptr, rows, nullptr, 0, 0, 0.0, bits,
-                         stream);
+                         workspace, workspace_bytes, stream);
 }
 
 extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,

@@ -106,6 +106,18 @@ class PdaTensors:
             self._c["table_keep"] = keep
         return t
 
+    def mask_workspace(self, rows: int, device: torch.device, stream: int) -> tuple[torch.Tensor, int]:
+        """Workspace of the memoised device mask (interned config-sets and
+        transition scratch per row), kept per stream so a step allocates
+        nothing once it has run at this size."""
+        need = int(lib().bpd_pda_workspace_bytes(rows, self.vocab_size))
+        key = ("ws", device, stream)
+        ws = self._c.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+            self._c[key] = ws
+        return ws, need
+
     def c_tokens(self) -> _lib.TokenBytesC:
         t = self._c.get("tokens")
         if t is None:
@@ -281,9 +293,11 @@ def pda_mask_(logits, g: PdaTensors, configs, slots=None, broken=None, neg_inf=f
     code = _lib.dtype_code(work.dtype)
     ld = work.stride(0) if B > 1 else V
     if dev.type == "cuda":
+        stream = _lib.stream_of(dev)
+        ws, ws_bytes = g.mask_workspace(B, dev, stream)
         check(lib().bpd_pda_apply_mask(g.c_table(), g.c_tokens(), ptr(configs), ptr(sl), ptr(br), B,
-                                       ptr(work), code, ld, float(neg_inf), None, 0,
-                                       _lib.stream_of(dev)))
+                                       ptr(work), code, ld, float(neg_inf), ptr(ws), ws_bytes,
+                                       stream))
     else:
         check(lib().bpd_host_pda_apply_mask(g.c_table(), g.c_tokens(), ptr(configs), ptr(sl),
                                             ptr(br), B, ptr(work), code, ld, float(neg_inf)))
@@ -305,8 +319,10 @@ def pda_compute_mask(g: PdaTensors, configs, slots=None) -> torch.Tensor:
     B = configs.size(0) if sl is None else sl.numel()
     out = torch.empty((B, (g.vocab_size + 31) // 32), dtype=torch.int32, device=dev)
     if dev.type == "cuda":
+        stream = _lib.stream_of(dev)
+        ws, ws_bytes = g.mask_workspace(B, dev, stream)
         check(lib().bpd_pda_compute_mask(g.c_table(), g.c_tokens(), ptr(configs), ptr(sl), B,
-                                         ptr(out), None, 0, _lib.stream_of(dev)))
+                                         ptr(out), ptr(ws), ws_bytes, stream))
     else:
         check(lib().bpd_host_pda_compute_mask(g.c_table(), g.c_tokens(), ptr(configs), ptr(sl), B,
                                               ptr(out)))

@@ -137,3 +137,42 @@ def test_json_batch_api_b64(dev, json_case):
         OP.advance(t, mirror, toks)
         assert status.cpu().tolist() == [1] * 64
         assert np.array_equal(batch._configs.cpu().numpy(), mirror)
+
+
+@pytest.mark.parametrize("limit", ["1", "3"])
+def test_json_memo_overflow_rows_match_oracle(dev, json_case, monkeypatch, limit):
+    """With the interned-set limit lowered, rows run out of sets and are
+    finished by the direct-walk kernel; masks stay identical."""
+    vocab, g, t = json_case
+    _log(f"case json V=151936 B=8 memo set limit {limit}")
+    monkeypatch.setenv("BPD_PDA_MEMO_SETS", limit)
+    cfgs = _json_configs(g, 8, seed=21)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    bits = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+    assert np.array_equal(bits, OP.compute_mask(t, cfgs.numpy()))
+    lg = synth.logits(8, vocab.size, 3.0, torch.bfloat16, seed=5)
+    got = lg.to(dev)
+    pda_mask_(got, gd, pool)
+    ref = lg.float().numpy().copy()
+    OP.apply_mask(t, cfgs.numpy().copy(), ref)
+    assert np.array_equal(got.float().cpu().numpy(), ref)
+
+
+def test_json_direct_walk_equals_memo(dev, json_case):
+    """The C ABI without a workspace runs the direct per-token walk; with one,
+    the memoised kernel: identical bits."""
+    from bpdecode_amd import _lib
+    from bpdecode_amd._lib import check, lib, ptr
+
+    vocab, g, t = json_case
+    _log("case json V=151936 B=16 direct vs memo")
+    cfgs = _json_configs(g, 16, seed=33)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    words = (vocab.size + 31) // 32
+    direct = torch.empty((16, words), dtype=torch.int32, device=dev)
+    check(lib().bpd_pda_compute_mask(gd.c_table(), gd.c_tokens(), ptr(pool), None, 16, ptr(direct),
+                                     None, 0, _lib.stream_of(dev)))
+    memo = pda_compute_mask(gd, pool)
+    assert torch.equal(direct.cpu(), memo.cpu())
