@@ -233,6 +233,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new
   __shared__ int32_t cand_lead[kMemoReq];
   __shared__ int32_t cand_id[kMemoReq];
+  __shared__ int16_t cand_lo[kMemoReq];
+  __shared__ int16_t cand_hi[kMemoReq];
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ int pool_count, nreq, row_flags, overflowed;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
@@ -336,6 +338,32 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       __syncthreads();
       const int n = nreq < kMemoReq ? nreq : kMemoReq;
       if (tid < n) {
+        // advance_byte(set, c) depends on c only through which byte edges of
+        // the set's top states contain c, so every byte of the elementary
+        // interval [lo, hi] around the request shares its result: the first
+        // request of an interval computes it and fills the whole interval
+        const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
+        const ConstFlatView src{pool + set * kConfigWords};
+        int lo = 0, hi = 255;
+        for (int i = 0; i < src.n(); ++i) {
+          const int d = src.depth(i);
+          if (d <= 0) continue;
+          const int top = src.frame(i, d - 1);
+          for (int e = a.g.edge_offsets[top]; e < a.g.edge_offsets[top + 1]; ++e) {
+            if (a.g.edge_kind[e] != BPD_PDA_EDGE_BYTE) continue;
+            const int el = a.g.edge_lo[e], eh = a.g.edge_hi[e];
+            if (el <= byte) lo = max(lo, el); else hi = min(hi, el - 1);
+            if (eh >= byte) hi = min(hi, eh); else lo = max(lo, eh + 1);
+          }
+        }
+        cand_lo[tid] = int16_t(lo);
+        cand_hi[tid] = int16_t(hi);
+        const uint32_t bit = 1u << (lo & 31);
+        const bool first = (atomicOr(&req[set * 8 + (lo >> 5)], bit) & bit) == 0;
+        cand_res[tid] = first ? 0 : -4;
+      }
+      __syncthreads();
+      if (tid < n && cand_res[tid] != -4) {
         const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
         FlatView dst{cand + tid * kConfigWords};
         dst.reset_all();
@@ -372,8 +400,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
       }
       __syncthreads();
-      if (tid < n) {
-        const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
+      if (tid < n && cand_res[tid] != -4) {
+        const int set = req_list[tid] >> 8;
         const int r = cand_res[tid];
         const int id = r == -2 ? cand_id[cand_lead[tid]] : r;
         uint8_t e;
@@ -385,7 +413,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         } else {
           e = uint8_t(id);
         }
-        T[set * 256 + byte] = e;
+        const int lo = cand_lo[tid], hi = cand_hi[tid];
+        for (int c = lo; c <= hi; ++c) T[set * 256 + c] = e;
+        atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
       }
       __syncthreads();
     }
