@@ -530,3 +530,7 @@ def advance_state(fsa: FsaTensors, states: torch.Tensor, token_ids: torch.Tensor
         return dense_advance(fsa.tok_next, states, token_ids)
     rows, idx = _walked_rows(fsa, states)
     return dense_advance(rows, idx, token_ids)
+
+
+# registers torch.ops.bpdecode.* (the reference loads its extension at this point)
+from . import torch_ops as _torch_ops  # noqa: E402,F401
