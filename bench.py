@@ -77,6 +77,18 @@ class HipEvents:
         return ms.value
 
 
+def _profiled_traffic(name: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprof counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration), or
+    None when no summary for this kernel is present."""
+    p = ROOT / "profiles" / name
+    try:
+        rec = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    return rec.get("traffic_bytes") if rec.get("kernel") == kernel else None
+
+
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -261,7 +273,8 @@ def main(argv=None) -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": _profiled_traffic("dense_mask_bits_email_b256_v151936.traffic.json",
+                                         "dense_mask_bits_kernel<2>"),
             "kernel": "dense_mask_bits_kernel<2>",
             "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1),
             "table_charged_as": "int32 tok_next rows (the kernel reads the packed allow-bit table)",
