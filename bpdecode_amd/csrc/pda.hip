@@ -179,12 +179,13 @@ struct MemoWs {
   int32_t* pool;      // [rows, kMemoSets, kConfigWords]
   int32_t* cand;      // [rows, kMemoReq, kConfigWords]
   int32_t* overflow;  // [rows]
+  uint4* tok16;       // [vocab] first 16 bytes of each token, zero padded
 };
 
-size_t memo_ws_bytes(int64_t rows) {
-  const size_t r = size_t(rows > 0 ? rows : 0);
+size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
+  const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
-  return sets + (r * sizeof(int32_t) + 255) / 256 * 256;
+  return sets + (r * sizeof(int32_t) + 255) / 256 * 256 + v * sizeof(uint4);
 }
 
 MemoWs memo_ws(void* base, int64_t rows) {
@@ -192,7 +193,27 @@ MemoWs memo_ws(void* base, int64_t rows) {
   w.pool = static_cast<int32_t*>(base);
   w.cand = w.pool + size_t(rows) * kMemoSets * kConfigWords;
   w.overflow = w.cand + size_t(rows) * kMemoReq * kConfigWords;
+  w.tok16 = reinterpret_cast<uint4*>(reinterpret_cast<char*>(w.overflow) +
+                                     (size_t(rows) * sizeof(int32_t) + 255) / 256 * 256);
   return w;
+}
+
+// tok16[t] = the first 16 bytes of token t (little-endian words, zero padded)
+__global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restrict__ off,
+                                                          const uint8_t* __restrict__ bytes,
+                                                          int32_t vocab, uint4* __restrict__ out) {
+  const int32_t t = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x);
+  if (t >= vocab) return;
+  const int32_t s = off[t];
+  const int32_t n = min(off[t + 1] - s, 16);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  for (int i = 0; i < n; ++i) w[i >> 2] |= uint32_t(bytes[s + i]) << ((i & 3) * 8);
+  out[t] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ inline int packed_byte(const uint4& p, int i) {
+  const uint32_t w = i < 4 ? p.x : (i < 8 ? p.y : (i < 12 ? p.z : p.w));
+  return int((w >> ((i & 3) * 8)) & 0xFFu);
 }
 
 // FNV-1a over a set's meaningful words.
@@ -224,7 +245,213 @@ __device__ bool same_set(const A& x, const B& y) {
   return true;
 }
 
-__global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets) {
+// ---- wave-cooperative advance_byte (resolution rounds of the memo kernel)
+// The same steps as advance_byte / close / prune_dead of pda_core.hpp on
+// FlatView sets held in LDS, with the inner work spread over the 64 lanes of
+// one wave: holds() compares config j's frames on lanes 8j..8j+7 and ballots,
+// append() copies frames lane-parallel, the compaction of prune_dead moves one
+// config at a time with its frames lane-parallel.  Control flow is uniform
+// across the wave, so every append happens in the sequential order.  LDS
+// operations of one wave complete in order, so a wave-scope fence is enough
+// between a lane's write and another lane's read.
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kF = 2 + kMaxConfigs;  // first frame word
+
+__device__ inline bool coop_holds(const int32_t* dst, const int32_t* src, int i, int keep, int x0,
+                                  int x1, int nx, int lane) {
+  const int D = keep + nx;
+  const int n = dst[0];
+  const int j = lane >> 3, q = lane & 7;
+  bool ok = j < n && dst[2 + j] == D;
+  for (int k = q; ok && k < D; k += 8) {
+    const int want = k < keep ? src[kF + i * kMaxDepth + k] : (k == keep ? x0 : x1);
+    ok = dst[kF + j * kMaxDepth + k] == want;
+  }
+  uint64_t t = __ballot(ok);
+  t &= t >> 1;
+  t &= t >> 2;
+  t &= t >> 4;
+  return (t & 0x0101010101010101ull) != 0;
+}
+
+__device__ inline bool coop_append(int32_t* dst, const int32_t* src, int i, int keep, int x0, int x1,
+                                   int nx, int lane) {
+  const int n = dst[0];
+  if (n >= kMaxConfigs) {
+    wave_sync();
+    if (lane == 0) dst[1] = 1;
+    wave_sync();
+    return false;
+  }
+  if (lane < keep) dst[kF + n * kMaxDepth + lane] = src[kF + i * kMaxDepth + lane];
+  wave_sync();
+  if (lane == 0) {
+    if (nx > 0) dst[kF + n * kMaxDepth + keep] = x0;
+    if (nx > 1) dst[kF + n * kMaxDepth + keep + 1] = x1;
+    dst[2 + n] = keep + nx;
+    dst[0] = n + 1;
+  }
+  wave_sync();
+  return true;
+}
+
+__device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
+  bool changed = true;
+  int guard = 0;
+  while (changed && guard++ < kRounds) {
+    changed = false;
+    const int n = c[0];
+    for (int i = 0; i < n; ++i) {
+      const int d = c[2 + i];
+      if (d <= 0) continue;
+      const int top = c[kF + i * kMaxDepth + d - 1];
+      if (g.accept[top] && d > 1) {
+        if (!coop_holds(c, c, i, d - 1, 0, 0, 0, lane) && coop_append(c, c, i, d - 1, 0, 0, 0, lane))
+          changed = true;
+      }
+      const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
+      for (int e = eb; e < ee; ++e) {
+        const int kind = g.edge_kind[e];
+        if (kind == BPD_PDA_EDGE_EPS) {
+          const int x = g.edge_dst[e];
+          if (!coop_holds(c, c, i, d - 1, x, 0, 1, lane) && coop_append(c, c, i, d - 1, x, 0, 1, lane))
+            changed = true;
+        } else if (kind == BPD_PDA_EDGE_CALL) {
+          if (d + 1 <= kMaxDepth) {
+            const int x0 = g.edge_dst[e], x1 = g.edge_callee[e];
+            if (!coop_holds(c, c, i, d - 1, x0, x1, 2, lane) &&
+                coop_append(c, c, i, d - 1, x0, x1, 2, lane))
+              changed = true;
+          } else {
+            wave_sync();
+            if (lane == 0) c[1] = 1;
+            wave_sync();
+          }
+        }
+      }
+    }
+  }
+  // prune_dead: order-preserving compaction, vacated words not cleared
+  int out = 0;
+  const int n = c[0];
+  for (int i = 0; i < n; ++i) {
+    const int d = c[2 + i];
+    if (d <= 0) continue;
+    if (!g.live[c[kF + i * kMaxDepth + d - 1]]) continue;
+    if (out != i) {
+      if (lane < d) c[kF + out * kMaxDepth + lane] = c[kF + i * kMaxDepth + lane];
+      wave_sync();
+      if (lane == 0) c[2 + out] = d;
+      wave_sync();
+    }
+    ++out;
+  }
+  wave_sync();
+  if (lane == 0) c[0] = out;
+  wave_sync();
+  return out > 0;
+}
+
+// next = close(byte step of src) with next freshly zeroed (as FlatView::reset_all)
+__device__ bool coop_advance_byte(const PdaTableView& g, const int32_t* src, int32_t* next, int byte,
+                                  int lane) {
+  for (int k = lane; k < kConfigWords; k += kWave) next[k] = 0;
+  wave_sync();
+  const int n = src[0];
+  for (int i = 0; i < n; ++i) {
+    const int d = src[2 + i];
+    if (d <= 0) continue;
+    const int top = src[kF + i * kMaxDepth + d - 1];
+    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
+    for (int e = eb; e < ee; ++e) {
+      if (g.edge_kind[e] != BPD_PDA_EDGE_BYTE) continue;
+      if (byte < g.edge_lo[e] || byte > g.edge_hi[e]) continue;
+      const int x = g.edge_dst[e];
+      if (!coop_holds(next, src, i, d - 1, x, 0, 1, lane)) coop_append(next, src, i, d - 1, x, 0, 1, lane);
+    }
+  }
+  wave_sync();
+  if (lane == 0) next[1] = (next[1] || src[1]) ? 1 : 0;
+  wave_sync();
+  return coop_close(g, next, lane);
+}
+
+// Is word w of a FlatView set with n configs and depths dep() meaningful?
+__device__ inline bool meaningful_word(const int32_t* c, int n, int w) {
+  if (w < 2) return true;
+  if (w < kF) return w - 2 < n;
+  const int i = (w - kF) / kMaxDepth, k = (w - kF) % kMaxDepth;
+  return i < n && k < c[2 + i];
+}
+
+__device__ inline uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352dU;
+  x ^= x >> 15;
+  x *= 0x846ca68bU;
+  x ^= x >> 16;
+  return x;
+}
+
+// Hash of a set's meaningful words (sum of per-word mixes, lane-parallel);
+// every lane gets the value.  c must be a well-formed set (n <= 8, depths <= 32).
+__device__ uint32_t coop_hash(const int32_t* c, int lane) {
+  const int n = c[0];
+  uint32_t h = 0;
+  for (int w = lane; w < kConfigWords; w += kWave)
+    if (meaningful_word(c, n, w)) h += mix32(uint32_t(w) * 0x9E3779B1u ^ uint32_t(c[w]));
+  for (int o = 32; o > 0; o >>= 1) h += __shfl_xor(h, o);
+  return h;
+}
+
+// Equal meaningful words (x in LDS, y anywhere); every lane gets the answer.
+__device__ bool coop_same(const int32_t* x, const int32_t* y, int lane) {
+  const int n = x[0];
+  if (n != y[0] || x[1] != y[1]) return false;
+  bool diff = false;
+  for (int w = lane; w < kConfigWords; w += kWave) {
+    if (w < kF) {
+      diff |= (w >= 2 && w - 2 < n && x[w] != y[w]);
+    } else {
+      const int i = (w - kF) / kMaxDepth, k = (w - kF) % kMaxDepth;
+      // depths are compared by lanes 2..9 above; a frame is compared where
+      // it is meaningful in x
+      diff |= (i < n && k < x[2 + i] && x[w] != y[w]);
+    }
+  }
+  return __ballot(diff) == 0;
+}
+
+// Byte-class interval of `byte` for a set given its top states: every byte
+// in [lo, hi] lies in the same byte edges of those tops.
+__device__ inline void byte_interval(const PdaTableView& g, const int32_t* tops, int n, int byte,
+                                     int& lo, int& hi) {
+  lo = 0;
+  hi = 255;
+  for (int i = 0; i < n; ++i) {
+    const int top = tops[i];
+    if (top < 0) continue;
+    for (int e = g.edge_offsets[top]; e < g.edge_offsets[top + 1]; ++e) {
+      if (g.edge_kind[e] != BPD_PDA_EDGE_BYTE) continue;
+      const int el = g.edge_lo[e], eh = g.edge_hi[e];
+      if (el <= byte) lo = max(lo, el); else hi = min(hi, el - 1);
+      if (eh >= byte) hi = min(hi, eh); else lo = max(lo, eh + 1);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
+                                                                     int table_in_lds) {
+  extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
+  __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
+  __shared__ int32_t set_n[kMemoSets];
+  __shared__ int32_t cand_tops[kMemoReq][kMaxConfigs];
+  __shared__ int32_t cand_n[kMemoReq];
   __shared__ uint32_t T32[kMemoSets * 256 / 4];
   __shared__ uint32_t req[kMemoSets * 8];
   __shared__ uint32_t pool_hash[kMemoSets];
@@ -236,6 +463,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int16_t cand_lo[kMemoReq];
   __shared__ int16_t cand_hi[kMemoReq];
   __shared__ int32_t row_cfg[kConfigWords];
+  __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
   __shared__ int pool_count, nreq, row_flags, overflowed;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
@@ -246,6 +474,38 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   int32_t* cand = ws.cand + b * kMemoReq * kConfigWords;
 
   for (int k = tid; k < kConfigWords; k += kMemoThreads) row_cfg[k] = a.configs[row * kConfigWords + k];
+  PdaTableView g = a.g;
+  if (table_in_lds) {
+    const int N = a.g.num_states, E = a.g.num_edges;
+    int32_t* eo = tab;
+    int32_t* ek = eo + N + 1;
+    int32_t* elo = ek + E;
+    int32_t* ehi = elo + E;
+    int32_t* ed = ehi + E;
+    int32_t* ec = ed + E;
+    uint8_t* acc = reinterpret_cast<uint8_t*>(ec + E);
+    uint8_t* lv = acc + N;
+    for (int i = tid; i <= N; i += kMemoThreads) eo[i] = a.g.edge_offsets[i];
+    for (int i = tid; i < E; i += kMemoThreads) {
+      ek[i] = a.g.edge_kind[i];
+      elo[i] = a.g.edge_lo[i];
+      ehi[i] = a.g.edge_hi[i];
+      ed[i] = a.g.edge_dst[i];
+      ec[i] = a.g.edge_callee[i];
+    }
+    for (int i = tid; i < N; i += kMemoThreads) {
+      acc[i] = a.g.accept[i];
+      lv[i] = a.g.live[i];
+    }
+    g.edge_offsets = eo;
+    g.edge_kind = ek;
+    g.edge_lo = elo;
+    g.edge_hi = ehi;
+    g.edge_dst = ed;
+    g.edge_callee = ec;
+    g.accept = acc;
+    g.live = lv;
+  }
   for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
   for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0;
   if (tid == 0) {
@@ -259,10 +519,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (tid == 0 && a.err) atomicOr(a.err, BPD_FLAG_STATE_RANGE);
       dead = true;
     }
+    const uint32_t h0 = dead ? 0u : coop_hash(row_cfg, tid);
     if (tid == 0) {
       const ConstFlatView C{row_cfg};
       row_flags = dead ? 1 : ((is_complete(a.g, C) ? 2 : 0) | (C.n() > 0 ? 4 : 0));
-      pool_hash[0] = dead ? 0u : set_hash(C);
+      pool_hash[0] = h0;
+    }
+    if (tid < kMaxConfigs) {
+      const int n = dead ? 0 : row_cfg[0];
+      const int d = tid < n ? row_cfg[2 + tid] : 0;
+      set_tops[0][tid] = d > 0 ? row_cfg[kF + tid * kMaxDepth + d - 1] : -1;
+      if (tid == 0) set_n[0] = n;
     }
   }
   for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
@@ -272,13 +539,16 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 
   const int64_t V = a.vocab;
   for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
-    int32_t pos[kMemoTok], end[kMemoTok];
+    // per token: length, position, set id, status and its first 16 bytes
+    int32_t pos[kMemoTok], len[kMemoTok];
     int cur[kMemoTok], st[kMemoTok];  // st: 0 walking, 1 allowed, 2 rejected, 3 overflow, 4 none
+    uint4 pk[kMemoTok];
 #pragma unroll
     for (int j = 0; j < kMemoTok; ++j) {
       const int64_t t = tile + int64_t(j) * kMemoThreads + tid;
-      pos[j] = end[j] = 0;
+      pos[j] = len[j] = 0;
       cur[j] = 0;
+      pk[j] = make_uint4(0u, 0u, 0u, 0u);
       if (t >= V) {
         st[j] = 4;
       } else if (dead_row) {
@@ -286,9 +556,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       } else if (t == a.eos) {
         st[j] = (flags & 2) ? 1 : 2;
       } else {
-        pos[j] = a.tok_off[t];
-        end[j] = a.tok_off[t + 1];
-        st[j] = pos[j] == end[j] ? ((flags & 4) ? 1 : 2) : 0;
+        len[j] = a.tok_off[t + 1] - a.tok_off[t];
+        pk[j] = ws.tok16[t];
+        st[j] = len[j] == 0 ? ((flags & 4) ? 1 : 2) : 0;
       }
     }
     while (true) {
@@ -296,11 +566,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 #pragma unroll
       for (int j = 0; j < kMemoTok; ++j) {
         while (st[j] == 0) {
-          if (pos[j] == end[j]) {
+          if (pos[j] == len[j]) {
             st[j] = 1;
             break;
           }
-          const int byte = a.tok_bytes[pos[j]];
+          const int byte = pos[j] < 16 ? packed_byte(pk[j], pos[j])
+                                       : int(a.tok_bytes[a.tok_off[tile + int64_t(j) * kMemoThreads + tid] + pos[j]]);
           const uint8_t nx = T[cur[j] * 256 + byte];
           if (nx == kTUnknown) {
             atomicOr(&req[cur[j] * 8 + (byte >> 5)], 1u << (byte & 31));
@@ -343,19 +614,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         // interval [lo, hi] around the request shares its result: the first
         // request of an interval computes it and fills the whole interval
         const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
-        const ConstFlatView src{pool + set * kConfigWords};
-        int lo = 0, hi = 255;
-        for (int i = 0; i < src.n(); ++i) {
-          const int d = src.depth(i);
-          if (d <= 0) continue;
-          const int top = src.frame(i, d - 1);
-          for (int e = a.g.edge_offsets[top]; e < a.g.edge_offsets[top + 1]; ++e) {
-            if (a.g.edge_kind[e] != BPD_PDA_EDGE_BYTE) continue;
-            const int el = a.g.edge_lo[e], eh = a.g.edge_hi[e];
-            if (el <= byte) lo = max(lo, el); else hi = min(hi, el - 1);
-            if (eh >= byte) hi = min(hi, eh); else lo = max(lo, eh + 1);
-          }
-        }
+        int lo, hi;
+        byte_interval(g, set_tops[set], set_n[set], byte, lo, hi);
         cand_lo[tid] = int16_t(lo);
         cand_hi[tid] = int16_t(hi);
         const uint32_t bit = 1u << (lo & 31);
@@ -363,20 +623,40 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         cand_res[tid] = first ? 0 : -4;
       }
       __syncthreads();
-      if (tid < n && cand_res[tid] != -4) {
-        const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
-        FlatView dst{cand + tid * kConfigWords};
-        dst.reset_all();
-        if (!advance_byte(a.g, ConstFlatView{pool + set * kConfigWords}, dst, byte)) {
-          cand_res[tid] = -1;
-        } else {
-          const uint32_t h = set_hash(dst);
-          cand_hash[tid] = h;
-          int found = -2;
-          const int pc = pool_count < max_sets ? pool_count : max_sets;
-          for (int k = 0; k < pc && found < 0; ++k)
-            if (pool_hash[k] == h && same_set(ConstFlatView{pool + k * kConfigWords}, dst)) found = k;
-          cand_res[tid] = found;
+      {
+        // one wave per claimed transition, working sets in LDS
+        const int lane = tid & (kWave - 1), wave = tid / kWave;
+        int32_t* wsrc = work[wave][0];
+        int32_t* wdst = work[wave][1];
+        for (int r = wave; r < n; r += kMemoThreads / kWave) {
+          if (cand_res[r] == -4) continue;
+          const int set = req_list[r] >> 8, byte = req_list[r] & 255;
+          const int32_t* ps = pool + set * kConfigWords;
+          for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
+          wave_sync();
+          const bool ok = coop_advance_byte(g, wsrc, wdst, byte, lane);
+          int32_t* out = cand + r * kConfigWords;
+          for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
+          if (!ok) {
+            if (lane == 0) cand_res[r] = -1;
+          } else {
+            const uint32_t h = coop_hash(wdst, lane);
+            int found = -2;
+            const int pc = pool_count < max_sets ? pool_count : max_sets;
+            for (int k = 0; k < pc && found < 0; ++k)
+              if (pool_hash[k] == h && coop_same(wdst, pool + k * kConfigWords, lane)) found = k;
+            if (lane < kMaxConfigs) {
+              const int nn = wdst[0];
+              const int d = lane < nn ? wdst[2 + lane] : 0;
+              cand_tops[r][lane] = d > 0 ? wdst[kF + lane * kMaxDepth + d - 1] : -1;
+              if (lane == 0) cand_n[r] = nn;
+            }
+            if (lane == 0) {
+              cand_hash[r] = h;
+              cand_res[r] = found;
+            }
+          }
+          wave_sync();
         }
       }
       __syncthreads();
@@ -391,8 +671,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (lead == tid) {
           const int id = atomicAdd(&pool_count, 1);
           if (id < max_sets) {
-            for (int k = 0; k < kConfigWords; ++k) pool[id * kConfigWords + k] = mine.w[k];
             pool_hash[id] = cand_hash[tid];
+            set_n[id] = cand_n[tid];
+            for (int i = 0; i < kMaxConfigs; ++i) set_tops[id][i] = cand_tops[tid][i];
             cand_id[tid] = id;
           } else {
             cand_id[tid] = -3;
@@ -416,6 +697,16 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         const int lo = cand_lo[tid], hi = cand_hi[tid];
         for (int c = lo; c <= hi; ++c) T[set * 256 + c] = e;
         atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
+      }
+      {
+        // new sets into the pool, one wave per set
+        const int lane = tid & (kWave - 1), wave = tid / kWave;
+        for (int r = wave; r < n; r += kMemoThreads / kWave) {
+          if (cand_res[r] != -2 || cand_lead[r] != r || cand_id[r] < 0) continue;
+          const int32_t* src = cand + r * kConfigWords;
+          int32_t* dst = pool + cand_id[r] * kConfigWords;
+          for (int k = lane; k < kConfigWords; k += kWave) dst[k] = src[k];
+        }
       }
       __syncthreads();
     }
@@ -570,8 +861,7 @@ bool host_config_ok(const int32_t* c, int32_t num_states) {
 using namespace bpd;
 
 extern "C" size_t bpd_pda_workspace_bytes(int64_t rows, int32_t vocab) {
-  (void)vocab;
-  return memo_ws_bytes(rows);
+  return memo_ws_bytes(rows, vocab);
 }
 
 extern "C" int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data,
@@ -643,16 +933,29 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
   a.err = nullptr;
   a.only_rows = nullptr;
   if (workspace) {
-    BPD_REQUIRE(workspace_bytes >= memo_ws_bytes(rows), "workspace too small (%zu < %zu bytes)",
-                workspace_bytes, memo_ws_bytes(rows));
+    const size_t need = memo_ws_bytes(rows, toks->vocab_size);
+    BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
     const MemoWs ws = memo_ws(workspace, rows);
+    pack_tokens_kernel<<<unsigned((toks->vocab_size + 255) / 256), 256, 0, as_stream(stream)>>>(
+        toks->offsets, toks->bytes, toks->vocab_size, ws.tok16);
+    BPD_LAUNCHED();
     // BPD_PDA_MEMO_SETS lowers the interned-set limit (tests of the overflow path)
     int max_sets = kMemoSets;
     if (const char* e = std::getenv("BPD_PDA_MEMO_SETS")) {
       const int v = std::atoi(e);
       if (v >= 1 && v < kMemoSets) max_sets = v;
     }
-    pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, 0, as_stream(stream)>>>(a, ws, max_sets);
+    // stage the grammar tables in LDS when they fit beside the static arrays
+    const size_t tab_bytes = (size_t(g->num_states) + 1) * 4 + size_t(g->num_edges) * 20 +
+                             (size_t(g->num_states) * 2 + 3) / 4 * 4;
+    int dev = 0, max_lds = 0;
+    BPD_HIP(hipGetDevice(&dev));
+    BPD_HIP(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    hipFuncAttributes fa{};
+    BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&pda_memo_mask_kernel)));
+    const bool in_lds = fa.sharedSizeBytes + tab_bytes <= size_t(max_lds);
+    pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
+        a, ws, max_sets, in_lds ? 1 : 0);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
   }
