@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
@@ -42,7 +42,7 @@ class PdaTableC(C.Structure):
 
 
 class TokenBytesC(C.Structure):
-    _fields_ = [("vocab_size", i32), ("eos_id", i32), ("offsets", vp), ("bytes", vp)]
+    _fields_ = [("vocab_size", i32), ("eos_id", i32), ("offsets", vp), ("bytes", vp), ("order", vp)]
 
 
 class SoftClassesC(C.Structure):

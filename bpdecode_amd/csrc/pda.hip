@@ -45,6 +45,7 @@ struct MaskArgs {
   int32_t chunk_tokens;  // multiple of 64
   int32_t* err;
   const int32_t* only_rows;  // non-null: process only rows b with only_rows[b] != 0
+  const int32_t* order;      // memo walk order (null: id order)
 };
 
 // Structural check of a row's config-set before any table lookup with its
@@ -171,6 +172,7 @@ constexpr int kMemoThreads = 1024;
 constexpr int kMemoSets = 128;
 constexpr int kMemoReq = 256;
 constexpr int kMemoTok = 4;
+constexpr int kMemoMaxVocab = 262144;  // verdict bitmap of a row in LDS
 constexpr uint8_t kTUnknown = 0xFE;
 constexpr uint8_t kTDead = 0xFF;
 constexpr uint8_t kTOverflow = 0xFD;
@@ -301,37 +303,28 @@ __device__ inline bool coop_append(int32_t* dst, const int32_t* src, int i, int 
 }
 
 __device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
-  bool changed = true;
-  int guard = 0;
-  while (changed && guard++ < kRounds) {
-    changed = false;
-    const int n = c[0];
-    for (int i = 0; i < n; ++i) {
-      const int d = c[2 + i];
-      if (d <= 0) continue;
-      const int top = c[kF + i * kMaxDepth + d - 1];
-      if (g.accept[top] && d > 1) {
-        if (!coop_holds(c, c, i, d - 1, 0, 0, 0, lane) && coop_append(c, c, i, d - 1, 0, 0, 0, lane))
-          changed = true;
-      }
-      const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
-      for (int e = eb; e < ee; ++e) {
-        const int kind = g.edge_kind[e];
-        if (kind == BPD_PDA_EDGE_EPS) {
-          const int x = g.edge_dst[e];
-          if (!coop_holds(c, c, i, d - 1, x, 0, 1, lane) && coop_append(c, c, i, d - 1, x, 0, 1, lane))
-            changed = true;
-        } else if (kind == BPD_PDA_EDGE_CALL) {
-          if (d + 1 <= kMaxDepth) {
-            const int x0 = g.edge_dst[e], x1 = g.edge_callee[e];
-            if (!coop_holds(c, c, i, d - 1, x0, x1, 2, lane) &&
-                coop_append(c, c, i, d - 1, x0, x1, 2, lane))
-              changed = true;
-          } else {
-            wave_sync();
-            if (lane == 0) c[1] = 1;
-            wave_sync();
-          }
+  // one visit per config in index order, as close() in pda_core.hpp
+  for (int i = 0; i < c[0]; ++i) {
+    const int d = c[2 + i];
+    if (d <= 0) continue;
+    const int top = c[kF + i * kMaxDepth + d - 1];
+    if (g.accept[top] && d > 1) {
+      if (!coop_holds(c, c, i, d - 1, 0, 0, 0, lane)) coop_append(c, c, i, d - 1, 0, 0, 0, lane);
+    }
+    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
+    for (int e = eb; e < ee; ++e) {
+      const int kind = g.edge_kind[e];
+      if (kind == BPD_PDA_EDGE_EPS) {
+        const int x = g.edge_dst[e];
+        if (!coop_holds(c, c, i, d - 1, x, 0, 1, lane)) coop_append(c, c, i, d - 1, x, 0, 1, lane);
+      } else if (kind == BPD_PDA_EDGE_CALL) {
+        if (d + 1 <= kMaxDepth) {
+          const int x0 = g.edge_dst[e], x1 = g.edge_callee[e];
+          if (!coop_holds(c, c, i, d - 1, x0, x1, 2, lane)) coop_append(c, c, i, d - 1, x0, x1, 2, lane);
+        } else {
+          wave_sync();
+          if (lane == 0) c[1] = 1;
+          wave_sync();
         }
       }
     }
@@ -453,6 +446,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t cand_tops[kMemoReq][kMaxConfigs];
   __shared__ int32_t cand_n[kMemoReq];
   __shared__ uint32_t T32[kMemoSets * 256 / 4];
+  __shared__ uint32_t vbits[kMemoMaxVocab / 32];  // allowed tokens of the row
   __shared__ uint32_t req[kMemoSets * 8];
   __shared__ uint32_t pool_hash[kMemoSets];
   __shared__ int32_t req_list[kMemoReq];
@@ -507,6 +501,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     g.live = lv;
   }
   for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
+  const int32_t vwords = (a.vocab + 31) / 32;
+  for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
   for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0;
   if (tid == 0) {
     pool_count = 1;
@@ -540,12 +536,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   const int64_t V = a.vocab;
   for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
     // per token: length, position, set id, status and its first 16 bytes
-    int32_t pos[kMemoTok], len[kMemoTok];
+    int32_t pos[kMemoTok], len[kMemoTok], tk[kMemoTok];
     int cur[kMemoTok], st[kMemoTok];  // st: 0 walking, 1 allowed, 2 rejected, 3 overflow, 4 none
     uint4 pk[kMemoTok];
 #pragma unroll
     for (int j = 0; j < kMemoTok; ++j) {
-      const int64_t t = tile + int64_t(j) * kMemoThreads + tid;
+      const int64_t k = tile + int64_t(j) * kMemoThreads + tid;
+      const int64_t t = k < V ? (a.order ? a.order[k] : k) : k;
+      tk[j] = int32_t(t);
       pos[j] = len[j] = 0;
       cur[j] = 0;
       pk[j] = make_uint4(0u, 0u, 0u, 0u);
@@ -570,8 +568,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             st[j] = 1;
             break;
           }
-          const int byte = pos[j] < 16 ? packed_byte(pk[j], pos[j])
-                                       : int(a.tok_bytes[a.tok_off[tile + int64_t(j) * kMemoThreads + tid] + pos[j]]);
+          const int byte = pos[j] < 16 ? packed_byte(pk[j], pos[j]) : int(a.tok_bytes[a.tok_off[tk[j]] + pos[j]]);
           const uint8_t nx = T[cur[j] * 256 + byte];
           if (nx == kTUnknown) {
             atomicOr(&req[cur[j] * 8 + (byte >> 5)], 1u << (byte & 31));
@@ -711,30 +708,44 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       __syncthreads();
     }
 
-    // verdicts of the tile; overflow tokens are left to the direct walk
+    // allowed tokens of the tile into the row's bitmap
 #pragma unroll
-    for (int j = 0; j < kMemoTok; ++j) {
-      const int64_t t = tile + int64_t(j) * kMemoThreads + tid;
-      if (a.logits) {
-        if (st[j] == 2) {
-          uint8_t* p = a.logits + b * a.ld_bytes + t * a.elem;
-          if (a.elem == 2)
-            *reinterpret_cast<uint16_t*>(p) = uint16_t(a.fill);
-          else
-            *reinterpret_cast<uint32_t*>(p) = a.fill;
-        }
-      } else {
-        const uint64_t m = __ballot(st[j] == 1);
-        if ((tid & 63) == 0) {
-          const int64_t w0 = (tile + int64_t(j) * kMemoThreads + tid) >> 5;
-          if (w0 < a.words) a.bits[b * a.words + w0] = uint32_t(m);
-          if (w0 + 1 < a.words) a.bits[b * a.words + w0 + 1] = uint32_t(m >> 32);
-        }
-      }
-    }
+    for (int j = 0; j < kMemoTok; ++j)
+      if (st[j] == 1) atomicOr(&vbits[tk[j] >> 5], 1u << (tk[j] & 31));
   }
   __syncthreads();
   if (tid == 0) ws.overflow[b] = overflowed;
+  if (overflowed) return;  // the direct walk writes this row
+  if (!a.logits) {
+    for (int w = tid; w < vwords && w < a.words; w += kMemoThreads) a.bits[b * a.words + w] = vbits[w];
+    return;
+  }
+  // logits: fill the rejected tokens, 8 columns per thread and step
+  uint8_t* rowp = a.logits + b * a.ld_bytes;
+  const bool vec = (reinterpret_cast<uintptr_t>(rowp) & 15u) == 0 && (a.ld_bytes & 15) == 0;
+  for (int64_t c0 = int64_t(tid) * 8; c0 < V; c0 += int64_t(kMemoThreads) * 8) {
+    const uint32_t m = (vbits[c0 >> 5] >> (c0 & 31)) & 0xFFu;
+    if (m == 0xFFu) continue;
+    const int nc = V - c0 < 8 ? int(V - c0) : 8;
+    if (m == 0u && nc == 8 && vec) {
+      if (a.elem == 2) {
+        const uint32_t f2 = (a.fill & 0xFFFFu) | (a.fill << 16);
+        *reinterpret_cast<uint4*>(rowp + c0 * 2) = make_uint4(f2, f2, f2, f2);
+      } else {
+        *reinterpret_cast<uint4*>(rowp + c0 * 4) = make_uint4(a.fill, a.fill, a.fill, a.fill);
+        *reinterpret_cast<uint4*>(rowp + c0 * 4 + 16) = make_uint4(a.fill, a.fill, a.fill, a.fill);
+      }
+      continue;
+    }
+    for (int i = 0; i < nc; ++i) {
+      if ((m >> i) & 1u) continue;
+      uint8_t* p = rowp + (c0 + i) * a.elem;
+      if (a.elem == 2)
+        *reinterpret_cast<uint16_t*>(p) = uint16_t(a.fill);
+      else
+        *reinterpret_cast<uint32_t*>(p) = a.fill;
+    }
+  }
 }
 
 struct AdvanceArgs {
@@ -932,7 +943,8 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
   a.chunk_tokens = int32_t(per);
   a.err = nullptr;
   a.only_rows = nullptr;
-  if (workspace) {
+  a.order = toks->order;
+  if (workspace && toks->vocab_size <= kMemoMaxVocab) {
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
     const MemoWs ws = memo_ws(workspace, rows);

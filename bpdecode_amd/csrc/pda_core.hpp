@@ -42,7 +42,6 @@ namespace bpd {
 constexpr int kMaxConfigs = BPD_PDA_MAX_CONFIGS;
 constexpr int kMaxDepth = BPD_PDA_MAX_DEPTH;
 constexpr int kConfigWords = BPD_PDA_CONFIG_WORDS;
-constexpr int kRounds = kMaxConfigs * kMaxDepth + 8;
 
 struct PdaTableView {
   int32_t num_states, root_start, root_accept, num_edges;
@@ -170,33 +169,37 @@ BPD_HD void prune_dead(const PdaTableView& g, S& c) {
   c.set_n(out);
 }
 
+// The closure visits every config once, in index order, including the
+// configs it appends.  This is the reference's round structure (pda.hpp:
+// 150-196: rounds over the configs present at each round's start until a
+// round appends nothing) without its repeated visits: configs are never
+// modified or removed while closing and the set only grows, so a config
+// visited again yields only candidates that are already present or that were
+// dropped because the set is full -- no append and no new saturation.  The
+// appends, their order and the saturated flag are therefore identical.  At
+// most kMaxConfigs configs exist, so at most kMaxConfigs + 1 reference rounds
+// run and its round guard (pda.hpp:154) is never reached.
 template <class S>
 BPD_HD bool close(const PdaTableView& g, S& c) {
-  bool changed = true;
-  int guard = 0;
-  while (changed && guard++ < kRounds) {
-    changed = false;
-    const int n = c.n();
-    for (int i = 0; i < n; ++i) {
-      const int d = c.depth(i);
-      if (d <= 0) continue;
-      const int top = c.frame(i, d - 1);
-      if (g.accept[top] && d > 1) {
-        if (!holds(c, c, i, d - 1, nullptr, 0) && append(c, c, i, d - 1, nullptr, 0)) changed = true;
-      }
-      const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
-      for (int e = eb; e < ee; ++e) {
-        const int kind = g.edge_kind[e];
-        if (kind == BPD_PDA_EDGE_EPS) {
-          const int x[1] = {g.edge_dst[e]};
-          if (!holds(c, c, i, d - 1, x, 1) && append(c, c, i, d - 1, x, 1)) changed = true;
-        } else if (kind == BPD_PDA_EDGE_CALL) {
-          if (d + 1 <= kMaxDepth) {
-            const int x[2] = {g.edge_dst[e], g.edge_callee[e]};
-            if (!holds(c, c, i, d - 1, x, 2) && append(c, c, i, d - 1, x, 2)) changed = true;
-          } else {
-            c.set_sat(1);
-          }
+  for (int i = 0; i < c.n(); ++i) {
+    const int d = c.depth(i);
+    if (d <= 0) continue;
+    const int top = c.frame(i, d - 1);
+    if (g.accept[top] && d > 1) {
+      if (!holds(c, c, i, d - 1, nullptr, 0)) append(c, c, i, d - 1, nullptr, 0);
+    }
+    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
+    for (int e = eb; e < ee; ++e) {
+      const int kind = g.edge_kind[e];
+      if (kind == BPD_PDA_EDGE_EPS) {
+        const int x[1] = {g.edge_dst[e]};
+        if (!holds(c, c, i, d - 1, x, 1)) append(c, c, i, d - 1, x, 1);
+      } else if (kind == BPD_PDA_EDGE_CALL) {
+        if (d + 1 <= kMaxDepth) {
+          const int x[2] = {g.edge_dst[e], g.edge_callee[e]};
+          if (!holds(c, c, i, d - 1, x, 2)) append(c, c, i, d - 1, x, 2);
+        } else {
+          c.set_sat(1);
         }
       }
     }

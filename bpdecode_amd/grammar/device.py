@@ -125,9 +125,12 @@ class PdaTensors:
             tb = self.tok_bytes.contiguous()
             if tb.numel() == 0:
                 tb = torch.zeros(1, dtype=torch.uint8, device=self.device)
-            t = _lib.TokenBytesC(self.vocab_size, self.eos_id, ptr(off), ptr(tb))
+            # walk order of the memoised device mask: shortest tokens first
+            lengths = off[1:] - off[:-1]
+            order = torch.argsort(lengths, stable=True).to(torch.int32)
+            t = _lib.TokenBytesC(self.vocab_size, self.eos_id, ptr(off), ptr(tb), ptr(order))
             self._c["tokens"] = t
-            self._c["tokens_keep"] = (off, tb)
+            self._c["tokens_keep"] = (off, tb, order)
         return t
 
     def init_config(self) -> torch.Tensor:

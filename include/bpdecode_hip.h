@@ -156,6 +156,10 @@ typedef struct BpdTokenBytes {
   int32_t eos_id;
   const int32_t* offsets; /* [vocab_size + 1] */
   const uint8_t* bytes;   /* [offsets[vocab_size]] */
+  /* optional (NULL = id order): a permutation of the token ids by byte
+   * length, shortest first; the memoised device mask walks tokens in this
+   * order (lanes of a wave then walk equally long tokens) */
+  const int32_t* order;
 } BpdTokenBytes;
 
 /* bpd_pda_init: the closed initial config-set (pda.hpp:200-207), host only,
