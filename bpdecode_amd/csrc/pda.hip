@@ -303,24 +303,34 @@ __device__ inline bool coop_append(int32_t* dst, const int32_t* src, int i, int 
 }
 
 __device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
-  // one visit per config in index order, as close() in pda_core.hpp
+  // one visit per config in index order, as close() in pda_core.hpp; the
+  // top state's edges are loaded lane-parallel and the eps / call edges taken
+  // in edge order from the ballot
   for (int i = 0; i < c[0]; ++i) {
     const int d = c[2 + i];
     if (d <= 0) continue;
     const int top = c[kF + i * kMaxDepth + d - 1];
+    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
     if (g.accept[top] && d > 1) {
       if (!coop_holds(c, c, i, d - 1, 0, 0, 0, lane)) coop_append(c, c, i, d - 1, 0, 0, 0, lane);
     }
-    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
-    for (int e = eb; e < ee; ++e) {
-      const int kind = g.edge_kind[e];
-      if (kind == BPD_PDA_EDGE_EPS) {
-        const int x = g.edge_dst[e];
-        if (!coop_holds(c, c, i, d - 1, x, 0, 1, lane)) coop_append(c, c, i, d - 1, x, 0, 1, lane);
-      } else if (kind == BPD_PDA_EDGE_CALL) {
-        if (d + 1 <= kMaxDepth) {
-          const int x0 = g.edge_dst[e], x1 = g.edge_callee[e];
-          if (!coop_holds(c, c, i, d - 1, x0, x1, 2, lane)) coop_append(c, c, i, d - 1, x0, x1, 2, lane);
+    for (int base = eb; base < ee; base += kWave) {
+      const int e = base + lane;
+      int kind = -1, x0 = 0, x1 = 0;
+      if (e < ee) {
+        kind = g.edge_kind[e];
+        x0 = g.edge_dst[e];
+        x1 = g.edge_callee[e];
+      }
+      uint64_t m = __ballot(kind == BPD_PDA_EDGE_EPS || kind == BPD_PDA_EDGE_CALL);
+      while (m) {
+        const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        m &= m - 1;
+        const int k = __shfl(kind, l), y0 = __shfl(x0, l), y1 = __shfl(x1, l);
+        if (k == BPD_PDA_EDGE_EPS) {
+          if (!coop_holds(c, c, i, d - 1, y0, 0, 1, lane)) coop_append(c, c, i, d - 1, y0, 0, 1, lane);
+        } else if (d + 1 <= kMaxDepth) {
+          if (!coop_holds(c, c, i, d - 1, y0, y1, 2, lane)) coop_append(c, c, i, d - 1, y0, y1, 2, lane);
         } else {
           wave_sync();
           if (lane == 0) c[1] = 1;
@@ -361,11 +371,21 @@ __device__ bool coop_advance_byte(const PdaTableView& g, const int32_t* src, int
     if (d <= 0) continue;
     const int top = src[kF + i * kMaxDepth + d - 1];
     const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
-    for (int e = eb; e < ee; ++e) {
-      if (g.edge_kind[e] != BPD_PDA_EDGE_BYTE) continue;
-      if (byte < g.edge_lo[e] || byte > g.edge_hi[e]) continue;
-      const int x = g.edge_dst[e];
-      if (!coop_holds(next, src, i, d - 1, x, 0, 1, lane)) coop_append(next, src, i, d - 1, x, 0, 1, lane);
+    for (int base = eb; base < ee; base += kWave) {
+      const int e = base + lane;
+      bool match = false;
+      int x = 0;
+      if (e < ee && g.edge_kind[e] == BPD_PDA_EDGE_BYTE) {
+        match = byte >= g.edge_lo[e] && byte <= g.edge_hi[e];
+        x = g.edge_dst[e];
+      }
+      uint64_t m = __ballot(match);
+      while (m) {
+        const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        m &= m - 1;
+        const int y = __shfl(x, l);
+        if (!coop_holds(next, src, i, d - 1, y, 0, 1, lane)) coop_append(next, src, i, d - 1, y, 0, 1, lane);
+      }
     }
   }
   wave_sync();
@@ -422,10 +442,13 @@ __device__ bool coop_same(const int32_t* x, const int32_t* y, int lane) {
 
 // Byte-class interval of `byte` for a set given its top states: every byte
 // in [lo, hi] lies in the same byte edges of those tops.
-__device__ inline void byte_interval(const PdaTableView& g, const int32_t* tops, int n, int byte,
+// Returns whether any of those byte edges contains `byte` (if none does, the
+// step from the set empties it for the whole interval).
+__device__ inline bool byte_interval(const PdaTableView& g, const int32_t* tops, int n, int byte,
                                      int& lo, int& hi) {
   lo = 0;
   hi = 255;
+  bool hit = false;
   for (int i = 0; i < n; ++i) {
     const int top = tops[i];
     if (top < 0) continue;
@@ -434,8 +457,10 @@ __device__ inline void byte_interval(const PdaTableView& g, const int32_t* tops,
       const int el = g.edge_lo[e], eh = g.edge_hi[e];
       if (el <= byte) lo = max(lo, el); else hi = min(hi, el - 1);
       if (eh >= byte) hi = min(hi, eh); else lo = max(lo, eh + 1);
+      hit |= el <= byte && byte <= eh;
     }
   }
+  return hit;
 }
 
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
@@ -612,12 +637,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         // request of an interval computes it and fills the whole interval
         const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
         int lo, hi;
-        byte_interval(g, set_tops[set], set_n[set], byte, lo, hi);
+        const bool hit = byte_interval(g, set_tops[set], set_n[set], byte, lo, hi);
         cand_lo[tid] = int16_t(lo);
         cand_hi[tid] = int16_t(hi);
-        const uint32_t bit = 1u << (lo & 31);
-        const bool first = (atomicOr(&req[set * 8 + (lo >> 5)], bit) & bit) == 0;
-        cand_res[tid] = first ? 0 : -4;
+        if (!hit) {
+          for (int x = lo; x <= hi; ++x) T[set * 256 + x] = kTDead;
+          cand_res[tid] = -4;
+        } else {
+          const uint32_t bit = 1u << (lo & 31);
+          const bool first = (atomicOr(&req[set * 8 + (lo >> 5)], bit) & bit) == 0;
+          cand_res[tid] = first ? 0 : -4;
+        }
       }
       __syncthreads();
       {
