@@ -73,7 +73,7 @@ _SIGNATURES = {
     "bpd_pda_compute_mask": (cint, [C.POINTER(PdaTableC), C.POINTER(TokenBytesC), vp, vp, i64,
                                     vp, vp, sz, vp]),
     "bpd_pda_advance": (cint, [C.POINTER(PdaTableC), C.POINTER(TokenBytesC), vp, vp, vp, cint,
-                               i64, vp, vp, vp, vp, vp]),
+                               i64, vp, vp, vp, vp, vp, sz, vp]),
     "bpd_host_pda_apply_mask": (cint, [C.POINTER(PdaTableC), C.POINTER(TokenBytesC), vp, vp, vp,
                                        i64, vp, cint, i64, f64]),
     "bpd_host_pda_compute_mask": (cint, [C.POINTER(PdaTableC), C.POINTER(TokenBytesC), vp, vp,

@@ -181,23 +181,48 @@ struct MemoWs {
   int32_t* pool;      // [rows, kMemoSets, kConfigWords]
   int32_t* cand;      // [rows, kMemoReq, kConfigWords]
   int32_t* overflow;  // [rows]
+  int32_t* meta;      // [rows, 4]: valid, tag low, tag high, unused
+  uint32_t* table;    // [rows, kMemoSets * 64]: the row's transition table after the mask
   uint4* tok16;       // [vocab] first 16 bytes of each token, zero padded
 };
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
-  return sets + (r * sizeof(int32_t) + 255) / 256 * 256 + v * sizeof(uint4);
+  return sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4);
 }
 
 MemoWs memo_ws(void* base, int64_t rows) {
   MemoWs w;
+  const size_t r = size_t(rows);
   w.pool = static_cast<int32_t*>(base);
-  w.cand = w.pool + size_t(rows) * kMemoSets * kConfigWords;
-  w.overflow = w.cand + size_t(rows) * kMemoReq * kConfigWords;
-  w.tok16 = reinterpret_cast<uint4*>(reinterpret_cast<char*>(w.overflow) +
-                                     (size_t(rows) * sizeof(int32_t) + 255) / 256 * 256);
+  w.cand = w.pool + r * kMemoSets * kConfigWords;
+  w.overflow = w.cand + r * kMemoReq * kConfigWords;
+  char* p = reinterpret_cast<char*>(w.overflow) + align256(r * 4);
+  w.meta = reinterpret_cast<int32_t*>(p);
+  p += align256(r * 16);
+  w.table = reinterpret_cast<uint32_t*>(p);
+  p += r * kMemoSets * 256;
+  w.tok16 = reinterpret_cast<uint4*>(p);
   return w;
+}
+
+// Identity of the grammar and token tables a workspace's transition tables
+// were built for (the commit reuses them only for the same tables).
+uint64_t memo_tag(const BpdPdaTable* g, const BpdTokenBytes* toks, int64_t rows) {
+  uint64_t h = 1469598103934665603ull ^ uint64_t(rows);
+  auto mix = [&](uint64_t x) { h = (h ^ x) * 1099511628211ull; };
+  mix(reinterpret_cast<uintptr_t>(g->edge_offsets));
+  mix(reinterpret_cast<uintptr_t>(g->edge_kind));
+  mix(reinterpret_cast<uintptr_t>(g->accept));
+  mix(uint64_t(uint32_t(g->num_states)));
+  mix(uint64_t(uint32_t(g->num_edges)));
+  mix(reinterpret_cast<uintptr_t>(toks->offsets));
+  mix(reinterpret_cast<uintptr_t>(toks->bytes));
+  mix(uint64_t(uint32_t(toks->vocab_size)));
+  return h;
 }
 
 // tok16[t] = the first 16 bytes of token t (little-endian words, zero padded)
@@ -464,7 +489,7 @@ __device__ inline bool byte_interval(const PdaTableView& g, const int32_t* tops,
 }
 
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
-                                                                     int table_in_lds) {
+                                                                     int table_in_lds, uint64_t tag) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
@@ -744,7 +769,15 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (st[j] == 1) atomicOr(&vbits[tk[j] >> 5], 1u << (tk[j] & 31));
   }
   __syncthreads();
-  if (tid == 0) ws.overflow[b] = overflowed;
+  // keep the transition table for the commit of this step
+  uint32_t* tout = ws.table + b * (kMemoSets * 64);
+  for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) tout[i] = T32[i];
+  if (tid == 0) {
+    ws.overflow[b] = overflowed;
+    ws.meta[b * 4 + 0] = dead_row ? 0 : 1;
+    ws.meta[b * 4 + 1] = int32_t(uint32_t(tag));
+    ws.meta[b * 4 + 2] = int32_t(uint32_t(tag >> 32));
+  }
   if (overflowed) return;  // the direct walk writes this row
   if (!a.logits) {
     for (int w = tid; w < vwords && w < a.words; w += kMemoThreads) a.bits[b * a.words + w] = vbits[w];
@@ -851,6 +884,99 @@ __global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a)
     if (a.status) a.status[b] = a.broken[row] ? -1 : 1;
   } else if (a.status) {
     a.status[b] = ok ? 1 : -1;
+  }
+}
+
+// Commit with the mask's transition tables: one wave per row.  When the
+// workspace row holds the tables of this config-set (same meaningful words as
+// its set 0, same grammar and tokens), the token's bytes but the last are
+// walked through the table and the last byte is stepped with advance_byte
+// from the interned set reached, so the written config-set has the raw words
+// of the direct walk.  Otherwise (or when the table walk meets an entry the
+// mask left unresolved) every byte is stepped with advance_byte.
+constexpr int kCommitWaves = 4;
+
+__global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(AdvanceArgs a, MemoWs ws,
+                                                                               uint64_t tag) {
+  __shared__ int32_t bufs[kCommitWaves][2][kConfigWords];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t b = int64_t(blockIdx.x) * kCommitWaves + wave;
+  if (b >= a.rows) return;
+  const int64_t row = a.slots ? a.slots[b] : b;
+  int32_t* cfg = a.configs + row * kConfigWords;
+  int32_t* x = bufs[wave][0];
+  int32_t* y = bufs[wave][1];
+  for (int k = lane; k < kConfigWords; k += kWave) x[k] = cfg[k];
+  wave_sync();
+  const int64_t t = a.tok_dtype == BPD_INDEX_I64
+                        ? int64_t(int32_t(static_cast<const int64_t*>(a.tokens)[b]))
+                        : int64_t(static_cast<const int32_t*>(a.tokens)[b]);
+  bool ok;
+  if (t < 0 || t >= a.vocab) {
+    if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
+    ok = false;
+  } else if (!config_ok(x, a.g.num_states, lane)) {
+    if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_STATE_RANGE);
+    ok = false;
+  } else if (t == a.eos) {
+    ok = is_complete(a.g, ConstFlatView{x});
+  } else {
+    const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
+    ok = true;
+    if (s < e) {
+      // set reached after all bytes but the last, via the mask's table
+      int cur = -1;  // -1: use the direct walk
+      const int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
+      if (ws.pool && ws.meta[b * 4] == 1 && ws.meta[b * 4 + 1] == int32_t(uint32_t(tag)) &&
+          ws.meta[b * 4 + 2] == int32_t(uint32_t(tag >> 32)) && coop_same(x, pool, lane)) {
+        const uint8_t* T = reinterpret_cast<const uint8_t*>(ws.table + b * (kMemoSets * 64));
+        cur = 0;
+        for (int32_t i = s; i + 1 < e; ++i) {
+          const uint8_t nx = T[cur * 256 + a.tok_bytes[i]];
+          if (nx == kTDead) {
+            cur = -2;
+            break;
+          }
+          if (nx >= kTOverflow) {
+            cur = -1;
+            break;
+          }
+          cur = nx;
+        }
+      }
+      if (cur == -2) {
+        ok = false;
+      } else if (cur >= 0) {
+        const int32_t* src = cur == 0 ? x : pool + cur * kConfigWords;
+        if (cur != 0) {
+          for (int k = lane; k < kConfigWords; k += kWave) y[k] = src[k];
+          wave_sync();
+          for (int k = lane; k < kConfigWords; k += kWave) x[k] = y[k];
+          wave_sync();
+        }
+        ok = coop_advance_byte(a.g, x, y, a.tok_bytes[e - 1], lane);
+        if (ok)
+          for (int k = lane; k < kConfigWords; k += kWave) cfg[k] = y[k];
+      } else {
+        for (int32_t i = s; i < e && ok; ++i) {
+          ok = coop_advance_byte(a.g, x, y, a.tok_bytes[i], lane);
+          int32_t* tmp = x;
+          x = y;
+          y = tmp;
+        }
+        if (ok)
+          for (int k = lane; k < kConfigWords; k += kWave) cfg[k] = x[k];
+      }
+    }
+  }
+  if (lane == 0) {
+    if (a.ok) a.ok[b] = ok ? 1 : 0;
+    if (a.broken) {
+      if (!ok) a.broken[row] = 1;
+      if (a.status) a.status[b] = a.broken[row] ? -1 : 1;
+    } else if (a.status) {
+      a.status[b] = ok ? 1 : -1;
+    }
   }
 }
 
@@ -997,7 +1123,7 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&pda_memo_mask_kernel)));
     const bool in_lds = fa.sharedSizeBytes + tab_bytes <= size_t(max_lds);
     pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
-        a, ws, max_sets, in_lds ? 1 : 0);
+        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows));
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
   }
@@ -1028,7 +1154,8 @@ extern "C" int bpd_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* t
 extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,
                                const int64_t* slots, const void* tokens, int token_dtype,
                                int64_t rows, uint8_t* ok, uint8_t* broken, int32_t* status,
-                               int32_t* err, void* stream) {
+                               int32_t* err, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   if (int rc = check_tables(g, toks)) return rc;
   BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64,
               "unknown token dtype code %d", token_dtype);
@@ -1049,6 +1176,16 @@ extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, 
   a.broken = broken;
   a.status = status;
   a.err = err;
+  if (workspace) {
+    // the mask's workspace of the same batch: reuse its transition tables
+    const size_t need = memo_ws_bytes(rows, toks->vocab_size);
+    BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
+    const MemoWs ws = memo_ws(workspace, rows);
+    const unsigned blocks = unsigned((rows + kCommitWaves - 1) / kCommitWaves);
+    pda_memo_advance_kernel<<<blocks, kCommitWaves * kWave, 0, as_stream(stream)>>>(a, ws, memo_tag(g, toks, rows));
+    BPD_LAUNCHED();
+    return BPD_OK;
+  }
   const unsigned blocks = unsigned((rows + kCommitRows - 1) / kCommitRows);
   pda_advance_kernel<<<blocks, kCommitRows, 0, as_stream(stream)>>>(a);
   BPD_LAUNCHED();

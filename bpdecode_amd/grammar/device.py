@@ -353,8 +353,11 @@ def pda_step(configs, g: PdaTensors, token_ids, slots=None, broken=None, err=Non
     status = torch.empty(B, dtype=torch.int32, device=dev)
     code = _lib.index_code(tk.dtype)
     if dev.type == "cuda":
+        stream = _lib.stream_of(dev)
+        ws, ws_bytes = g.mask_workspace(B, dev, stream)
         check(lib().bpd_pda_advance(g.c_table(), g.c_tokens(), ptr(configs), ptr(sl), ptr(tk), code, B,
-                                    ptr(ok), ptr(broken), ptr(status), ptr(err), _lib.stream_of(dev)))
+                                    ptr(ok), ptr(broken), ptr(status), ptr(err), ptr(ws), ws_bytes,
+                                    stream))
     else:
         check(lib().bpd_host_pda_advance(g.c_table(), g.c_tokens(), ptr(configs), ptr(sl), ptr(tk),
                                          code, B, ptr(ok), ptr(broken), ptr(status)))

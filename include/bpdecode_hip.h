@@ -197,10 +197,15 @@ int bpd_pda_compute_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
  * completeness (advance_state_pda_batch, pda_cpu.cpp:35-54).  With broken
  * non-NULL, broken[row(b)] |= !ok[b] and status[b] = broken[row(b)] ? -1 : 1
  * (CFGConstraintBatch.commit, device.py:268-283); without it status[b] =
- * ok[b] ? 1 : -1.  ok, broken and status may each be NULL. */
+ * ok[b] ? 1 : -1.  ok, broken and status may each be NULL.  With the
+ * workspace of the preceding bpd_pda_apply_mask / bpd_pda_compute_mask of the
+ * same rows (bpd_pda_workspace_bytes(rows, vocab) bytes, same stream), the
+ * token is walked through the transition tables that call built, and only
+ * its last byte is stepped; results are identical (raw words included). */
 int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, int32_t* configs,
                     const int64_t* slots, const void* tokens, int token_dtype, int64_t rows,
-                    uint8_t* ok, uint8_t* broken, int32_t* status, int32_t* err, void* stream);
+                    uint8_t* ok, uint8_t* broken, int32_t* status, int32_t* err,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 int bpd_host_pda_apply_mask(const BpdPdaTable* g, const BpdTokenBytes* toks,
                             const int32_t* configs, const int64_t* slots,

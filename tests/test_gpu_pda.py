@@ -176,3 +176,36 @@ def test_json_direct_walk_equals_memo(dev, json_case):
                                      None, 0, _lib.stream_of(dev)))
     memo = pda_compute_mask(gd, pool)
     assert torch.equal(direct.cpu(), memo.cpu())
+
+
+@pytest.mark.parametrize("limit", [None, "1"])
+def test_json_commit_paths_match_oracle(dev, json_case, monkeypatch, limit):
+    """Commit after the mask of the same config-sets (transition tables
+    reused; with the set limit lowered they hold overflow entries), after a
+    mask of other config-sets (stale tables) and with no mask at all: raw
+    config words and ok flags as the oracle's."""
+    vocab, g, t = json_case
+    _log(f"case json commit paths limit={limit}")
+    if limit:
+        monkeypatch.setenv("BPD_PDA_MEMO_SETS", limit)
+    gd = g.to(dev)
+    cfgs = _json_configs(g, 16, seed=41)
+    other = _json_configs(g, 16, seed=42)
+    rng = np.random.default_rng(3)
+    for mode in ("fresh", "stale", "none"):
+        pool = cfgs.to(dev)
+        if mode == "fresh":
+            pda_compute_mask(gd, pool)
+        elif mode == "stale":
+            pda_compute_mask(gd, other.to(dev))
+        bits = OP.compute_mask(t, cfgs.numpy())
+        allowed = [np.nonzero(np.unpackbits(bits[r].view(np.uint8), bitorder="little")[:vocab.size])[0]
+                   for r in range(16)]
+        # mostly allowed tokens, a few arbitrary ones (rejected paths)
+        toks = [int(rng.choice(a)) if (len(a) and r % 4) else int(rng.integers(0, vocab.size))
+                for r, a in enumerate(allowed)]
+        mirror = cfgs.numpy().copy()
+        ok_o = OP.advance(t, mirror, np.array(toks, dtype=np.int32))
+        ok, _ = pda_step(pool, gd, torch.tensor(toks, dtype=torch.int32, device=dev))
+        assert ok.cpu().numpy().astype(bool).tolist() == ok_o.astype(bool).tolist(), mode
+        assert np.array_equal(pool.cpu().numpy(), mirror), mode
