@@ -1,0 +1,143 @@
+"""HF and vLLM adapters on top of the constraint step (the scenarios of the
+reference's test_hf.py / test_vllm.py): no model is loaded, a fixed bias
+vector stands in for the model and the generate() / vLLM calling conventions
+are driven by hand. Each scenario runs on CPU tensors and, marked ``gpu``, on
+the device. Ground truth is the host RegexConstraint (token-by-token DFA)."""
+
+from __future__ import annotations
+
+import re
+
+import pytest
+import torch
+
+from bpdecode_amd.hf import RegexLogitsProcessor as HFRegex
+from bpdecode_amd.reference import RegexConstraint
+from bpdecode_amd.tokenizer import Vocabulary
+from bpdecode_amd.vllm import BatchConstraintState, RegexLogitsProcessor, RegexLogitsProcessorFactory
+
+TOKENS = ["0", "1", "2", "3", "4", "5", "6", "7", "8", "9", ".", "-", " ", "x", "</s>"]
+VOCAB = Vocabulary.from_tokens(TOKENS, eos_id=len(TOKENS) - 1)
+DECIMAL = "-?[0-9]+(\\.[0-9]+)?"
+DEVICES = ["cpu", pytest.param("cuda", marks=pytest.mark.gpu)]
+
+
+def _decode(ids):
+    return "".join(TOKENS[i] for i in ids if i != VOCAB.eos_id)
+
+
+def _hf_greedy(pattern, bias, device, max_new=12):
+    lp = HFRegex(pattern, VOCAB, device=device)
+    input_ids = torch.zeros(1, 1, dtype=torch.long, device=device)
+    out = []
+    for _ in range(max_new):
+        scores = lp(input_ids, bias.clone().unsqueeze(0).to(device))
+        nxt = int(scores[0].argmax())
+        out.append(nxt)
+        if nxt == VOCAB.eos_id:
+            break
+        input_ids = torch.cat([input_ids, torch.tensor([[nxt]], device=device)], dim=1)
+    return out
+
+
+def _valid_prefix(pattern, ids):
+    ref = RegexConstraint(pattern, VOCAB)
+    for tok in ids:
+        if tok == VOCAB.eos_id:
+            return ref.is_complete()
+        if not ref.accepts(tok):
+            return False
+        ref.advance(tok)
+    return True
+
+
+@pytest.mark.parametrize("device", DEVICES)
+@pytest.mark.parametrize("pattern", [DECIMAL, "[12][0-9][0-9]", "[0-9]+ [0-9]+"])
+def test_hf_every_step_stays_a_valid_prefix(device, pattern):
+    bias = torch.zeros(VOCAB.size)
+    bias[TOKENS.index("x")] = 10.0
+    ids = _hf_greedy(pattern, bias, device)
+    assert TOKENS.index("x") not in ids
+    assert _valid_prefix(pattern, ids)
+
+
+@pytest.mark.parametrize("device", DEVICES)
+def test_hf_eos_only_when_complete(device):
+    pattern = "[12][0-9][0-9]"
+    bias = torch.zeros(VOCAB.size)
+    bias[VOCAB.eos_id] = 10.0
+    ids = _hf_greedy(pattern, bias, device)
+    assert ids[-1] == VOCAB.eos_id and re.fullmatch(pattern, _decode(ids))
+
+
+@pytest.mark.parametrize("device", DEVICES)
+def test_hf_tracks_reference_and_batches_rows(device):
+    lp = HFRegex(DECIMAL, VOCAB, device=device)
+    refs = [RegexConstraint(DECIMAL, VOCAB) for _ in range(2)]
+    seqs = [[TOKENS.index(c) for c in "-4.2"], [TOKENS.index(c) for c in "17.05"]]
+    input_ids = torch.zeros(2, 1, dtype=torch.long, device=device)
+    for step in range(4):
+        scores = lp(input_ids, torch.zeros(2, VOCAB.size, device=device)).cpu()
+        for r in range(2):
+            got = {i for i in range(VOCAB.size) if scores[r, i] == 0.0}
+            assert got == set(refs[r].allowed_ids())
+            refs[r].advance(seqs[r][step])
+        nxt = torch.tensor([[seqs[0][step]], [seqs[1][step]]], device=device)
+        input_ids = torch.cat([input_ids, nxt], dim=1)
+
+
+def _vllm_greedy(proc, bias, max_new=12):
+    past = []
+    for _ in range(max_new):
+        nxt = int(proc(past, bias.clone()).argmax())
+        if nxt == VOCAB.eos_id:
+            break
+        past.append(nxt)
+    return past
+
+
+@pytest.mark.parametrize("device", DEVICES)
+def test_vllm_request_processor(device):
+    bias = torch.zeros(VOCAB.size, device=device)
+    bias[TOKENS.index("x")] = 9.0
+    proc = RegexLogitsProcessor(DECIMAL, VOCAB, device=device)
+    past = _vllm_greedy(proc, bias)
+    assert TOKENS.index("x") not in past and _valid_prefix(DECIMAL, past)
+    # tracks the reference token by token, and restarts when the history shrinks
+    proc = RegexLogitsProcessorFactory(VOCAB, device=device).make(DECIMAL)
+    ref = RegexConstraint(DECIMAL, VOCAB)
+    past = []
+    for tok in [TOKENS.index(c) for c in "-4.2"]:
+        logits = proc(past, torch.zeros(VOCAB.size, device=device)).cpu()
+        assert {i for i in range(VOCAB.size) if logits[i] == 0.0} == set(ref.allowed_ids())
+        ref.advance(tok)
+        past.append(tok)
+    fresh = proc([], torch.zeros(VOCAB.size, device=device)).cpu()
+    assert {i for i in range(VOCAB.size) if fresh[i] == 0.0} == set(RegexConstraint(DECIMAL, VOCAB).allowed_ids())
+
+
+@pytest.mark.parametrize("device", DEVICES)
+@pytest.mark.parametrize("mask_cache", [True, False])
+def test_vllm_batch_state_slot_events(device, mask_cache):
+    st = BatchConstraintState(VOCAB, device=device, mask_cache=mask_cache, capacity=8)
+    st.add(0, DECIMAL)
+    st.add(2, DECIMAL)
+    gen = {0: [TOKENS.index(c) for c in "-1"], 2: [TOKENS.index(c) for c in "3."]}
+    for row, ids in gen.items():
+        st.advance(row, ids)
+    st.move(2, 5)
+    st.advance(5, gen[2] + [TOKENS.index("7")])
+    logits = torch.zeros(6, VOCAB.size, device=device)
+    st.mask(logits)
+    logits = logits.cpu()
+    for row, text in ((0, "-1"), (5, "3.7")):
+        ref = RegexConstraint(DECIMAL, VOCAB)
+        for c in text:
+            ref.advance(TOKENS.index(c))
+        assert {i for i in range(VOCAB.size) if logits[row, i] == 0.0} == set(ref.allowed_ids())
+    for row in (1, 2, 3, 4):
+        assert torch.all(logits[row] == 0.0)  # rows without a request are untouched
+    assert st.is_complete(5) and st.is_complete(0)
+    st.remove(0)
+    with pytest.raises(KeyError):  # as the reference: the row no longer exists
+        st.is_complete(0)
