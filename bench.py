@@ -131,8 +131,9 @@ def calibrate_copy(mb: int) -> None:
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(rows shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the constraint "
+              "step is row-parallel, so N GPUs each run it on their own B/N rows with no exchange, "
+              "and the one-GPU figure is the per-GPU rate", file=sys.stderr)
         return 2
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)

@@ -488,6 +488,15 @@ __device__ inline bool byte_interval(const PdaTableView& g, const int32_t* tops,
   return hit;
 }
 
+// byte p of the token at walk position k (its first 16 bytes are packed)
+__device__ __forceinline__ int long_byte(const MaskArgs& a, int64_t k, int32_t p) {
+  const int64_t t = a.order ? a.order[k] : k;
+  return a.tok_bytes[a.tok_off[t] + p];
+}
+
+// verdicts of a token in the memoised walk, past every set id
+constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
+
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
                                                                      int table_in_lds, uint64_t tag) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
@@ -509,6 +518,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
   __shared__ int pool_count, nreq, row_flags, overflowed;
+  __shared__ uint32_t h0_sh;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
   const int tid = threadIdx.x;
@@ -570,6 +580,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       const ConstFlatView C{row_cfg};
       row_flags = dead ? 1 : ((is_complete(a.g, C) ? 2 : 0) | (C.n() > 0 ? 4 : 0));
       pool_hash[0] = h0;
+      h0_sh = h0;
     }
     if (tid < kMaxConfigs) {
       const int n = dead ? 0 : row_cfg[0];
@@ -584,51 +595,50 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   const bool dead_row = (flags & 1) != 0;
 
   const int64_t V = a.vocab;
-  for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
-    // per token: length, position, set id, status and its first 16 bytes
-    int32_t pos[kMemoTok], len[kMemoTok], tk[kMemoTok];
-    int cur[kMemoTok], st[kMemoTok];  // st: 0 walking, 1 allowed, 2 rejected, 3 overflow, 4 none
+  bool retry = false;  // the tile is being walked again after a pool reset
+  for (int64_t tile = 0; tile < V;) {
+    // per token: length, position, state and its first 16 bytes; the state
+    // is the current set id (< 256) while walking, else kAllowed / kRejected
+    // / kNone. Token j of the thread is order[tile + j * kMemoThreads + tid].
+    int32_t pos[kMemoTok], len[kMemoTok];
+    int cur[kMemoTok];
     uint4 pk[kMemoTok];
 #pragma unroll
     for (int j = 0; j < kMemoTok; ++j) {
       const int64_t k = tile + int64_t(j) * kMemoThreads + tid;
       const int64_t t = k < V ? (a.order ? a.order[k] : k) : k;
-      tk[j] = int32_t(t);
       pos[j] = len[j] = 0;
-      cur[j] = 0;
       pk[j] = make_uint4(0u, 0u, 0u, 0u);
       if (t >= V) {
-        st[j] = 4;
+        cur[j] = kNone;
       } else if (dead_row) {
-        st[j] = 2;
+        cur[j] = kRejected;
       } else if (t == a.eos) {
-        st[j] = (flags & 2) ? 1 : 2;
+        cur[j] = (flags & 2) ? kAllowed : kRejected;
       } else {
         len[j] = a.tok_off[t + 1] - a.tok_off[t];
         pk[j] = ws.tok16[t];
-        st[j] = len[j] == 0 ? ((flags & 4) ? 1 : 2) : 0;
+        cur[j] = len[j] == 0 ? ((flags & 4) ? kAllowed : kRejected) : 0;
       }
     }
     while (true) {
       bool waiting = false;
 #pragma unroll
       for (int j = 0; j < kMemoTok; ++j) {
-        while (st[j] == 0) {
+        while (cur[j] < kWalkEnd) {
           if (pos[j] == len[j]) {
-            st[j] = 1;
+            cur[j] = kAllowed;
             break;
           }
-          const int byte = pos[j] < 16 ? packed_byte(pk[j], pos[j]) : int(a.tok_bytes[a.tok_off[tk[j]] + pos[j]]);
+          const int byte = pos[j] < 16 ? packed_byte(pk[j], pos[j]) : long_byte(a, tile + int64_t(j) * kMemoThreads + tid, pos[j]);
           const uint8_t nx = T[cur[j] * 256 + byte];
           if (nx == kTUnknown) {
             atomicOr(&req[cur[j] * 8 + (byte >> 5)], 1u << (byte & 31));
             waiting = true;
             break;
           }
-          if (nx == kTDead) {
-            st[j] = 2;
-          } else if (nx == kTOverflow) {
-            st[j] = 3;
+          if (nx == kTDead || nx == kTOverflow) {
+            cur[j] = kRejected;  // an overflow entry only exists in a tile that is abandoned
           } else {
             cur[j] = nx;
             ++pos[j];
@@ -761,12 +771,42 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
       }
       __syncthreads();
+      if (overflowed) break;
+    }
+    if (overflowed) {
+      // the pool is full: drop every interned set and transition and walk the
+      // tile again from an empty pool; a tile that fills the pool twice leaves
+      // the whole row to the direct walk
+      if (retry) break;
+      for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
+      for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
+      if (tid < kMaxConfigs) {
+        const int n0 = row_cfg[0];
+        const int d = tid < n0 ? row_cfg[2 + tid] : 0;
+        set_tops[0][tid] = d > 0 ? row_cfg[kF + tid * kMaxDepth + d - 1] : -1;
+        if (tid == 0) set_n[0] = n0;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        pool_count = 1;
+        pool_hash[0] = h0_sh;
+        overflowed = 0;
+      }
+      __syncthreads();
+      retry = true;
+      continue;
     }
 
     // allowed tokens of the tile into the row's bitmap
 #pragma unroll
     for (int j = 0; j < kMemoTok; ++j)
-      if (st[j] == 1) atomicOr(&vbits[tk[j] >> 5], 1u << (tk[j] & 31));
+      if (cur[j] == kAllowed) {
+        const int64_t k = tile + int64_t(j) * kMemoThreads + tid;
+        const int32_t t = int32_t(a.order ? a.order[k] : k);
+        atomicOr(&vbits[t >> 5], 1u << (t & 31));
+      }
+    retry = false;
+    tile += int64_t(kMemoThreads) * kMemoTok;
   }
   __syncthreads();
   // keep the transition table for the commit of this step

@@ -139,10 +139,11 @@ def test_json_batch_api_b64(dev, json_case):
         assert np.array_equal(batch._configs.cpu().numpy(), mirror)
 
 
-@pytest.mark.parametrize("limit", ["1", "3"])
+@pytest.mark.parametrize("limit", ["1", "3", "12", "40"])
 def test_json_memo_overflow_rows_match_oracle(dev, json_case, monkeypatch, limit):
-    """With the interned-set limit lowered, rows run out of sets and are
-    finished by the direct-walk kernel; masks stay identical."""
+    """With the interned-set limit lowered, rows run out of sets: a tile that
+    fills the pool restarts from an empty pool, and a row whose tile fills it
+    twice is finished by the direct-walk kernel; masks stay identical."""
     vocab, g, t = json_case
     _log(f"case json V=151936 B=8 memo set limit {limit}")
     monkeypatch.setenv("BPD_PDA_MEMO_SETS", limit)
@@ -178,7 +179,7 @@ def test_json_direct_walk_equals_memo(dev, json_case):
     assert torch.equal(direct.cpu(), memo.cpu())
 
 
-@pytest.mark.parametrize("limit", [None, "1"])
+@pytest.mark.parametrize("limit", [None, "1", "12"])
 def test_json_commit_paths_match_oracle(dev, json_case, monkeypatch, limit):
     """Commit after the mask of the same config-sets (transition tables
     reused; with the set limit lowered they hold overflow entries), after a
