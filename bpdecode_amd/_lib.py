@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
@@ -50,6 +50,7 @@ class SoftClassesC(C.Structure):
         ("num_classes", i32), ("num_members", i32), ("num_pieces", i32), ("num_pairs", i32),
         ("class_off", vp), ("class_tok", vp), ("class_piece", vp), ("piece_off", vp),
         ("state_off", vp), ("pair_class", vp), ("pair_next", vp), ("token_class", vp),
+        ("token_class16", vp),
     ]
 
 

@@ -375,12 +375,20 @@ __device__ inline int32_t ord_of(float x) {
 }
 __device__ inline float float_of_ord(int32_t i) { return __int_as_float(i >= 0 ? i : i ^ 0x7FFFFFFF); }
 
+// lse_merge by the hardware exponential (the prior kernels' reductions)
+__device__ inline Lse lse_merge_fast(Lse a, Lse b) {
+  const float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return Lse{m, 0.0f};
+  const float mb = m * kLog2e;
+  return Lse{m, a.s * exp_shift(a.m, mb) + b.s * exp_shift(b.m, mb)};
+}
+
 __device__ inline Lse wave_lse(Lse a) {
   for (int o = 32; o > 0; o >>= 1) {
     Lse b;
     b.m = __shfl_xor(a.m, o);
     b.s = __shfl_xor(a.s, o);
-    a = lse_merge(a, b);
+    a = lse_merge_fast(a, b);
   }
   return a;
 }
@@ -398,7 +406,7 @@ __device__ inline Lse block_lse(Lse a) {
   }
   __syncthreads();
   Lse r{-INFINITY, 0.0f};
-  for (int i = 0; i < kThreads / 64; ++i) r = lse_merge(r, Lse{wm[i], ws[i]});
+  for (int i = 0; i < kThreads / 64; ++i) r = lse_merge_fast(r, Lse{wm[i], ws[i]});
   __syncthreads();
   return r;
 }
@@ -456,18 +464,21 @@ size_t prior_ws_bytes(int64_t rows, const PriorPlan& pl, int32_t C, int32_t P) {
 }
 
 size_t prior_lds_bytes(int32_t S, int32_t C, int32_t P, int64_t pairs, bool pairs_in_lds, bool pieces) {
-  size_t n = size_t(C) * 4 + size_t(S) * 8 + size_t(S + 3) / 4 * 4 + size_t(S + 1) * 4;
+  size_t n = size_t(C) * (pieces ? 4 : 8) + size_t(S) * 8 + size_t(S + 3) / 4 * 4 + size_t(S + 1) * 4;
   if (pairs_in_lds) n += size_t(pairs) * 4;
   n = (n + 7) / 8 * 8;
   return pieces ? n + size_t(P) * 8 : n;
 }
 
+__device__ inline int32_t narrow_class(uint32_t c) { return c == 0xFFFFu ? -1 : int32_t(c); }
+
 // Class-atomic stats, grid (G, rows): block g takes tokens
-// [kStatChunk g, kStatChunk (g+1)) of its row.
-template <bool Vec>
+// [kStatChunk g, kStatChunk (g+1)) of its row.  Narrow: the class map is read
+// as uint16 (0xFFFF: no class).
+template <bool Vec, bool Narrow>
 __global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
     const float* __restrict__ logits, int64_t ld, int64_t V, const int32_t* __restrict__ token_class,
-    int32_t C, PriorWs ws) {
+    const uint16_t* __restrict__ token_class16, int32_t C, PriorWs ws) {
   __shared__ int32_t cmax[kLdsClasses];
   __shared__ float csum[kLdsClasses];
   constexpr int kE = 4 * kStatLoads;
@@ -490,7 +501,13 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
       int4 kv = make_int4(-1, -1, -1, -1);
       if (t < V) {
         xv = *reinterpret_cast<const float4*>(row + t);
-        kv = *reinterpret_cast<const int4*>(token_class + t);
+        if (Narrow) {
+          const uint2 n = *reinterpret_cast<const uint2*>(token_class16 + t);
+          kv = make_int4(narrow_class(n.x & 0xFFFFu), narrow_class(n.x >> 16), narrow_class(n.y & 0xFFFFu),
+                         narrow_class(n.y >> 16));
+        } else {
+          kv = *reinterpret_cast<const int4*>(token_class + t);
+        }
       }
       x[4 * u] = xv.x;
       x[4 * u + 1] = xv.y;
@@ -506,7 +523,7 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
     for (int e = 0; e < kE; ++e) {
       const int64_t t = base + int64_t(e) * kPriorThreads + threadIdx.x;
       x[e] = t < V ? row[t] : -INFINITY;
-      k[e] = t < V ? token_class[t] : -1;
+      k[e] = t < V ? (Narrow ? narrow_class(token_class16[t]) : token_class[t]) : -1;
     }
   }
   // chunk logsumexp
@@ -622,9 +639,44 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_pieces_kernel(
 // One block per row: merge the partials into lse[b] and the class sums, run
 // the k-1 rounds with logZ, the class sums and (when they fit) the
 // (class, next) pairs in LDS, and write zcls[b, c] = logZ(next state of
-// class c from s_b) and lse[b].
+// class c from s_b) and lse[b].  The global loads of the prologue are all
+// issued before the first wait.  In a round, a quad of lanes takes one
+// state: each lane folds every fourth pair of the state into a running
+// (max, sum of exp(v - max)), and the quad merges the four by DPP exchanges.
+constexpr int kRoundThreads = 1024;
+constexpr int kQuadLoads = 16;   // pairs per lane in flight
+constexpr int kPairRegs = 8;     // pairs per thread held in registers while they load
+constexpr int kMergeRegs = 4;    // class partials per thread held in registers
+
+// DPP quad permutations: lane i reads lane i ^ 1, lane i ^ 2 of its quad
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+
+template <int Ctrl>
+__device__ inline float quad_read(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), Ctrl, 0xF, 0xF, false));
+}
+
+// (m, s) <- merge of (m, s) with the pair held by the lane Ctrl names
+template <int Ctrl>
+__device__ inline void quad_lse_step(float& m, float& s) {
+  const float mo = quad_read<Ctrl>(m), so = quad_read<Ctrl>(s);
+  const float nm = fmaxf(m, mo);
+  if (nm != -INFINITY) {
+    const float nb = nm * kLog2e;
+    s = s * exp_shift(m, nb) + so * exp_shift(mo, nb);
+  }
+  m = nm;
+}
+
+template <bool PairsInLds>
+__device__ inline uint32_t prior_pair(const uint32_t* pr, const BpdSoftClasses& cls, int32_t i) {
+  if (PairsInLds) return pr[i];
+  return (uint32_t(cls.pair_class[i]) << 16) | uint32_t(cls.pair_next[i]);
+}
+
 template <bool PairsInLds, bool ClassStats>
-__global__ __launch_bounds__(kPriorThreads) void prior_rounds_kernel(
+__global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
     const float* __restrict__ logits, int64_t ld, int32_t S, int G, BpdSoftClasses cls,
     const uint8_t* __restrict__ accept, const uint8_t* __restrict__ live, int32_t eos,
     const int32_t* __restrict__ states, const int64_t* __restrict__ slots, int32_t rounds,
@@ -632,127 +684,156 @@ __global__ __launch_bounds__(kPriorThreads) void prior_rounds_kernel(
   extern __shared__ __align__(16) float lds[];
   __shared__ float lse_sh;
   const int64_t b = blockIdx.x;
-  const int32_t C = cls.num_classes, P = cls.num_pieces;
-  if (threadIdx.x < 64) {
-    Lse r{-INFINITY, 0.0f};
-    for (int i = threadIdx.x; i < G; i += 64)
-      r = lse_merge(r, Lse{ws.part[(b * G + i) * 2], ws.part[(b * G + i) * 2 + 1]});
-    r = wave_lse(r);
-    if (threadIdx.x == 0) lse_sh = lse_value(r);
-  }
-  float* lc = lds;           // [C] class logsumexp (unnormalised), later zcls
-  float* z0 = lc + C;        // [S]
-  float* z1 = z0 + S;        // [S]
-  uint8_t* flag = reinterpret_cast<uint8_t*>(z1 + S);  // [S] bit 0 live, bit 1 accept
+  const int tid = threadIdx.x;
+  const int32_t C = cls.num_classes, P = cls.num_pieces, NP = cls.num_pairs;
+  float* lc = lds;                                        // [C] class logsumexp, later zcls
+  int32_t* lci = reinterpret_cast<int32_t*>(lc);          // [C] class max (ord) while merging
+  float* cs = lc + C;                                     // [C] class sums while merging (ClassStats)
+  float* z0 = ClassStats ? cs + C : cs;                   // [S]
+  float* z1 = z0 + S;                                     // [S]
+  uint8_t* flag = reinterpret_cast<uint8_t*>(z1 + S);     // [S] bit 0 live, bit 1 accept
   int32_t* so = reinterpret_cast<int32_t*>(z1 + S + (S + 3) / 4);  // [S + 1]
-  uint32_t* pr = reinterpret_cast<uint32_t*>(so + S + 1);  // [pairs] class << 16 | next (PairsInLds)
+  uint32_t* pr = reinterpret_cast<uint32_t*>(so + S + 1); // [pairs] class << 16 | next (PairsInLds)
+
+  // global loads: the EOS logit, the pairs, the class partials, the row
+  // partials, the state flags and offsets
+  const float x_eos = eos >= 0 ? logits[b * ld + eos] : -INFINITY;
+  uint32_t pv[kPairRegs];
+  if (PairsInLds) {
+#pragma unroll
+    for (int u = 0; u < kPairRegs; ++u) {
+      const int32_t j = tid + u * kRoundThreads;
+      pv[u] = j < NP ? (uint32_t(cls.pair_class[j]) << 16) | uint32_t(cls.pair_next[j]) : 0u;
+    }
+  }
+  const int CG = ClassStats ? C * G : 0;
+  const float* mid = ws.mid + b * int64_t(G) * C * 2;  // [G][C] (max, sum)
+  float2 mv[kMergeRegs];
   if (ClassStats) {
-    // class c: merge of the G chunk partials (loads issued 4 at a time)
-    for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
-      Lse a{-INFINITY, 0.0f};
-      const float* src = ws.mid + (b * G) * int64_t(C) * 2 + 2 * c;
-      int i = 0;
-      for (; i + 4 <= G; i += 4) {
-        float2 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float2*>(src + int64_t(i + u) * C * 2);
+    for (int u = 0; u < kMergeRegs; ++u) {
+      const int e = tid + u * kRoundThreads;
+      mv[u] = e < CG ? *reinterpret_cast<const float2*>(mid + 2 * int64_t(e)) : make_float2(-INFINITY, 0.0f);
+    }
+  }
+  Lse part{-INFINITY, 0.0f};
+  if (tid < 64 && tid < G) part = Lse{ws.part[(b * G + tid) * 2], ws.part[(b * G + tid) * 2 + 1]};
+  const uint8_t lv0 = tid < S ? live[tid] : 0;
+  const uint8_t ac0 = tid < S ? accept[tid] : 0;
+  const int32_t so0 = tid <= S ? cls.state_off[tid] : 0;
+
+  if (tid < 64) {
+    for (int i = tid + 64; i < G; i += 64) part = lse_merge(part, Lse{ws.part[(b * G + i) * 2], ws.part[(b * G + i) * 2 + 1]});
+    part = wave_lse(part);
+    if (tid == 0) lse_sh = lse_value(part);
+  }
+  if (ClassStats) {
+    for (int32_t c = tid; c < C; c += kRoundThreads) {
+      lci[c] = ord_of(-INFINITY);
+      cs[c] = 0.0f;
+    }
+  }
+  for (int32_t s = tid; s < S; s += kRoundThreads) {
+    const bool lv = (s == tid ? lv0 : live[s]) != 0;
+    const bool ac = (s == tid ? ac0 : accept[s]) != 0;
+    flag[s] = uint8_t((lv ? 1 : 0) | (ac ? 2 : 0));
+    z0[s] = lv ? 0.0f : -INFINITY;
+  }
+  for (int32_t s = tid; s <= S; s += kRoundThreads) so[s] = s == tid ? so0 : cls.state_off[s];
+  if (PairsInLds) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a = lse_merge(a, Lse{v[u].x, v[u].y});
-      }
-      for (; i < G; ++i) {
-        const float2 v = *reinterpret_cast<const float2*>(src + int64_t(i) * C * 2);
-        a = lse_merge(a, Lse{v.x, v.y});
-      }
-      lc[c] = lse_value(a);
+    for (int u = 0; u < kPairRegs; ++u) {
+      const int32_t j = tid + u * kRoundThreads;
+      if (j < NP) pr[j] = pv[u];
+    }
+    for (int32_t j = tid + kPairRegs * kRoundThreads; j < NP; j += kRoundThreads)
+      pr[j] = (uint32_t(cls.pair_class[j]) << 16) | uint32_t(cls.pair_next[j]);
+  }
+  __syncthreads();
+  if (ClassStats) {
+    // class c: max over the G chunk partials, then the rescaled sum
+#pragma unroll
+    for (int u = 0; u < kMergeRegs; ++u) {
+      const int e = tid + u * kRoundThreads;
+      if (e < CG && mv[u].x != -INFINITY) atomicMax(&lci[e % C], ord_of(mv[u].x));
+    }
+    for (int e = tid + kMergeRegs * kRoundThreads; e < CG; e += kRoundThreads) {
+      const float m = mid[2 * int64_t(e)];
+      if (m != -INFINITY) atomicMax(&lci[e % C], ord_of(m));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kMergeRegs; ++u) {
+      const int e = tid + u * kRoundThreads;
+      if (e < CG && mv[u].x != -INFINITY)
+        atomicAdd(&cs[e % C], mv[u].y * exp_shift(mv[u].x, float_of_ord(lci[e % C]) * kLog2e));
+    }
+    for (int e = tid + kMergeRegs * kRoundThreads; e < CG; e += kRoundThreads) {
+      const float2 v = *reinterpret_cast<const float2*>(mid + 2 * int64_t(e));
+      if (v.x != -INFINITY) atomicAdd(&cs[e % C], v.y * exp_shift(v.x, float_of_ord(lci[e % C]) * kLog2e));
+    }
+    __syncthreads();
+    for (int32_t c = tid; c < C; c += kRoundThreads) {
+      const float s = cs[c];
+      lc[c] = s > 0.0f ? float_of_ord(lci[c]) + logf(s) : -INFINITY;
     }
   } else {
     // [P] piece (max, sum) pairs, 8-byte aligned after the pairs
-    const uintptr_t pc_at = reinterpret_cast<uintptr_t>(pr + (PairsInLds ? cls.num_pairs : 0));
+    const uintptr_t pc_at = reinterpret_cast<uintptr_t>(pr + (PairsInLds ? NP : 0));
     float2* pc = reinterpret_cast<float2*>((pc_at + 7) & ~uintptr_t(7));
-    for (int32_t p = threadIdx.x; p < P; p += kPriorThreads)
+    for (int32_t p = tid; p < P; p += kRoundThreads)
       pc[p] = make_float2(ws.mid[(b * P + p) * 2], ws.mid[(b * P + p) * 2 + 1]);
     __syncthreads();
-    for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    for (int32_t c = tid; c < C; c += kRoundThreads) {
       Lse a{-INFINITY, 0.0f};
       for (int32_t p = cls.class_piece[c]; p < cls.class_piece[c + 1]; ++p) a = lse_merge(a, Lse{pc[p].x, pc[p].y});
       lc[c] = lse_value(a);
     }
   }
-  for (int32_t s = threadIdx.x; s < S; s += kPriorThreads) {
-    const bool lv = live[s] != 0;
-    flag[s] = uint8_t((lv ? 1 : 0) | (accept[s] ? 2 : 0));
-    z0[s] = lv ? 0.0f : -INFINITY;
-  }
-  for (int32_t s = threadIdx.x; s <= S; s += kPriorThreads) so[s] = cls.state_off[s];
-  if (PairsInLds) {
-    constexpr int kU = 8;
-    for (int32_t i = threadIdx.x; i < cls.num_pairs; i += kPriorThreads * kU) {
-      int32_t pc_[kU], pn_[kU];
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int32_t j = i + u * kPriorThreads;
-        pc_[u] = j < cls.num_pairs ? cls.pair_class[j] : 0;
-        pn_[u] = j < cls.num_pairs ? cls.pair_next[j] : 0;
-      }
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int32_t j = i + u * kPriorThreads;
-        if (j < cls.num_pairs) pr[j] = (uint32_t(pc_[u]) << 16) | uint32_t(pn_[u]);
-      }
-    }
-  }
   __syncthreads();
   const float lse = lse_sh;
-  const float lp_eos = eos >= 0 ? logits[b * ld + eos] - lse : -INFINITY;
+  const float lp_eos = eos >= 0 ? x_eos - lse : -INFINITY;
 
-  // k-1 rounds; a group of Q lanes (a power of two dividing 64) per state,
-  // each lane taking every Q-th pair of the state: a max pass, then a sum of
-  // exp(v - max) pass, each closed by a Q-lane reduction
-  int Q = 1;
-  while (Q < 64 && 2 * Q * S <= kPriorThreads) Q *= 2;
-  const int groups = kPriorThreads / Q;
-  const int sub = threadIdx.x & (Q - 1);
-  const int passes = (S + groups - 1) / groups;
+  const int quad = tid >> 2, ql = tid & 3;
+  constexpr int kQuads = kRoundThreads / 4;
   float* zc = z0;
   float* zn = z1;
   for (int32_t j = 0; j < rounds; ++j) {
-    for (int pass = 0; pass < passes; ++pass) {
-      const int32_t s = pass * groups + int32_t(threadIdx.x) / Q;
+    for (int32_t s0 = 0; s0 < S; s0 += kQuads) {
+      const int32_t s = s0 + quad;
       const bool on = s < S;
-      const int32_t i0 = on ? so[s] : 0;
       const int32_t i1 = on ? so[s + 1] : 0;
-      float mx = -INFINITY;
-      for (int32_t i = i0 + sub; i < i1; i += Q) {
-        int32_t c, d;
-        if (PairsInLds) {
-          c = int32_t(pr[i] >> 16);
-          d = int32_t(pr[i] & 0xFFFFu);
-        } else {
-          c = cls.pair_class[i];
-          d = cls.pair_next[i];
+      float m = -INFINITY, sm = 0.0f;
+      for (int32_t base = (on ? so[s] : 0) + ql; base < i1; base += 4 * kQuadLoads) {
+        // indices clamped into the state's pairs, so that every read of the
+        // batch is issued before the first wait; the clamped ones read -inf
+        uint32_t pp[kQuadLoads];
+#pragma unroll
+        for (int u = 0; u < kQuadLoads; ++u) pp[u] = prior_pair<PairsInLds>(pr, cls, min(base + 4 * u, i1 - 1));
+        float v[kQuadLoads];
+#pragma unroll
+        for (int u = 0; u < kQuadLoads; ++u) {
+          const float x = lc[pp[u] >> 16] + zc[pp[u] & 0xFFFFu];
+          v[u] = base + 4 * u < i1 ? x : -INFINITY;
         }
-        mx = fmaxf(mx, lc[c] + zc[d]);
-      }
-      for (int o = Q / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-      float sm = 0.0f;
-      if (mx != -INFINITY) {
-        const float mb = mx * kLog2e;
-        for (int32_t i = i0 + sub; i < i1; i += Q) {
-          int32_t c, d;
-          if (PairsInLds) {
-            c = int32_t(pr[i] >> 16);
-            d = int32_t(pr[i] & 0xFFFFu);
-          } else {
-            c = cls.pair_class[i];
-            d = cls.pair_next[i];
-          }
-          sm += exp_shift(lc[c] + zc[d], mb);
+        float bm = v[0];
+#pragma unroll
+        for (int u = 1; u < kQuadLoads; ++u) bm = fmaxf(bm, v[u]);
+        if (bm != -INFINITY) {
+          const float nm = fmaxf(m, bm);
+          const float nb = nm * kLog2e;
+          float acc = sm * exp_shift(m, nb);  // 0 while m is -inf
+#pragma unroll
+          for (int u = 0; u < kQuadLoads; ++u) acc += exp_shift(v[u], nb);
+          sm = acc;
+          m = nm;
         }
       }
-      for (int o = Q / 2; o > 0; o >>= 1) sm += __shfl_xor(sm, o);
-      if (sub == 0 && on) {
+      quad_lse_step<kDppQuadXor1>(m, sm);
+      quad_lse_step<kDppQuadXor2>(m, sm);
+      if (on && ql == 0) {
         const uint8_t f = flag[s];
-        float v = mx == -INFINITY ? -INFINITY : mx + logf(sm) - lse;
+        float v = m == -INFINITY ? -INFINITY : m + logf(sm) - lse;
         if (f & 2) v = log_add_exp(v, lp_eos);
         zn[s] = (f & 1) ? v : -INFINITY;
       }
@@ -765,18 +846,17 @@ __global__ __launch_bounds__(kPriorThreads) void prior_rounds_kernel(
 
   // zcls[b, c] = logZ(next state of class c from s_b), -inf when rejected
   const int32_t sb = states[slots ? slots[b] : b];
-  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) lc[c] = -INFINITY;
+  for (int32_t c = tid; c < C; c += kRoundThreads) lc[c] = -INFINITY;
   __syncthreads();
   if (sb >= 0 && sb < S) {
-    for (int32_t i = so[sb] + threadIdx.x; i < so[sb + 1]; i += kPriorThreads) {
-      const int32_t c = PairsInLds ? int32_t(pr[i] >> 16) : cls.pair_class[i];
-      const int32_t d = PairsInLds ? int32_t(pr[i] & 0xFFFFu) : cls.pair_next[i];
-      lc[c] = zc[d];
+    for (int32_t i = so[sb] + tid; i < so[sb + 1]; i += kRoundThreads) {
+      const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
+      lc[p >> 16] = zc[p & 0xFFFFu];
     }
   }
   __syncthreads();
-  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) ws.zcls[b * C + c] = lc[c];
-  if (threadIdx.x == 0) ws.lse[b] = lse;
+  for (int32_t c = tid; c < C; c += kRoundThreads) ws.zcls[b * C + c] = lc[c];
+  if (tid == 0) ws.lse[b] = lse;
 }
 
 __device__ inline float prior_value(float x, float lse, int64_t t, float z, bool acc_s, int32_t eos,
@@ -905,13 +985,19 @@ extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_
   const bool vec = vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) && aligned16(cls.token_class);
   if (pl.class_stats) {
     const dim3 grid = dim3(unsigned(pl.G), unsigned(rows));
-    if (vec) {
-      prior_stats_classes_kernel<true><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab, cls.token_class,
-                                                                      cls.num_classes, ws);
-    } else {
-      prior_stats_classes_kernel<false><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab, cls.token_class,
-                                                                       cls.num_classes, ws);
-    }
+    const bool narrow = cls.token_class16 != nullptr && cls.num_classes < 65535;
+    const bool nvec = vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) &&
+                      (reinterpret_cast<uintptr_t>(cls.token_class16) & 7u) == 0;
+#define BPD_PRIOR_STATS(VEC, NARROW)                                                            \
+  prior_stats_classes_kernel<VEC, NARROW><<<grid, kPriorThreads, 0, st>>>(logits, ld, vocab,    \
+                                                                         cls.token_class,       \
+                                                                         cls.token_class16,     \
+                                                                         cls.num_classes, ws)
+    if (narrow && nvec) BPD_PRIOR_STATS(true, true);
+    else if (narrow) BPD_PRIOR_STATS(false, true);
+    else if (vec) BPD_PRIOR_STATS(true, false);
+    else BPD_PRIOR_STATS(false, false);
+#undef BPD_PRIOR_STATS
   } else {
     int64_t chunk = (vocab + pl.G - 1) / pl.G;
     chunk = (chunk + 3) / 4 * 4;
@@ -924,7 +1010,7 @@ extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_
   }
   BPD_LAUNCHED();
 #define BPD_PRIOR_ROUNDS(LDSP, CLS)                                                                  \
-  prior_rounds_kernel<LDSP, CLS><<<unsigned(rows), kPriorThreads, lds, st>>>(                       \
+  prior_rounds_kernel<LDSP, CLS><<<unsigned(rows), kRoundThreads, lds, st>>>(                       \
       logits, ld, num_states, pl.G, cls, accept, live, eos_id, states, slots, k - 1, ws)
   if (pairs_in_lds && pl.class_stats) BPD_PRIOR_ROUNDS(true, true);
   else if (pairs_in_lds) BPD_PRIOR_ROUNDS(true, false);
@@ -1048,6 +1134,9 @@ extern "C" int bpd_host_soft_classes(const int32_t* tok_next, int32_t num_states
     }
   }
   out->state_off[S] = int32_t(q);
+  if (out->token_class16 && C < 65535)
+    for (int64_t t = 0; t < V; ++t)
+      out->token_class16[t] = cls[size_t(t)] < 0 ? uint16_t(0xFFFF) : uint16_t(cls[size_t(t)]);
   return BPD_OK;
 }
 

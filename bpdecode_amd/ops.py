@@ -51,7 +51,9 @@ class SoftClasses:
     ``c`` being ``class_piece[c]:class_piece[c + 1]``); the (class, next
     state) pairs of state ``s`` are
     ``pair_class/pair_next[state_off[s]:state_off[s + 1]]``; ``token_class``
-    maps each token to its class (-1: rejected in every state)."""
+    maps each token to its class (-1: rejected in every state), and
+    ``token_class16`` is the same map as int16 (-1 read as 0xFFFF) when
+    there are fewer than 65535 classes."""
 
     class_off: torch.Tensor
     class_tok: torch.Tensor
@@ -63,6 +65,7 @@ class SoftClasses:
     token_class: torch.Tensor
     num_members: int = 0
     num_pairs: int = 0
+    token_class16: torch.Tensor | None = None
 
     def __post_init__(self) -> None:
         self._c: _lib.SoftClassesC | None = None
@@ -78,12 +81,14 @@ class SoftClasses:
 
     def to(self, device) -> SoftClasses:
         return SoftClasses(*(getattr(self, n).to(device) for n in _SOFT_ARRAYS),
-                           num_members=self.num_members, num_pairs=self.num_pairs)
+                           num_members=self.num_members, num_pairs=self.num_pairs,
+                           token_class16=None if self.token_class16 is None else self.token_class16.to(device))
 
     def c_struct(self) -> _lib.SoftClassesC:
         if self._c is None:
             self._c = _lib.SoftClassesC(self.num_classes, self.num_members, self.num_pieces,
-                                        self.num_pairs, *(ptr(getattr(self, n)) for n in _SOFT_ARRAYS))
+                                        self.num_pairs, *(ptr(getattr(self, n)) for n in _SOFT_ARRAYS),
+                                        ptr(self.token_class16))
         return self._c
 
     def workspace(self, rows: int, device: torch.device, stream: int) -> tuple[torch.Tensor, int]:
@@ -111,9 +116,11 @@ class SoftClasses:
         arrays = {n: torch.empty(max(k, 1), dtype=torch.int32) for n, k in sizes.items()}
         for n in _SOFT_ARRAYS:
             setattr(c, n, ptr(arrays[n]))
+        tc16 = torch.empty(V, dtype=torch.int16) if c.num_classes < 65535 else None
+        c.token_class16 = ptr(tc16)
         check(lib().bpd_host_soft_classes(ptr(tn), S, V, C.byref(c)))
         return cls(*(arrays[n][:sizes[n]] for n in _SOFT_ARRAYS), num_members=c.num_members,
-                   num_pairs=c.num_pairs)
+                   num_pairs=c.num_pairs, token_class16=tc16)
 
 
 @dataclass

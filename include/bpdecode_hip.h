@@ -266,11 +266,15 @@ int bpd_host_soft_apply(void* logits, int dtype, int64_t rows, int64_t vocab, in
  * cut into pieces piece_off[p] .. piece_off[p+1] of at most 256 members, its
  * pieces being class_piece[c] .. class_piece[c+1]; the (class, next state)
  * pairs of state s are pair_class / pair_next[state_off[s] .. state_off[s+1]);
- * token_class[t] is t's class, -1 for tokens rejected in every state.  Called
- * with any array null it only sets the counts; called again with arrays of
- * those sizes (counts left in place) it fills them.
+ * token_class[t] is t's class, -1 for tokens rejected in every state;
+ * token_class16, when given and num_classes < 65535, receives the same map
+ * narrowed to uint16 (0xFFFF for -1).  Called with any of the int32 arrays
+ * null it only sets the counts; called again with arrays of those sizes
+ * (counts left in place) it fills them.
  *
- * bpd_soft_prior takes the same struct with the arrays copied to the device.
+ * bpd_soft_prior takes the same struct with the arrays copied to the device;
+ * with token_class16 set its statistics pass reads the narrow map instead of
+ * token_class.
  * Workspace: bpd_soft_prior_workspace_bytes(rows, vocab, num_classes, num_pieces)
  * bytes (no initial contents needed; calls that overlap on one workspace race).
  */
@@ -284,6 +288,7 @@ typedef struct BpdSoftClasses {
   int32_t* pair_class;  /* [num_pairs] */
   int32_t* pair_next;   /* [num_pairs] */
   int32_t* token_class; /* [vocab] */
+  uint16_t* token_class16; /* [vocab] optional: token_class as uint16, 0xFFFF for -1 */
 } BpdSoftClasses;
 
 int bpd_host_soft_classes(const int32_t* tok_next, int32_t num_states, int64_t vocab,

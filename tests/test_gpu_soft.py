@@ -179,3 +179,29 @@ def test_prior_pieces_path_email(dev, monkeypatch):
     ops.apply_soft_prior_(b, fd, st.to(dev), 4, 1.0)
     a, b = a.cpu().double().numpy(), b.cpu().double().numpy()
     assert close(b, a)
+
+
+def test_prior_wide_class_map_and_extreme_logits(dev):
+    """The statistics read the uint16 class map when it is present and the
+    int32 one otherwise: same results.  Rows mixing -inf, very negative and
+    large logits keep every class sum exact (checked against the oracle)."""
+    fsa = FsaTensors.build("-?[0-9]+(\\.[0-9]+)?", TOY_VOCAB).densify()
+    S, V = fsa.tok_next.shape
+    st = torch.tensor(list(range(S)) * 2, dtype=torch.int32)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(len(st), V, generator=g) * 3
+    x[1::2, ::3] = -1.0e4
+    x[2::4, 1::5] = float("-inf")
+    x[3::4, 2] = 60.0
+    want = OS.prior_lookahead(x.double().numpy(), fsa.tok_next.numpy(), fsa.live.numpy(),
+                              fsa.accept.numpy(), fsa.eos_id, st.numpy(), 4, 0.8)
+    fd = fsa.to(dev)
+    sc = fd.ensure_soft_classes()
+    assert sc.token_class16 is not None
+    a = x.to(dev)
+    ops.apply_soft_prior_(a, fd, st.to(dev), 4, 0.8)
+    assert close(a.cpu().double().numpy(), want)
+    sc.token_class16, sc._c = None, None
+    b = x.to(dev)
+    ops.apply_soft_prior_(b, fd, st.to(dev), 4, 0.8)
+    assert close(b.cpu().double().numpy(), want)

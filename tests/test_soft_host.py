@@ -37,6 +37,7 @@ def check_classes(tn: np.ndarray, sc: SoftClasses) -> None:
     assert len(np.unique(norm[:, reps], axis=1).T) == sc.num_classes  # distinct columns
     assert (norm[:, cls < 0] == -1).all() and (cls[(norm >= 0).any(axis=0)] >= 0).all()
     assert np.array_equal(sc.token_class.numpy(), cls)
+    assert sc.token_class16 is not None and np.array_equal(sc.token_class16.numpy().astype(np.int64), cls)
     po, cp = sc.piece_off.numpy(), sc.class_piece.numpy()
     assert po[0] == 0 and po[-1] == len(mem) and np.all(np.diff(po) > 0) and np.all(np.diff(po) <= 256)
     for c in range(sc.num_classes):
