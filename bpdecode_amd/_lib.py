@@ -45,6 +45,14 @@ class TokenBytesC(C.Structure):
     _fields_ = [("vocab_size", i32), ("eos_id", i32), ("offsets", vp), ("bytes", vp), ("order", vp)]
 
 
+class FsaTableC(C.Structure):
+    _fields_ = [
+        ("trans", vp), ("num_states", i32), ("num_symbols", i32), ("dead", i32),
+        ("accept", vp), ("live", vp), ("tok_offsets", vp), ("tok_symbols", vp),
+        ("vocab", i64), ("eos_id", i32),
+    ]
+
+
 class SoftClassesC(C.Structure):
     _fields_ = [
         ("num_classes", i32), ("num_members", i32), ("num_pieces", i32), ("num_pairs", i32),
@@ -62,6 +70,9 @@ _SIGNATURES = {
     "bpd_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, cint, i64, vp, cint, vp, vp]),
     "bpd_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp, vp, vp]),
     "bpd_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp, vp]),
+    "bpd_fsa_apply_mask": (cint, [C.POINTER(FsaTableC), vp, cint, i64, i64, vp, vp, f64, vp, vp]),
+    "bpd_fsa_compute_mask": (cint, [C.POINTER(FsaTableC), vp, vp, i64, vp, vp, vp]),
+    "bpd_fsa_advance": (cint, [C.POINTER(FsaTableC), vp, vp, vp, cint, i64, vp, cint, vp, vp]),
     "bpd_host_dense_apply_mask": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f64]),
     "bpd_host_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, cint, i64, vp, cint]),
     "bpd_host_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp]),

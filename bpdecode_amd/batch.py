@@ -57,7 +57,13 @@ class MaskCache:
         return len(self._allowed)
 
     def apply(self, states: torch.Tensor, logits: torch.Tensor, neg_inf: float = float("-inf")):
-        """In place: mask ``logits`` [n, vocab] given one state per row."""
+        """In place: mask ``logits`` [n, vocab] given one state per row.  On
+        the device the grammar's packed allow-bit table (every state's mask,
+        built once) or the walking kernel masks all rows in one launch, with
+        no host round trip; on the host rows are grouped by state and the
+        cached id lists applied."""
+        if logits.device.type == "cuda":
+            return ops.apply_mask_(logits, self._fsa, states.to(logits.device), neg_inf)
         by_state: dict[int, list[int]] = defaultdict(list)
         for i, s in enumerate(states.tolist()):
             by_state[s].append(i)
@@ -190,6 +196,8 @@ class ConstraintBatch:
             ops.dense_mask_bits_(logits, self.fsa.allow_bits, pool, slots, neg_inf, self._err)
         elif self.fsa.tok_next is not None:
             ops.dense_mask_(logits, self.fsa.tok_next, pool, slots, neg_inf, self._err)
+        elif logits.device.type == "cuda":
+            ops.fsa_mask_(logits, self.fsa, pool, slots, neg_inf, self._err)
         else:
             apply_mask_(logits, self.fsa, pool[slots], neg_inf)
         return logits
@@ -219,6 +227,8 @@ class ConstraintBatch:
         pool = self._state
         if self.fsa.tok_next is not None:
             return ops.dense_advance(self.fsa.tok_next, pool, tokens, slots, True, self._err)
+        if pool.device.type == "cuda":
+            return ops.fsa_advance(self.fsa, pool, tokens, slots, True, self._err)
         nxt = advance_state(self.fsa, pool[slots], tokens.to(torch.int32))
         pool[slots] = nxt
         return nxt

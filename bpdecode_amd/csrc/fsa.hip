@@ -1,0 +1,278 @@
+// Symbol-class FSA kernels that walk each token through the transition table
+// on the fly (no [states, vocab] tok_next table): the device form of the
+// reference's non-dense operators for grammars too large to densify.
+//
+// One block covers kFsaRows rows and kFsaThreads * kFsaTok tokens.  The
+// transition table and the live flags are staged in LDS when they fit; each
+// token's first 16 symbol classes are loaded once into registers and walked
+// from every row state of the block.  Verdicts become fill stores (logits)
+// or wave64 ballots (packed bits).
+
+#include "bpd_common.hpp"
+
+namespace bpd {
+namespace {
+
+constexpr int kFsaThreads = 256;
+constexpr int kFsaTok = 4;     // tokens per thread, kFsaThreads apart
+constexpr int kFsaRows = 8;    // rows per block
+constexpr size_t kFsaMaxLds = 48 * 1024;
+constexpr int32_t kNoRow = INT32_MIN;
+constexpr int kFsaAdvThreads = 256;
+
+struct FsaView {
+  const int32_t* trans;
+  int32_t S, NS, dead;
+  const uint8_t* accept;
+  const uint8_t* live;
+  const int32_t* off;
+  const uint8_t* sym;
+  int64_t V;
+  int32_t eos;
+};
+
+__device__ __forceinline__ int packed_sym(const uint4& p, int i) {
+  const uint32_t w = i < 8 ? (i < 4 ? p.x : p.y) : (i < 12 ? p.z : p.w);
+  return int((w >> (8 * (i & 3))) & 0xFFu);
+}
+
+// The token's first min(len, 16) symbol classes, byte i at bits 8 (i % 4)
+// of word i / 4.
+__device__ __forceinline__ uint4 load_syms(const uint8_t* __restrict__ p, int32_t len) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  const int n = len < 16 ? int(len) : 16;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i < n) w[i >> 2] |= uint32_t(p[i]) << (8 * (i & 3));
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// step() of mask_cpu.cpp:53-71 for a non-EOS token from a valid state s:
+// true iff the walk never leaves the table, never meets `dead` and ends on
+// a live state.
+__device__ __forceinline__ bool walk_token(const FsaView& f, const int32_t* __restrict__ tr,
+                                           const uint8_t* __restrict__ lv, int32_t s, uint4 pk,
+                                           const uint8_t* __restrict__ rest, int32_t len) {
+  int32_t cur = s;
+  for (int32_t i = 0; i < len; ++i) {
+    const int k = i < 16 ? packed_sym(pk, i) : int(rest[i]);
+    if (k >= f.NS) return false;
+    cur = tr[int64_t(cur) * f.NS + k];
+    if (cur == f.dead || cur < 0 || cur >= f.S) return false;
+  }
+  return lv[cur] != 0;
+}
+
+// Mask (Bits = false: fill the rejected logits, element size E) or packed
+// allow bits (Bits = true).  grid (ceil(V / (kFsaThreads kFsaTok)), ceil(rows / kFsaRows)).
+template <int E, bool Bits, bool InLds>
+__global__ __launch_bounds__(kFsaThreads) void fsa_mask_kernel(
+    FsaView f, const int32_t* __restrict__ states, const int64_t* __restrict__ slots, int64_t rows,
+    uint8_t* __restrict__ logits, int64_t ld_bytes, uint32_t fill, uint32_t* __restrict__ bits,
+    int64_t words, int32_t* __restrict__ err) {
+  extern __shared__ __align__(16) int32_t lds[];
+  __shared__ int32_t rs[kFsaRows];
+  const int tid = threadIdx.x;
+  const int32_t* tr = f.trans;
+  const uint8_t* lv = f.live;
+  if (InLds) {
+    const int64_t n = int64_t(f.S) * f.NS;
+    for (int64_t i = tid; i < n; i += kFsaThreads) lds[i] = f.trans[i];
+    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds + n);
+    for (int32_t i = tid; i < f.S; i += kFsaThreads) l8[i] = f.live[i];
+    tr = lds;
+    lv = l8;
+  }
+  const int64_t r0 = int64_t(blockIdx.y) * kFsaRows;
+  if (tid < kFsaRows) {
+    const int64_t r = r0 + tid;
+    int32_t s = kNoRow;
+    if (r < rows) {
+      s = states[slots ? slots[r] : r];
+      if (s >= f.S) {
+        if (err) atomicOr(err, BPD_FLAG_STATE_RANGE);
+        s = -1;  // the whole row is masked
+      }
+    }
+    rs[tid] = s;
+  }
+  __syncthreads();
+  const int64_t t0 = int64_t(blockIdx.x) * (kFsaThreads * kFsaTok);
+#pragma unroll
+  for (int j = 0; j < kFsaTok; ++j) {
+    const int64_t t = t0 + int64_t(j) * kFsaThreads + tid;
+    const bool on = t < f.V;
+    const bool is_eos = t == f.eos;
+    int32_t len = 0;
+    uint4 pk = make_uint4(0u, 0u, 0u, 0u);
+    const uint8_t* rest = f.sym;
+    if (on && !is_eos) {
+      const int32_t b = f.off[t];
+      len = f.off[t + 1] - b;
+      rest = f.sym + b;
+      pk = load_syms(rest, len);
+    }
+    for (int r = 0; r < kFsaRows; ++r) {
+      const int32_t s = rs[r];
+      if (s == kNoRow) break;  // rows past the batch come last
+      bool ok = false;
+      if (on && s >= 0) ok = is_eos ? f.accept[s] != 0 : walk_token(f, tr, lv, s, pk, rest, len);
+      if (Bits) {
+        const uint64_t m = __ballot(ok);
+        const int64_t tw = t - (tid & 63);  // first token of the wave, a multiple of 64
+        if ((tid & 63) == 0 && tw < f.V) {
+          uint32_t* out = bits + (r0 + r) * words + (tw >> 5);
+          out[0] = uint32_t(m);
+          if ((tw >> 5) + 1 < words) out[1] = uint32_t(m >> 32);
+        }
+      } else if (on && !ok) {
+        uint8_t* p = logits + (r0 + r) * ld_bytes + t * E;
+        if (E == 2)
+          *reinterpret_cast<uint16_t*>(p) = uint16_t(fill);
+        else
+          *reinterpret_cast<uint32_t*>(p) = fill;
+      }
+    }
+  }
+}
+
+// advance: one thread per row (mask_cpu.cpp:53-71 with the range handling
+// of the dense commit: token ids wrap once like torch indexing, ids still
+// out of range and states >= S give -1 and set the error flags).
+__global__ __launch_bounds__(kFsaAdvThreads) void fsa_advance_kernel(
+    FsaView f, const int32_t* __restrict__ states, const int64_t* __restrict__ slots,
+    const void* __restrict__ tokens, int tok_dtype, int64_t rows, int32_t* __restrict__ next_out,
+    int32_t* __restrict__ err) {
+  const int64_t b = int64_t(blockIdx.x) * kFsaAdvThreads + threadIdx.x;
+  if (b >= rows) return;
+  const int32_t s = states[slots ? slots[b] : b];
+  int64_t t = tok_dtype == BPD_INDEX_I64 ? int64_t(int32_t(static_cast<const int64_t*>(tokens)[b]))
+                                         : int64_t(static_cast<const int32_t*>(tokens)[b]);
+  if (t < 0) t += f.V;
+  int32_t res = -1;
+  if (t < 0 || t >= f.V) {
+    if (err) atomicOr(err, BPD_FLAG_TOKEN_RANGE);
+  } else if (s >= f.S) {
+    if (err) atomicOr(err, BPD_FLAG_STATE_RANGE);
+  } else if (s >= 0) {
+    if (t == f.eos) {
+      res = f.accept[s] ? s : -1;
+    } else {
+      const int32_t b0 = f.off[t], len = f.off[t + 1] - b0;
+      int32_t cur = s;
+      bool ok = true;
+      for (int32_t i = 0; i < len && ok; ++i) {
+        const int k = f.sym[b0 + i];
+        if (k >= f.NS) {
+          ok = false;
+        } else {
+          cur = f.trans[int64_t(cur) * f.NS + k];
+          ok = cur != f.dead && cur >= 0 && cur < f.S;
+        }
+      }
+      res = ok && f.live[cur] ? cur : -1;
+    }
+  }
+  next_out[b] = res;
+}
+
+__global__ void fsa_scatter_kernel(int32_t* __restrict__ states, const int64_t* __restrict__ slots,
+                                   const int32_t* __restrict__ next, int64_t rows) {
+  const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= rows) return;
+  states[slots ? slots[b] : b] = next[b];
+}
+
+int check_fsa(const BpdFsaTable* t) {
+  BPD_REQUIRE(t, "null table argument");
+  BPD_REQUIRE(t->num_states > 0 && t->num_symbols > 0 && t->vocab >= 0, "bad FSA table shape");
+  BPD_REQUIRE(t->dead >= 0 && t->dead < t->num_states, "dead state out of range");
+  BPD_REQUIRE(t->vocab < (int64_t(1) << 31), "vocab too large");
+  BPD_REQUIRE(t->trans && t->accept && t->live && t->tok_offsets && t->tok_symbols, "null table array");
+  return BPD_OK;
+}
+
+FsaView view_of(const BpdFsaTable& t) {
+  return FsaView{t.trans, t.num_states, t.num_symbols, t.dead, t.accept, t.live,
+                 t.tok_offsets, t.tok_symbols, t.vocab, t.eos_id};
+}
+
+size_t fsa_lds_bytes(const BpdFsaTable& t) {
+  return size_t(t.num_states) * size_t(t.num_symbols) * 4 + size_t(t.num_states);
+}
+
+template <int E, bool Bits>
+int launch_fsa_mask(const BpdFsaTable& t, const int32_t* states, const int64_t* slots, int64_t rows,
+                    void* logits, int64_t ld_bytes, uint32_t fill, uint32_t* bits, int64_t words,
+                    int32_t* err, hipStream_t s) {
+  const size_t lds = fsa_lds_bytes(t);
+  const bool in_lds = lds <= kFsaMaxLds;
+  const int64_t gx = (t.vocab + kFsaThreads * kFsaTok - 1) / (kFsaThreads * kFsaTok);
+  const int64_t gy = (rows + kFsaRows - 1) / kFsaRows;
+  BPD_REQUIRE(gy < 65536, "at most %d rows per launch", 65535 * kFsaRows);
+  const dim3 grid = dim3(unsigned(gx), unsigned(gy));
+  uint8_t* lg = static_cast<uint8_t*>(logits);
+  if (in_lds)
+    fsa_mask_kernel<E, Bits, true><<<grid, kFsaThreads, lds, s>>>(view_of(t), states, slots, rows, lg,
+                                                                   ld_bytes, fill, bits, words, err);
+  else
+    fsa_mask_kernel<E, Bits, false><<<grid, kFsaThreads, 0, s>>>(view_of(t), states, slots, rows, lg,
+                                                                  ld_bytes, fill, bits, words, err);
+  BPD_LAUNCHED();
+  return BPD_OK;
+}
+
+}  // namespace
+}  // namespace bpd
+
+using namespace bpd;
+
+extern "C" int bpd_fsa_apply_mask(const BpdFsaTable* table, void* logits, int dtype, int64_t rows,
+                                  int64_t ld, const int32_t* states, const int64_t* slots, double neg_inf,
+                                  int32_t* err, void* stream) {
+  if (int rc = check_fsa(table)) return rc;
+  const int E = elem_bytes(dtype);
+  BPD_REQUIRE(E != 0, "unknown logits dtype code %d", dtype);
+  BPD_REQUIRE(rows >= 0 && ld >= table->vocab, "bad logits shape rows=%lld ld=%lld", (long long)rows,
+              (long long)ld);
+  uint32_t fill = 0;
+  if (int rc = fill_bits(dtype, neg_inf, &fill)) return rc;
+  if (rows == 0 || table->vocab == 0) return BPD_OK;
+  BPD_REQUIRE(logits && states, "null pointer argument");
+  hipStream_t s = as_stream(stream);
+  if (E == 2) return launch_fsa_mask<2, false>(*table, states, slots, rows, logits, ld * E, fill, nullptr, 0, err, s);
+  return launch_fsa_mask<4, false>(*table, states, slots, rows, logits, ld * E, fill, nullptr, 0, err, s);
+}
+
+extern "C" int bpd_fsa_compute_mask(const BpdFsaTable* table, const int32_t* states, const int64_t* slots,
+                                    int64_t rows, uint32_t* bits, int32_t* err, void* stream) {
+  if (int rc = check_fsa(table)) return rc;
+  BPD_REQUIRE(rows >= 0, "negative row count");
+  const int64_t words = (table->vocab + 31) / 32;
+  if (rows == 0 || words == 0) return BPD_OK;
+  BPD_REQUIRE(states && bits, "null pointer argument");
+  return launch_fsa_mask<4, true>(*table, states, slots, rows, nullptr, 0, 0u, bits, words, err,
+                                  as_stream(stream));
+}
+
+extern "C" int bpd_fsa_advance(const BpdFsaTable* table, int32_t* states, const int64_t* slots,
+                               const void* tokens, int token_dtype, int64_t rows, int32_t* next_out,
+                               int write_back, int32_t* err, void* stream) {
+  if (int rc = check_fsa(table)) return rc;
+  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64, "unknown token dtype code %d",
+              token_dtype);
+  BPD_REQUIRE(table->vocab > 0, "empty vocabulary");
+  BPD_REQUIRE(rows >= 0, "negative row count");
+  if (rows == 0) return BPD_OK;
+  BPD_REQUIRE(states && tokens && next_out, "null pointer argument");
+  hipStream_t s = as_stream(stream);
+  const unsigned g = unsigned((rows + kFsaAdvThreads - 1) / kFsaAdvThreads);
+  fsa_advance_kernel<<<g, kFsaAdvThreads, 0, s>>>(view_of(*table), states, slots, tokens, token_dtype, rows,
+                                                   next_out, err);
+  BPD_LAUNCHED();
+  if (write_back) {
+    fsa_scatter_kernel<<<g, kFsaAdvThreads, 0, s>>>(states, slots, next_out, rows);
+    BPD_LAUNCHED();
+  }
+  return BPD_OK;
+}

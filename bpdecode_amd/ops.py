@@ -16,8 +16,9 @@ Dense ``tok_next`` semantics (ops.py:143-197, 262-311):
 * ``advance_state``: ``-1`` for a negative state, else ``tok_next[s, t]``
   (a negative ``t`` indexes from the end, as torch indexing does).
 
-A bundle without ``tok_next`` gets the rows it needs walked on the fly by the
-table-builder kernel, which computes ``step`` entry for entry.
+A bundle without ``tok_next`` (mask_cpu.cpp:53-71 ``step`` semantics) runs
+the symbol-class walking kernels on the device; on the host its rows are
+walked by the table builder, entry for entry the same ``step``.
 """
 
 from __future__ import annotations
@@ -172,6 +173,21 @@ class FsaTensors:
         if self.tok_next is not None:
             return self
         return replace(self, tok_next=build_token_transitions(self))
+
+    def c_fsa_table(self) -> _lib.FsaTableC:
+        """The C view of this bundle for the walking kernels (symbol classes
+        narrowed to uint8 once and kept with it)."""
+        c = self.__dict__.get("_c_fsa")
+        if c is None:
+            sym8 = _symbols_u8(self)
+            trans, offs = _i32(self.trans), _i32(self.offsets)
+            acc, live = self.accept.contiguous(), self.live.contiguous()
+            eos = self.eos_id if self.eos_id is not None and 0 <= self.eos_id < self.vocab_size else -1
+            c = _lib.FsaTableC(ptr(trans), self.num_states, self.num_symbols, self.dead, ptr(acc), ptr(live),
+                               ptr(offs), ptr(sym8), self.vocab_size, eos)
+            self.__dict__["_c_fsa"] = c
+            self.__dict__["_c_fsa_keep"] = (sym8, trans, offs, acc, live)
+        return c
 
     def ensure_allow_bits(self) -> torch.Tensor:
         """The packed allow-bit table (built once from tok_next and kept on
@@ -419,6 +435,67 @@ def dense_compute_mask(tok_next, states, slots=None, err=None):
     return out
 
 
+def fsa_mask_(logits, fsa: FsaTensors, states, slots=None, neg_inf=float("-inf"), err=None):
+    """Device mask of a bundle without ``tok_next``: every token walked from
+    the row's state (``states[slots[b]]`` with ``slots``) by the symbol-class
+    kernel; rows whose state is out of range are masked and flagged in
+    ``err``."""
+    dev = _same_device(logits, fsa.trans, states, slots)
+    if dev.type != "cuda":
+        raise RuntimeError("the walking kernels run on the device")
+    work, copied = _unit_stride_rows(logits)
+    B, V = work.shape
+    if V != fsa.vocab_size:
+        raise RuntimeError(f"logits have {V} columns but the vocabulary has {fsa.vocab_size} tokens")
+    if slots is not None and slots.numel() != B:
+        raise RuntimeError("one slot per logits row")
+    st = _i32(states)
+    if slots is None and st.numel() != B:
+        raise RuntimeError(f"one state per logits row (got {st.numel()} states for {B} rows)")
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    ld = work.stride(0) if B > 1 else V
+    check(lib().bpd_fsa_apply_mask(C.byref(fsa.c_fsa_table()), ptr(work), _lib.dtype_code(work.dtype), B, ld,
+                                   ptr(st), ptr(sl), float(neg_inf), ptr(err), _lib.stream_of(dev)))
+    if copied:
+        logits.copy_(work)
+    return logits
+
+
+def fsa_compute_mask(fsa: FsaTensors, states, slots=None, err=None) -> torch.Tensor:
+    dev = _same_device(fsa.trans, states, slots)
+    st = _i32(states)
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    B = st.numel() if sl is None else sl.numel()
+    out = torch.empty((B, (fsa.vocab_size + 31) // 32), dtype=torch.int32, device=dev)
+    check(lib().bpd_fsa_compute_mask(C.byref(fsa.c_fsa_table()), ptr(st), ptr(sl), B, ptr(out), ptr(err),
+                                     _lib.stream_of(dev)))
+    return out
+
+
+def fsa_advance(fsa: FsaTensors, states, tokens, slots=None, write_back=False, err=None):
+    """Next state per row by the walking kernel; with ``write_back`` the
+    pool ``states`` is updated at the rows' slots as well."""
+    tk = tokens.contiguous()
+    if tk.dtype not in (torch.int32, torch.int64):
+        tk = tk.to(torch.int64)
+    if tk.device != fsa.trans.device and tk.device.type == "cpu":
+        tk = tk.to(fsa.trans.device, non_blocking=True)
+    dev = _same_device(fsa.trans, states, tk, slots)
+    B = tk.numel()
+    if slots is None and states.numel() != B:
+        raise RuntimeError("one token id per state")
+    if slots is not None and slots.numel() != B:
+        raise RuntimeError("one token id per slot")
+    if write_back and (states.dtype != torch.int32 or not states.is_contiguous()):
+        raise RuntimeError("write_back needs a contiguous int32 state pool")
+    st = states if write_back else _i32(states)
+    sl = None if slots is None else slots.to(torch.int64).contiguous()
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    check(lib().bpd_fsa_advance(C.byref(fsa.c_fsa_table()), ptr(st), ptr(sl), ptr(tk), _lib.index_code(tk.dtype),
+                                B, ptr(out), int(write_back), ptr(err), _lib.stream_of(dev)))
+    return out.view(tokens.shape) if tokens.dim() else out.reshape(())
+
+
 def _walked_rows(fsa: FsaTensors, states: torch.Tensor):
     """For a bundle without ``tok_next``: each row's table row, walked now,
     plus the per-row state index into it (negative states kept)."""
@@ -517,6 +594,8 @@ def apply_mask_(logits: torch.Tensor, fsa: FsaTensors, states: torch.Tensor,
         if logits.device.type == "cuda":
             return dense_mask_bits_(logits, fsa.ensure_allow_bits(), states, neg_inf=neg_inf)
         return dense_mask_(logits, fsa.tok_next, states, neg_inf=neg_inf)
+    if logits.device.type == "cuda":
+        return fsa_mask_(logits, fsa, states, neg_inf=neg_inf)
     rows, idx = _walked_rows(fsa, states)
     return dense_mask_(logits, rows, idx, neg_inf=neg_inf)
 
@@ -526,6 +605,8 @@ def compute_mask(fsa: FsaTensors, states: torch.Tensor) -> torch.Tensor:
     LSB-first (ops.py:284-292)."""
     if fsa.tok_next is not None:
         return dense_compute_mask(fsa.tok_next, states)
+    if states.device.type == "cuda":
+        return fsa_compute_mask(fsa, states)
     rows, idx = _walked_rows(fsa, states)
     return dense_compute_mask(rows, idx)
 
@@ -535,6 +616,8 @@ def advance_state(fsa: FsaTensors, states: torch.Tensor, token_ids: torch.Tensor
     (ops.py:295-311)."""
     if fsa.tok_next is not None:
         return dense_advance(fsa.tok_next, states, token_ids)
+    if states.device.type == "cuda":
+        return fsa_advance(fsa, states, token_ids)
     rows, idx = _walked_rows(fsa, states)
     return dense_advance(rows, idx, token_ids)
 

@@ -114,6 +114,46 @@ int bpd_build_tok_next(const int32_t* trans, int32_t num_states, int32_t num_sym
                        int64_t vocab, int32_t eos_id, const int32_t* row_states,
                        int32_t num_rows, int32_t* out, void* stream);
 
+/* Symbol-class FSA walked per token on the device, without a tok_next table
+ * (grammars too large to densify).  The reference's FsaTable + TokenSymbols
+ * (mask.hpp:18-38) with the symbol classes narrowed to uint8.  The verdict
+ * of (state s, token t) is step() of mask_cpu.cpp:53-71: EOS allowed iff
+ * s >= 0 and accept[s]; otherwise s >= 0, every symbol < num_symbols, the
+ * walk never meets `dead` (nor leaves [0, num_states)) and ends live. */
+typedef struct BpdFsaTable {
+  const int32_t* trans;       /* [num_states * num_symbols] */
+  int32_t num_states, num_symbols, dead;
+  const uint8_t* accept;      /* [num_states] */
+  const uint8_t* live;        /* [num_states] */
+  const int32_t* tok_offsets; /* [vocab + 1] */
+  const uint8_t* tok_symbols; /* [tok_offsets[vocab]] */
+  int64_t vocab;
+  int32_t eos_id;             /* -1: none */
+} BpdFsaTable;
+
+/* bpd_fsa_apply_mask: logits[b, t] = neg_inf (checked conversion as in
+ * bpd_dense_apply_mask) iff token t is rejected from state(b) =
+ * states[slots ? slots[b] : b]; every entry of a row with state(b) < 0 is
+ * rejected, and so is every entry of a row whose state is >= num_states
+ * (BPD_FLAG_STATE_RANGE set in err).  Any float dtype.  Replaces
+ * apply_mask_batch_cuda (mask.hpp:107-113) behind torch_ops.cpp:109-152. */
+int bpd_fsa_apply_mask(const BpdFsaTable* table, void* logits, int dtype, int64_t rows, int64_t ld,
+                       const int32_t* states, const int64_t* slots, double neg_inf, int32_t* err,
+                       void* stream);
+
+/* bpd_fsa_compute_mask: packed allow bits [rows, ceil(vocab/32)], LSB-first.
+ * Replaces compute_mask_batch_cuda (mask.hpp:91-97, torch_ops.cpp:154-189). */
+int bpd_fsa_compute_mask(const BpdFsaTable* table, const int32_t* states, const int64_t* slots,
+                         int64_t rows, uint32_t* bits, int32_t* err, void* stream);
+
+/* bpd_fsa_advance: next_out[b] = step(state(b), t(b)) (-1 off a valid path),
+ * t(b) read as in bpd_dense_advance (int32 or int64, negative ids indexing
+ * from the end); with write_back the pool slot is updated too.  Replaces
+ * advance_state_batch_cuda (mask.hpp:99-105, torch_ops.cpp:191-229). */
+int bpd_fsa_advance(const BpdFsaTable* table, int32_t* states, const int64_t* slots,
+                    const void* tokens, int token_dtype, int64_t rows, int32_t* next_out,
+                    int write_back, int32_t* err, void* stream);
+
 /* Host (CPU-tensor) forms of the dense entry points. */
 int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                               const int32_t* tok_next, int32_t num_states,
