@@ -101,8 +101,12 @@ def parse_args(argv=None):
     p.add_argument("--cpu-steps", type=int, default=8, help="recorded steps replayed on the CPU")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
-    p.add_argument("--workload", choices=["dense", "pda", "soft"], default="dense",
-                   help="dense: email-regex tok_next step (the headline); pda: recursive-JSON PDA step")
+    p.add_argument("--workload", choices=["dense", "pda", "soft", "schema"], default="dense",
+                   help="dense: email-regex tok_next step (the headline); pda: recursive-JSON PDA step; "
+                        "soft: prior-weighted lookahead; schema: flat JSON-Schema DFA at B=512, dense "
+                        "table and walking kernel side by side")
+    p.add_argument("--schema-rows", type=int, default=512)
+    p.add_argument("--schema-steps", type=int, default=64)
     p.add_argument("--pda-rows", type=int, default=256)
     p.add_argument("--pda-steps", type=int, default=64)
     p.add_argument("--pda-cpu-rows", type=int, default=4, help="rows of one step replayed on the CPU oracle")
@@ -142,6 +146,8 @@ def main(argv=None) -> int:
         return bench_pda(args)
     if args.workload == "soft":
         return bench_soft(args)
+    if args.workload == "schema":
+        return bench_schema(args)
 
     import numpy as np
     import torch
@@ -308,6 +314,110 @@ def main(argv=None) -> int:
             "host_cpus": os.cpu_count(),
         }
         out["parity_vs_oracle"] = parity
+    print(json.dumps(out))
+    return 0
+
+
+def bench_schema(args) -> int:
+    """Flat JSON-Schema document DFA (826 states) over the serving vocab,
+    B rows at random reachable states, bf16 logits N(0, 3), no churn.  Each
+    step masks and commits twice on identical inputs: through the dense
+    allow-bit table (the timed headline of this workload) and through the
+    symbol-class walking kernel (no [states, vocab] table); the two results
+    are compared bit for bit every step."""
+    import numpy as np
+    import torch
+
+    from bpdecode_amd import synth
+    from bpdecode_amd.batch import ConstraintBatch
+    from bpdecode_amd.grammar.json_schema import json_schema_to_grammar
+    from bpdecode_amd.grammar.pda import CompiledGrammar
+    from bpdecode_amd.grammar.regular import residual_dfa
+    from bpdecode_amd.ops import FsaTensors
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, V = args.schema_rows, args.vocab
+    vocab = synth.serving_vocab(V, seed=1)
+    comp = CompiledGrammar.build(json_schema_to_grammar(synth.FLAT_SCHEMA))
+    dfa = residual_dfa(comp, comp.root, comp.rules[comp.root].start)
+    plain = FsaTensors.build(dfa, vocab, dense=False).to(dev)
+    dense = plain.densify()
+    dense.ensure_allow_bits()
+    S = plain.num_states
+    starts = synth.random_walk_states(dense.tok_next.cpu(), plain.start, vocab.eos_id, B, 12, seed=4)
+    batches = [ConstraintBatch(dense, capacity=B, device=dev), ConstraintBatch(plain, capacity=B, device=dev)]
+    for bt in batches:
+        for i in range(B):
+            bt.add(i)
+        bt._state[:B] = starts.to(dev)
+    ids = list(range(B))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    logits = [torch.empty((B, V), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    flush64 = torch.zeros(512 << 20, dtype=torch.uint8, device=dev).view(torch.int64)
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    n_total = args.warmup + args.schema_steps
+    kev = HipEvents(8 * n_total)
+    distinct, parity = [], True
+    for k in range(n_total):
+        logits[0].copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
+        logits[1].copy_(logits[0])
+        st = batches[0]._state[:B]
+        distinct.append(int(torch.unique(st[st >= 0]).numel()))
+        toks = None
+        for p, bt in enumerate(batches):
+            bt._slots(ids)
+            bt._state  # queued slot writes land before the timed region
+            if not args.no_flush:
+                flush64.sum()
+            kev.record(8 * k + 4 * p, sh)
+            bt.apply_mask(ids, logits[p])
+            kev.record(8 * k + 4 * p + 1, sh)
+            if toks is None:
+                toks = torch.multinomial(torch.softmax(logits[p].float(), dim=-1), 1, generator=gen).view(-1)
+            kev.record(8 * k + 4 * p + 2, sh)
+            bt.commit(ids, toks)
+            kev.record(8 * k + 4 * p + 3, sh)
+        parity &= bool(torch.equal(logits[0].view(torch.int16), logits[1].view(torch.int16)))
+        parity &= bool(torch.equal(batches[0]._state[:B], batches[1]._state[:B]))
+    torch.cuda.synchronize()
+    timed = range(args.warmup, n_total)
+    ms = {name: [kev.elapsed_ms(8 * k + a, 8 * k + a + 1) for k in timed]
+          for name, a in (("mask", 0), ("commit", 2), ("walk_mask", 4), ("walk_commit", 6))}
+    step_ms = [a + b for a, b in zip(ms["mask"], ms["commit"])]
+    U = distinct[args.warmup:]
+    d_bytes = [B * V * 2 * 2 + u * V * 4 for u in U]
+    achieved = sum(d_bytes) / (sum(ms["mask"]) * 1e-3) / 1e9
+    mean_ms = statistics.fmean(step_ms)
+    out = {
+        "metric": "µs/step apply_mask+commit, flat JSON-Schema DFA, B=512 V=151936 bf16",
+        "value": round(mean_ms * 1e3, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.schema_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "dense tok_next apply_mask+commit, flat JSON-Schema document DFA",
+                   "batch_rows": B, "vocab": V, "dfa_states": S, "symbol_classes": plain.num_symbols,
+                   "logits": "bf16 N(0,3)", "cache_flush": "512 MB read before each mask and commit pair"},
+        "mask_us": round(statistics.fmean(ms["mask"]) * 1e3, 3),
+        "commit_us": round(statistics.fmean(ms["commit"]) * 1e3, 3),
+        "walk_mask_us": round(statistics.fmean(ms["walk_mask"]) * 1e3, 3),
+        "walk_commit_us": round(statistics.fmean(ms["walk_commit"]) * 1e3, 3),
+        "distinct_live_states_mean": round(statistics.fmean(U), 2),
+        "row_vocab_entries_per_s": round(B * V / (mean_ms * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "dense_mask_bits_kernel<2>",
+                     "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1)},
+        "parity_dense_vs_walk_every_step": parity,
+    }
     print(json.dumps(out))
     return 0
 
