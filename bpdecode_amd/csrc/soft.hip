@@ -365,8 +365,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 // 2^x by the hardware exponential (v_exp_f32); used for x <= 0.
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// exp(x - m) for x <= m
-__device__ inline float exp_shift(float x, float m_log2e) { return exp2_fast(fmaf(x, kLog2e, -m_log2e)); }
+// exp(x - m) for x <= m: the difference is formed first (exact for x close
+// to m), so the result keeps full precision however large m is
+__device__ inline float exp_shift(float x, float m) { return exp2_fast((x - m) * kLog2e); }
 
 // Order-preserving int image of a float (and back: the map is an involution).
 __device__ inline int32_t ord_of(float x) {
@@ -379,8 +380,7 @@ __device__ inline float float_of_ord(int32_t i) { return __int_as_float(i >= 0 ?
 __device__ inline Lse lse_merge_fast(Lse a, Lse b) {
   const float m = fmaxf(a.m, b.m);
   if (m == -INFINITY) return Lse{m, 0.0f};
-  const float mb = m * kLog2e;
-  return Lse{m, a.s * exp_shift(a.m, mb) + b.s * exp_shift(b.m, mb)};
+  return Lse{m, a.s * exp_shift(a.m, m) + b.s * exp_shift(b.m, m)};
 }
 
 __device__ inline Lse wave_lse(Lse a) {
@@ -532,10 +532,9 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
   for (int e = 0; e < kE; ++e) m = fmaxf(m, x[e]);
   Lse acc{-INFINITY, 0.0f};
   if (m != -INFINITY) {
-    const float mb = m * kLog2e;
     float sum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kE; ++e) sum += exp_shift(x[e], mb);
+    for (int e = 0; e < kE; ++e) sum += exp_shift(x[e], m);
     acc = Lse{m, sum};
   }
   acc = block_lse<kPriorThreads>(acc);  // its barriers also publish the LDS init
@@ -552,7 +551,7 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
   for (int e = 0; e < kE; ++e) {
     if (k[e] >= 0 && x[e] != -INFINITY) {
       const float cm = float_of_ord(cmax[k[e]]);
-      atomicAdd(&csum[k[e]], exp_shift(x[e], cm * kLog2e));
+      atomicAdd(&csum[k[e]], exp_shift(x[e], cm));
     }
   }
   __syncthreads();
@@ -618,11 +617,10 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_pieces_kernel(
 #pragma unroll
       for (int u = 0; u < kStatLoads; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
       if (m != -INFINITY) {
-        const float mb = m * kLog2e;
         float sum = 0.0f;
 #pragma unroll
         for (int u = 0; u < kStatLoads; ++u)
-          sum += (exp_shift(x[u].x, mb) + exp_shift(x[u].y, mb)) + (exp_shift(x[u].z, mb) + exp_shift(x[u].w, mb));
+          sum += (exp_shift(x[u].x, m) + exp_shift(x[u].y, m)) + (exp_shift(x[u].z, m) + exp_shift(x[u].w, m));
         acc = lse_merge(acc, Lse{m, sum});
       }
     }
@@ -663,8 +661,7 @@ __device__ inline void quad_lse_step(float& m, float& s) {
   const float mo = quad_read<Ctrl>(m), so = quad_read<Ctrl>(s);
   const float nm = fmaxf(m, mo);
   if (nm != -INFINITY) {
-    const float nb = nm * kLog2e;
-    s = s * exp_shift(m, nb) + so * exp_shift(mo, nb);
+    s = s * exp_shift(m, nm) + so * exp_shift(mo, nm);
   }
   m = nm;
 }
@@ -766,11 +763,11 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
     for (int u = 0; u < kMergeRegs; ++u) {
       const int e = tid + u * kRoundThreads;
       if (e < CG && mv[u].x != -INFINITY)
-        atomicAdd(&cs[e % C], mv[u].y * exp_shift(mv[u].x, float_of_ord(lci[e % C]) * kLog2e));
+        atomicAdd(&cs[e % C], mv[u].y * exp_shift(mv[u].x, float_of_ord(lci[e % C])));
     }
     for (int e = tid + kMergeRegs * kRoundThreads; e < CG; e += kRoundThreads) {
       const float2 v = *reinterpret_cast<const float2*>(mid + 2 * int64_t(e));
-      if (v.x != -INFINITY) atomicAdd(&cs[e % C], v.y * exp_shift(v.x, float_of_ord(lci[e % C]) * kLog2e));
+      if (v.x != -INFINITY) atomicAdd(&cs[e % C], v.y * exp_shift(v.x, float_of_ord(lci[e % C])));
     }
     __syncthreads();
     for (int32_t c = tid; c < C; c += kRoundThreads) {
@@ -821,10 +818,9 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
         for (int u = 1; u < kQuadLoads; ++u) bm = fmaxf(bm, v[u]);
         if (bm != -INFINITY) {
           const float nm = fmaxf(m, bm);
-          const float nb = nm * kLog2e;
-          float acc = sm * exp_shift(m, nb);  // 0 while m is -inf
+          float acc = sm * exp_shift(m, nm);  // 0 while m is -inf
 #pragma unroll
-          for (int u = 0; u < kQuadLoads; ++u) acc += exp_shift(v[u], nb);
+          for (int u = 0; u < kQuadLoads; ++u) acc += exp_shift(v[u], nm);
           sm = acc;
           m = nm;
         }
