@@ -352,7 +352,7 @@ extern "C" int bpd_host_soft_apply(void* logits, int dtype, int64_t rows, int64_
 namespace bpd {
 namespace {
 
-constexpr int kPriorThreads = 512;
+constexpr int kPriorThreads = 256;
 constexpr int kPriorOutThreads = 256;
 constexpr int kPriorMaxStates = 4096;
 constexpr int kPieceMembers = 256;
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_pieces_kernel(
 constexpr int kRoundThreads = 1024;
 constexpr int kQuadLoads = 16;   // pairs per lane in flight
 constexpr int kPairRegs = 8;     // pairs per thread held in registers while they load
-constexpr int kMergeRegs = 4;    // class partials per thread held in registers
+constexpr int kMergeRegs = 8;    // class partials per thread held in registers
 
 // DPP quad permutations: lane i reads lane i ^ 1, lane i ^ 2 of its quad
 constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
