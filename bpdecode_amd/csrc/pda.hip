@@ -465,27 +465,55 @@ __device__ bool coop_same(const int32_t* x, const int32_t* y, int lane) {
   return __ballot(diff) == 0;
 }
 
-// Byte-class interval of `byte` for a set given its top states: every byte
-// in [lo, hi] lies in the same byte edges of those tops.
-// Returns whether any of those byte edges contains `byte` (if none does, the
-// step from the set empties it for the whole interval).
-__device__ inline bool byte_interval(const PdaTableView& g, const int32_t* tops, int n, int byte,
-                                     int& lo, int& hi) {
-  lo = 0;
-  hi = 255;
-  bool hit = false;
+// Elementary byte intervals of a set, from its top states: advance_byte
+// of the set depends on a byte c only through which of the tops' byte edges
+// contain c, so [0, 255] splits into intervals of equal behaviour.  Bit x of
+// `bnd` marks an interval start (x = lo of a byte edge, or hi + 1), bit x of
+// `hit` a byte some edge contains.  One wave builds both (lanes over the
+// edges, LDS atomics); edges outside [0, 255] clip as they would in a
+// byte-by-byte comparison.
+__device__ void coop_set_intervals(const PdaTableView& g, const int32_t* tops, int n, uint32_t* bnd,
+                                   uint32_t* hit, int lane) {
+  if (lane < 8) {
+    bnd[lane] = 0u;
+    hit[lane] = 0u;
+  }
+  wave_sync();
   for (int i = 0; i < n; ++i) {
     const int top = tops[i];
     if (top < 0) continue;
-    for (int e = g.edge_offsets[top]; e < g.edge_offsets[top + 1]; ++e) {
+    const int ee = g.edge_offsets[top + 1];
+    for (int e = g.edge_offsets[top] + lane; e < ee; e += kWave) {
       if (g.edge_kind[e] != BPD_PDA_EDGE_BYTE) continue;
       const int el = g.edge_lo[e], eh = g.edge_hi[e];
-      if (el <= byte) lo = max(lo, el); else hi = min(hi, el - 1);
-      if (eh >= byte) hi = min(hi, eh); else lo = max(lo, eh + 1);
-      hit |= el <= byte && byte <= eh;
+      if (el >= 1 && el <= 255) atomicOr(&bnd[el >> 5], 1u << (el & 31));
+      if (eh >= 0 && eh <= 254) atomicOr(&bnd[(eh + 1) >> 5], 1u << ((eh + 1) & 31));
+      const int a = el < 0 ? 0 : el, z = eh > 255 ? 255 : eh;
+      for (int w = a >> 5; a <= z && w <= (z >> 5); ++w) {
+        const int b0 = (a > w * 32 ? a : w * 32) - w * 32, b1 = (z < w * 32 + 31 ? z : w * 32 + 31) - w * 32;
+        const uint32_t upto = b1 == 31 ? 0xFFFFFFFFu : ((1u << (b1 + 1)) - 1u);
+        atomicOr(&hit[w], upto & ~((1u << b0) - 1u));
+      }
     }
   }
-  return hit;
+  wave_sync();
+}
+
+// The elementary interval [lo, hi] of `byte` from a set's bitmaps; returns
+// whether some byte edge contains it (if none does, the step from the set
+// empties it on the whole interval).
+__device__ inline bool set_interval(const uint32_t* bnd, const uint32_t* hit, int byte, int& lo, int& hi) {
+  const int b = byte & 31;
+  const uint32_t le = b == 31 ? 0xFFFFFFFFu : ((2u << b) - 1u);  // bits 0..b
+  int w = byte >> 5;
+  uint32_t m = bnd[w] & le;
+  while (m == 0u && w > 0) m = bnd[--w];
+  lo = m ? w * 32 + 31 - __clz(m) : 0;
+  w = byte >> 5;
+  m = bnd[w] & ~le;
+  while (m == 0u && w < 7) m = bnd[++w];
+  hi = m ? w * 32 + __ffs(m) - 2 : 255;
+  return (hit[byte >> 5] >> b) & 1u;
 }
 
 // byte p of the token at walk position k (its first 16 bytes are packed)
@@ -502,6 +530,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
+  __shared__ uint32_t set_bnd[kMemoSets][8];  // interval starts of each set's bytes
+  __shared__ uint32_t set_hit[kMemoSets][8];  // bytes some top's byte edge contains
   __shared__ int32_t cand_tops[kMemoReq][kMaxConfigs];
   __shared__ int32_t cand_n[kMemoReq];
   __shared__ uint32_t T32[kMemoSets * 256 / 4];
@@ -588,6 +618,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       set_tops[0][tid] = d > 0 ? row_cfg[kF + tid * kMaxDepth + d - 1] : -1;
       if (tid == 0) set_n[0] = n;
     }
+    wave_sync();
+    coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], tid);
   }
   for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
   __syncthreads();
@@ -666,13 +698,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       __syncthreads();
       const int n = nreq < kMemoReq ? nreq : kMemoReq;
       if (tid < n) {
-        // advance_byte(set, c) depends on c only through which byte edges of
-        // the set's top states contain c, so every byte of the elementary
-        // interval [lo, hi] around the request shares its result: the first
-        // request of an interval computes it and fills the whole interval
+        // every byte of the request's elementary interval [lo, hi] shares
+        // its result: the first request of an interval computes it and
+        // fills the whole interval
         const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
         int lo, hi;
-        const bool hit = byte_interval(g, set_tops[set], set_n[set], byte, lo, hi);
+        const bool hit = set_interval(set_bnd[set], set_hit[set], byte, lo, hi);
         cand_lo[tid] = int16_t(lo);
         cand_hi[tid] = int16_t(hi);
         if (!hit) {
@@ -703,10 +734,18 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             if (lane == 0) cand_res[r] = -1;
           } else {
             const uint32_t h = coop_hash(wdst, lane);
+            // the first pool set with this hash and these meaningful words;
+            // hashes compared 64 at a time
             int found = -2;
             const int pc = pool_count < max_sets ? pool_count : max_sets;
-            for (int k = 0; k < pc && found < 0; ++k)
-              if (pool_hash[k] == h && coop_same(wdst, pool + k * kConfigWords, lane)) found = k;
+            for (int k0 = 0; k0 < pc && found < 0; k0 += kWave) {
+              uint64_t m = __ballot(k0 + lane < pc && pool_hash[k0 + lane] == h);
+              while (m != 0u && found < 0) {
+                const int k = k0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+                m &= m - 1;
+                if (coop_same(wdst, pool + k * kConfigWords, lane)) found = k;
+              }
+            }
             if (lane < kMaxConfigs) {
               const int nn = wdst[0];
               const int d = lane < nn ? wdst[2 + lane] : 0;
@@ -768,6 +807,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           const int32_t* src = cand + r * kConfigWords;
           int32_t* dst = pool + cand_id[r] * kConfigWords;
           for (int k = lane; k < kConfigWords; k += kWave) dst[k] = src[k];
+          coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]], lane);
         }
       }
       __syncthreads();
@@ -787,6 +827,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (tid == 0) set_n[0] = n0;
       }
       __syncthreads();
+      if (tid < kWave) coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], tid);
       if (tid == 0) {
         pool_count = 1;
         pool_hash[0] = h0_sh;
