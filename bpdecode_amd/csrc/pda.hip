@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ uint32_t pool_hash[kMemoSets];
   __shared__ int32_t req_list[kMemoReq];
   __shared__ uint32_t cand_hash[kMemoReq];
-  __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new
+  __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new, -4 duplicate, -5 no edge
   __shared__ int32_t cand_lead[kMemoReq];
   __shared__ int32_t cand_id[kMemoReq];
   __shared__ int16_t cand_lo[kMemoReq];
@@ -707,8 +707,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         cand_lo[tid] = int16_t(lo);
         cand_hi[tid] = int16_t(hi);
         if (!hit) {
-          for (int x = lo; x <= hi; ++x) T[set * 256 + x] = kTDead;
-          cand_res[tid] = -4;
+          cand_res[tid] = -5;  // rejected on the whole interval, nothing to compute
         } else {
           const uint32_t bit = 1u << (lo & 31);
           const bool first = (atomicOr(&req[set * 8 + (lo >> 5)], bit) & bit) == 0;
@@ -722,7 +721,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         int32_t* wsrc = work[wave][0];
         int32_t* wdst = work[wave][1];
         for (int r = wave; r < n; r += kMemoThreads / kWave) {
-          if (cand_res[r] == -4) continue;
+          if (cand_res[r] < -3) continue;
           const int set = req_list[r] >> 8, byte = req_list[r] & 255;
           const int32_t* ps = pool + set * kConfigWords;
           for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
@@ -782,26 +781,28 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
       }
       __syncthreads();
-      if (tid < n && cand_res[tid] != -4) {
-        const int set = req_list[tid] >> 8;
-        const int r = cand_res[tid];
-        const int id = r == -2 ? cand_id[cand_lead[tid]] : r;
-        uint8_t e;
-        if (id == -1) {
-          e = kTDead;
-        } else if (id == -3) {
-          e = kTOverflow;
-          overflowed = 1;
-        } else {
-          e = uint8_t(id);
-        }
-        const int lo = cand_lo[tid], hi = cand_hi[tid];
-        for (int c = lo; c <= hi; ++c) T[set * 256 + c] = e;
-        atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
-      }
       {
-        // new sets into the pool, one wave per set
+        // transitions into T, one wave per request with the lanes over the
+        // interval's bytes; then new sets into the pool, one wave per set
         const int lane = tid & (kWave - 1), wave = tid / kWave;
+        for (int r = wave; r < n; r += kMemoThreads / kWave) {
+          const int res = cand_res[r];
+          if (res == -4) continue;  // a duplicate of another request's interval
+          const int set = req_list[r] >> 8;
+          const int id = res == -2 ? cand_id[cand_lead[r]] : res;
+          uint8_t e;
+          if (id == -1 || id == -5) {
+            e = kTDead;
+          } else if (id == -3) {
+            e = kTOverflow;
+            if (lane == 0) overflowed = 1;
+          } else {
+            e = uint8_t(id);
+          }
+          const int lo = cand_lo[r], hi = cand_hi[r];
+          for (int c = lo + lane; c <= hi; c += kWave) T[set * 256 + c] = e;
+          if (lane == 0 && res != -5) atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
+        }
         for (int r = wave; r < n; r += kMemoThreads / kWave) {
           if (cand_res[r] != -2 || cand_lead[r] != r || cand_id[r] < 0) continue;
           const int32_t* src = cand + r * kConfigWords;
