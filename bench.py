@@ -291,26 +291,42 @@ def main(argv=None) -> int:
     if n_cpu:
         from oracle import dense as OD
 
-        tn_host = fsa.tok_next.cpu().numpy()
+        # the reference's CPU step is ATen: ops.py:271-276 (mask) and
+        # ops.py:301-306 (commit), timed here op for op on CPU tensors with
+        # torch's host threads (OMP_NUM_THREADS); the numpy oracle checks the
+        # GPU's masks as well
+        tn_host = fsa.tok_next.cpu()
+        tn_np = tn_host.numpy()
         fill = OD.fill_bits(torch.bfloat16, float("-inf"))
         parity = True
         times = []
         for _ in range(args.cpu_repeats):
             for lg, st, tk, masked in recorded:
-                bits = lg.view(torch.int16).numpy().view(np.uint16).copy()
+                x = lg.clone()
+                st_t = torch.from_numpy(st.astype(np.int32))
+                tk_t = torch.from_numpy(np.asarray(tk))
                 c0 = time.perf_counter()
-                OD.apply_mask_bits(bits, tn_host, st, fill)
-                nxt = OD.advance(tn_host, st, tk)
+                s_ = st_t.long()
+                broken = s_ < 0
+                rejected = tn_host.index_select(0, s_.clamp_(min=0)) == -1
+                rejected |= broken.unsqueeze(1)
+                x.masked_fill_(rejected, float("-inf"))
+                s2 = st_t.long()
+                nxt = tn_host[s2.clamp_(min=0), tk_t.long()]
+                nxt = torch.where(s2 < 0, torch.full_like(nxt, -1), nxt).to(torch.int32)
                 times.append(time.perf_counter() - c0)
+                parity &= bool(torch.equal(x.view(torch.int16), masked.view(torch.int16)))
+                bits = lg.view(torch.int16).numpy().view(np.uint16).copy()
+                OD.apply_mask_bits(bits, tn_np, st, fill)
                 parity &= bool(np.array_equal(bits, masked.view(torch.int16).numpy().view(np.uint16)))
-                del nxt
         out["cpu_baseline"] = {
             "value": round(statistics.fmean(times) * 1e6, 1),
             "unit": "us/step",
-            "cores": 1,
+            "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{len(recorded)} recorded steps of the same workload (B={B}, V={V}, bf16), "
-                      f"replayed {args.cpu_repeats}x through oracle/dense.py (numpy, one thread)",
+                      f"replayed {args.cpu_repeats}x through the reference's ATen op sequence "
+                      f"(ops.py:271-276 mask, ops.py:301-306 commit) on CPU tensors",
             "host_cpus": os.cpu_count(),
         }
         out["parity_vs_oracle"] = parity
@@ -514,25 +530,36 @@ def bench_pda(args) -> int:
     }
     if not args.no_cpu and args.pda_cpu_rows:
         from oracle import pda as OP
+        from oracle import ref as OR
 
         t = OP.Table(g)
         cfgs, raw, masked = first
         n = min(args.pda_cpu_rows, B)
         sub = cfgs[:n].numpy().copy()
         lg = raw[:n].numpy().copy()
+        # the reference's own apply_mask_pda_batch (pda_cpu.cpp, compiled from
+        # its sources into oracle/_ref) where that build is present, else the
+        # C restatement
+        use_ref = OR.available()
         c0 = time.perf_counter()
-        OP.apply_mask(t, sub, lg)
+        if use_ref:
+            OR.pda_apply_mask(t, sub, lg)
+        else:
+            OP.apply_mask(t, sub, lg)
         cpu_s = time.perf_counter() - c0
         out["cpu_baseline"] = {
             "value": round(cpu_s / n * B * 1e6, 1),
             "unit": "us/step",
             "cores": 1,
-            "kind": "port",
-            "sample": f"mask of {n} rows of the first timed step through oracle/pda_oracle.c "
-                      f"(C restatement of pda_cpu.cpp, one thread), scaled to B={B}",
+            "kind": "reference" if use_ref else "port",
+            "sample": (f"mask of {n} rows of the first timed step through "
+                       + ("the reference's pda_cpu.cpp apply_mask_pda_batch (oracle/_ref, one thread)"
+                          if use_ref else "oracle/pda_oracle.c (C restatement of pda_cpu.cpp, one thread)")
+                       + f", scaled to B={B}"),
             "host_cpus": os.cpu_count(),
         }
-        out["parity_vs_oracle_sampled_rows"] = bool(np.array_equal(lg, masked[:n].numpy()))
+        key = "parity_vs_reference_sampled_rows" if use_ref else "parity_vs_oracle_sampled_rows"
+        out[key] = bool(np.array_equal(lg, masked[:n].numpy()))
     print(json.dumps(out))
     return 0
 
