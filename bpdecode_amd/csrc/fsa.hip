@@ -8,6 +8,9 @@
 // from every row state of the block.  Verdicts become fill stores (logits)
 // or wave64 ballots (packed bits).
 
+#include <cstdlib>
+#include <cstring>
+
 #include "bpd_common.hpp"
 
 namespace bpd {
@@ -16,7 +19,10 @@ namespace {
 constexpr int kFsaThreads = 256;
 constexpr int kFsaTok = 4;     // tokens per thread, kFsaThreads apart
 constexpr int kFsaRows = 8;    // rows per block
-constexpr size_t kFsaMaxLds = 48 * 1024;
+// The table is staged in LDS only when small: every block stages its own
+// copy, which for large tables costs more than reading them through L2
+// (a 75 KB uint16 copy per block measured 3x slower than L2 reads).
+constexpr size_t kFsaMaxLds = 16 * 1024;
 constexpr int32_t kNoRow = INT32_MIN;
 constexpr int kFsaAdvThreads = 256;
 
@@ -206,7 +212,11 @@ int launch_fsa_mask(const BpdFsaTable& t, const int32_t* states, const int64_t* 
                     void* logits, int64_t ld_bytes, uint32_t fill, uint32_t* bits, int64_t words,
                     int32_t* err, hipStream_t s) {
   const size_t lds = fsa_lds_bytes(t);
-  const bool in_lds = lds <= kFsaMaxLds;
+  bool in_lds = lds <= kFsaMaxLds;
+  // BPD_FSA_TABLE=global forces the global-memory form (tests cover both
+  // forms on small grammars with it)
+  if (const char* e = std::getenv("BPD_FSA_TABLE"))
+    if (std::strcmp(e, "global") == 0) in_lds = false;
   const int64_t gx = (t.vocab + kFsaThreads * kFsaTok - 1) / (kFsaThreads * kFsaTok);
   const int64_t gy = (rows + kFsaRows - 1) / kFsaRows;
   BPD_REQUIRE(gy < 65536, "at most %d rows per launch", 65535 * kFsaRows);

@@ -175,18 +175,28 @@ class FsaTensors:
         return replace(self, tok_next=build_token_transitions(self))
 
     def c_fsa_table(self) -> _lib.FsaTableC:
-        """The C view of this bundle for the walking kernels (symbol classes
-        narrowed to uint8 once and kept with it)."""
+        """The C view of this bundle for the walking kernels, built once and
+        kept with it: symbols whose ``trans`` columns are equal are merged
+        into one class (a walk cannot tell them apart), so the table the
+        kernels read shrinks to [states, classes]; symbol ids at or above
+        ``num_symbols`` stay invalid (mapped past the last class)."""
         c = self.__dict__.get("_c_fsa")
         if c is None:
+            S, M = self.num_states, self.num_symbols
             sym8 = _symbols_u8(self)
-            trans, offs = _i32(self.trans), _i32(self.offsets)
+            table = self.trans.to("cpu", torch.int32).reshape(S, M)
+            cols, cls = torch.unique(table.t().contiguous(), dim=0, return_inverse=True)
+            remap = torch.full((256,), cols.shape[0], dtype=torch.int32)
+            remap[:M] = cls.to(torch.int32)
+            trans = cols.t().contiguous().reshape(-1).to(self.device)
+            sym = remap.to(self.device)[sym8.long()].to(torch.uint8)
+            offs = _i32(self.offsets)
             acc, live = self.accept.contiguous(), self.live.contiguous()
             eos = self.eos_id if self.eos_id is not None and 0 <= self.eos_id < self.vocab_size else -1
-            c = _lib.FsaTableC(ptr(trans), self.num_states, self.num_symbols, self.dead, ptr(acc), ptr(live),
-                               ptr(offs), ptr(sym8), self.vocab_size, eos)
+            c = _lib.FsaTableC(ptr(trans), S, int(cols.shape[0]), self.dead, ptr(acc), ptr(live), ptr(offs),
+                               ptr(sym), self.vocab_size, eos)
             self.__dict__["_c_fsa"] = c
-            self.__dict__["_c_fsa_keep"] = (sym8, trans, offs, acc, live)
+            self.__dict__["_c_fsa_keep"] = (sym, trans, offs, acc, live)
         return c
 
     def ensure_allow_bits(self) -> torch.Tensor:

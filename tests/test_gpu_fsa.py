@@ -1,8 +1,9 @@
 """Symbol-class FSA walking kernels (bundles without tok_next, the
 reference's non-dense operators) on the device against the oracle: every
-state of the toy grammars in every logits dtype, the flat JSON-Schema DFA
-at serving scale (826 states, V = 151,936: its transition table is read
-from global memory, not LDS), ConstraintBatch with slots and churn, the
+state of the toy grammars in every logits dtype with the transition table
+in LDS and in global memory, the flat JSON-Schema DFA at serving scale
+(826 states, V = 151,936: its table, 256 symbols merged into fewer
+classes, is read through L2), ConstraintBatch with slots and churn, the
 range flags, and MaskCache without a host round trip.  Bit-exact."""
 
 from __future__ import annotations
@@ -29,8 +30,11 @@ def _log(msg):
 
 @pytest.mark.parametrize("pattern", TOY_PATTERNS)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-def test_toy_every_state(dev, pattern, dtype):
-    _log(f"case fsa walk toy {pattern!r} {dtype}")
+@pytest.mark.parametrize("table", [None, "global"])
+def test_toy_every_state(dev, pattern, dtype, table, monkeypatch):
+    _log(f"case fsa walk toy {pattern!r} {dtype} table={table}")
+    if table:
+        monkeypatch.setenv("BPD_FSA_TABLE", table)
     f = FsaTensors.build(pattern, TOY_VOCAB, dense=False)
     assert f.tok_next is None
     tn = oracle_table(f)
@@ -59,7 +63,8 @@ def test_flat_schema_serving_scale(dev):
     dfa = residual_dfa(comp, comp.root, comp.rules[comp.root].start)
     plain = FsaTensors.build(dfa, vocab, dense=False)
     assert plain.tok_next is None
-    assert plain.num_states * plain.num_symbols * 4 > 48 * 1024  # the global-memory table form
+    c = plain.to(dev).c_fsa_table()  # equal symbol columns merged: 256 symbols -> fewer classes
+    assert c.num_symbols < plain.num_symbols and plain.num_states * c.num_symbols * 4 > 16 * 1024
     fd = plain.to(dev)
     dense_dev = fd.densify()
     tn_dev = dense_dev.tok_next
