@@ -210,3 +210,32 @@ def test_json_commit_paths_match_oracle(dev, json_case, monkeypatch, limit):
         ok, _ = pda_step(pool, gd, torch.tensor(toks, dtype=torch.int32, device=dev))
         assert ok.cpu().numpy().astype(bool).tolist() == ok_o.astype(bool).tolist(), mode
         assert np.array_equal(pool.cpu().numpy(), mirror), mode
+
+
+@pytest.mark.parametrize("eps_reduce", [False, True])
+def test_grammar_logits_processor_on_device(dev, eps_reduce):
+    """GrammarLogitsProcessor(device=cuda) — the HF calling convention over
+    the device PDA kernels — masks exactly as the memoised CPU backend,
+    step after step, on a recursive grammar (bf16 scores on the device,
+    fp32 on the host)."""
+    import random
+
+    from bpdecode_amd.hf import GrammarLogitsProcessor
+
+    _log(f"case GrammarLogitsProcessor device eps_reduce={eps_reduce}")
+    grammar = 'root ::= "(" root ")" | "[" "1"? "]" | "x" | "{a" ":0," root "}"'
+    lp_cpu = GrammarLogitsProcessor(grammar, VOCAB, backend="cpu")
+    lp_dev = GrammarLogitsProcessor(grammar, VOCAB, device=dev, eps_reduce=eps_reduce)
+    assert lp_dev.backend == "device"
+    input_ids = torch.zeros(3, 1, dtype=torch.long)
+    rng = random.Random(7)
+    for _ in range(10):
+        s_cpu = torch.zeros(3, VOCAB.size)
+        s_dev = torch.zeros(3, VOCAB.size, dtype=torch.bfloat16, device=dev)
+        lp_cpu(input_ids, s_cpu)
+        lp_dev(input_ids.to(dev), s_dev)
+        assert torch.equal(torch.isneginf(s_cpu), torch.isneginf(s_dev.cpu()))
+        for r in range(3):
+            assert lp_cpu.is_complete(r) == lp_dev.is_complete(r)
+        toks = [rng.choice((~torch.isneginf(s_cpu[r])).nonzero().flatten().tolist()) for r in range(3)]
+        input_ids = torch.cat([input_ids, torch.tensor(toks).unsqueeze(1)], dim=1)
