@@ -12,6 +12,7 @@ itself and everything else to ``-1``.
 from __future__ import annotations
 
 from collections import deque
+from collections.abc import Sequence
 from dataclasses import dataclass, field
 
 from .regex.compile import DFA
@@ -37,7 +38,7 @@ class FsaTable:
 class TokenSymbols:
     vocab_size: int
     eos_id: int
-    offsets: list[int] = field(default_factory=lambda: [0])
+    offsets: Sequence[int] = field(default_factory=lambda: [0])  # list or int32 array
     symbols: bytes = b""
 
 
@@ -79,14 +80,12 @@ def fsa_from_dfa(dfa: DFA) -> FsaTable:
 
 def token_symbols(dfa: DFA, vocab: Vocabulary) -> TokenSymbols:
     lut = bytes(dfa.symbol_of(b) for b in range(256))
-    offsets = [0]
-    for tb in vocab.token_bytes:
-        offsets.append(offsets[-1] + len(tb))
+    data, offsets = vocab.packed
     return TokenSymbols(
         vocab_size=vocab.size,
         eos_id=vocab.eos_id if vocab.eos_id is not None else -1,
         offsets=offsets,
-        symbols=b"".join(tb.translate(lut) for tb in vocab.token_bytes),
+        symbols=data.translate(lut),
     )
 
 

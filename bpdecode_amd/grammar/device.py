@@ -234,10 +234,7 @@ def build_pda_tensors(compiled: CompiledGrammar, vocab: Vocabulary, device="cpu"
                 callee_l.append(row[4])
     offsets[total] = len(kind)
     root = compiled.rules[compiled.root]
-    tok_offsets = [0]
-    for tb in vocab.token_bytes:
-        tok_offsets.append(tok_offsets[-1] + len(tb))
-    raw = b"".join(vocab.token_bytes)
+    raw, tok_offsets = vocab.packed
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32)  # noqa: E731
     g = PdaTensors(
         num_states=total,
@@ -251,7 +248,7 @@ def build_pda_tensors(compiled: CompiledGrammar, vocab: Vocabulary, device="cpu"
         edge_hi=i32(hi),
         edge_dst=i32(dst_l),
         edge_callee=i32(callee_l),
-        tok_offsets=i32(tok_offsets),
+        tok_offsets=torch.from_numpy(tok_offsets.copy()),
         tok_bytes=torch.frombuffer(bytearray(raw or b"\0"), dtype=torch.uint8)[: len(raw)].clone(),
         vocab_size=vocab.size,
         eos_id=vocab.eos_id if vocab.eos_id is not None else -1,

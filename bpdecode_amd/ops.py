@@ -26,6 +26,7 @@ from __future__ import annotations
 import ctypes as C
 from dataclasses import dataclass, replace
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -230,7 +231,7 @@ class FsaTensors:
             live=torch.tensor(fsa.live, dtype=torch.uint8),
             num_symbols=fsa.num_symbols,
             dead=fsa.dead,
-            offsets=torch.tensor(toks.offsets, dtype=torch.int32),
+            offsets=torch.from_numpy(np.asarray(toks.offsets, dtype=np.int32).copy()),
             symbols=torch.frombuffer(bytearray(toks.symbols or b"\x00"), dtype=torch.uint8)[
                 : len(toks.symbols)
             ].to(torch.int32),
