@@ -15,6 +15,7 @@
 // a freshly cleared set, so the 266 words written back on acceptance are
 // exactly those the reference produces.
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "bpd_common.hpp"
@@ -183,7 +184,9 @@ struct MemoWs {
   int32_t* overflow;  // [rows]
   int32_t* meta;      // [rows, 4]: valid, tag low, tag high, unused
   uint32_t* table;    // [rows, kMemoSets * 64]: the row's transition table after the mask
-  uint4* tok16;       // [vocab] first 16 bytes of each token, zero padded
+  uint4* recs;        // [vocab] first 16 bytes of the token at walk position k, zero padded
+  int2* tmeta;        // [vocab] (token id, length) of the token at walk position k
+  uint2* queue;       // [rows, 2, vocab] paused tokens of the row-wide walk (two buffers)
 };
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
@@ -191,10 +194,11 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
-  return sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4);
+  return sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
+         v * sizeof(int2) + r * 2 * v * sizeof(uint2);
 }
 
-MemoWs memo_ws(void* base, int64_t rows) {
+MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   MemoWs w;
   const size_t r = size_t(rows);
   w.pool = static_cast<int32_t*>(base);
@@ -205,7 +209,11 @@ MemoWs memo_ws(void* base, int64_t rows) {
   p += align256(r * 16);
   w.table = reinterpret_cast<uint32_t*>(p);
   p += r * kMemoSets * 256;
-  w.tok16 = reinterpret_cast<uint4*>(p);
+  w.recs = reinterpret_cast<uint4*>(p);
+  p += size_t(vocab) * sizeof(uint4);
+  w.tmeta = reinterpret_cast<int2*>(p);
+  p += size_t(vocab) * sizeof(int2);
+  w.queue = reinterpret_cast<uint2*>(p);
   return w;
 }
 
@@ -225,17 +233,24 @@ uint64_t memo_tag(const BpdPdaTable* g, const BpdTokenBytes* toks, int64_t rows)
   return h;
 }
 
-// tok16[t] = the first 16 bytes of token t (little-endian words, zero padded)
+// Token records in walk order (k -> t = order[k], or t = k): recs[k] = the
+// first 16 bytes of t (little-endian words, zero padded), meta[k] = (t,
+// length of t), so the walks read them coalesced.
 __global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restrict__ off,
                                                           const uint8_t* __restrict__ bytes,
-                                                          int32_t vocab, uint4* __restrict__ out) {
-  const int32_t t = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x);
-  if (t >= vocab) return;
+                                                          const int32_t* __restrict__ order,
+                                                          int32_t vocab, uint4* __restrict__ recs,
+                                                          int2* __restrict__ meta) {
+  const int32_t k = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x);
+  if (k >= vocab) return;
+  const int32_t t = order ? order[k] : k;
   const int32_t s = off[t];
-  const int32_t n = min(off[t + 1] - s, 16);
+  const int32_t len = off[t + 1] - s;
+  const int32_t n = min(len, 16);
   uint32_t w[4] = {0u, 0u, 0u, 0u};
   for (int i = 0; i < n; ++i) w[i >> 2] |= uint32_t(bytes[s + i]) << ((i & 3) * 8);
-  out[t] = make_uint4(w[0], w[1], w[2], w[3]);
+  recs[k] = make_uint4(w[0], w[1], w[2], w[3]);
+  meta[k] = make_int2(t, len);
 }
 
 __device__ inline int packed_byte(const uint4& p, int i) {
@@ -471,9 +486,10 @@ __device__ bool coop_same(const int32_t* x, const int32_t* y, int lane) {
 // `bnd` marks an interval start (x = lo of a byte edge, or hi + 1), bit x of
 // `hit` a byte some edge contains.  One wave builds both (lanes over the
 // edges, LDS atomics); edges outside [0, 255] clip as they would in a
-// byte-by-byte comparison.
+// byte-by-byte comparison.  The set's transition row `trow` gets "dead" for
+// every byte no edge contains (the step empties the set there).
 __device__ void coop_set_intervals(const PdaTableView& g, const int32_t* tops, int n, uint32_t* bnd,
-                                   uint32_t* hit, int lane) {
+                                   uint32_t* hit, uint8_t* trow, int lane) {
   if (lane < 8) {
     bnd[lane] = 0u;
     hit[lane] = 0u;
@@ -497,6 +513,8 @@ __device__ void coop_set_intervals(const PdaTableView& g, const int32_t* tops, i
     }
   }
   wave_sync();
+  for (int c = lane; c < 256; c += kWave)
+    if (((hit[c >> 5] >> (c & 31)) & 1u) == 0u) trow[c] = kTDead;
 }
 
 // The elementary interval [lo, hi] of `byte` from a set's bitmaps; returns
@@ -526,7 +544,8 @@ __device__ __forceinline__ int long_byte(const MaskArgs& a, int64_t k, int32_t p
 constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
-                                                                     int table_in_lds, uint64_t tag) {
+                                                                     int table_in_lds, uint64_t tag,
+                                                                     int row_mode) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
@@ -547,7 +566,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int16_t cand_hi[kMemoReq];
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
-  __shared__ int pool_count, nreq, row_flags, overflowed;
+  __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail;
   __shared__ uint32_t h0_sh;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
@@ -619,7 +638,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (tid == 0) set_n[0] = n;
     }
     wave_sync();
-    coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], tid);
+    coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
   }
   for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
   __syncthreads();
@@ -627,8 +646,338 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   const bool dead_row = (flags & 1) != 0;
 
   const int64_t V = a.vocab;
+
+  // Resolve the requested transitions: compact the request bits, claim one
+  // request per elementary interval, compute each claimed transition (one
+  // wave each), intern the new sets and fill T; sets `overflowed` when the
+  // pool is full.  Called by every thread, between barriers.
+  auto resolve = [&]() {
+    if (tid == 0) nreq = 0;
+    __syncthreads();
+    for (int w = tid; w < kMemoSets * 8; w += kMemoThreads) {
+      uint32_t bits = req[w];
+      if (bits) {
+        req[w] = 0;
+        int at = atomicAdd(&nreq, __popc(bits));
+        while (bits) {
+          const int bit = __ffs(bits) - 1;
+          bits &= bits - 1;
+          if (at < kMemoReq) req_list[at] = ((w >> 3) << 8) | ((w & 7) * 32 + bit);
+          ++at;
+        }
+      }
+    }
+    __syncthreads();
+    const int n = nreq < kMemoReq ? nreq : kMemoReq;
+    if (tid < n) {
+      // every byte of the request's elementary interval [lo, hi] shares
+      // its result: the first request of an interval computes it and
+      // fills the whole interval
+      const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
+      int lo, hi;
+      const bool hit = set_interval(set_bnd[set], set_hit[set], byte, lo, hi);
+      cand_lo[tid] = int16_t(lo);
+      cand_hi[tid] = int16_t(hi);
+      if (!hit) {
+        cand_res[tid] = -5;  // rejected on the whole interval, nothing to compute
+      } else {
+        const uint32_t bit = 1u << (lo & 31);
+        const bool first = (atomicOr(&req[set * 8 + (lo >> 5)], bit) & bit) == 0;
+        cand_res[tid] = first ? 0 : -4;
+      }
+    }
+    __syncthreads();
+    {
+      // one wave per claimed transition, working sets in LDS
+      const int lane = tid & (kWave - 1), wave = tid / kWave;
+      int32_t* wsrc = work[wave][0];
+      int32_t* wdst = work[wave][1];
+      for (int r = wave; r < n; r += kMemoThreads / kWave) {
+        if (cand_res[r] < -3) continue;
+        const int set = req_list[r] >> 8, byte = req_list[r] & 255;
+        const int32_t* ps = pool + set * kConfigWords;
+        for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
+        wave_sync();
+        const bool ok = coop_advance_byte(g, wsrc, wdst, byte, lane);
+        int32_t* out = cand + r * kConfigWords;
+        for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
+        if (!ok) {
+          if (lane == 0) cand_res[r] = -1;
+        } else {
+          const uint32_t h = coop_hash(wdst, lane);
+          // the first pool set with this hash and these meaningful words;
+          // hashes compared 64 at a time
+          int found = -2;
+          const int pc = pool_count < max_sets ? pool_count : max_sets;
+          for (int k0 = 0; k0 < pc && found < 0; k0 += kWave) {
+            uint64_t m = __ballot(k0 + lane < pc && pool_hash[k0 + lane] == h);
+            while (m != 0u && found < 0) {
+              const int k = k0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+              m &= m - 1;
+              if (coop_same(wdst, pool + k * kConfigWords, lane)) found = k;
+            }
+          }
+          if (lane < kMaxConfigs) {
+            const int nn = wdst[0];
+            const int d = lane < nn ? wdst[2 + lane] : 0;
+            cand_tops[r][lane] = d > 0 ? wdst[kF + lane * kMaxDepth + d - 1] : -1;
+            if (lane == 0) cand_n[r] = nn;
+          }
+          if (lane == 0) {
+            cand_hash[r] = h;
+            cand_res[r] = found;
+          }
+        }
+        wave_sync();
+      }
+    }
+    __syncthreads();
+    {
+      // new sets equal to an earlier candidate of the round: a wave per
+      // candidate matches the earlier hashes 64 at a time by ballot and
+      // compares meaningful words lane-parallel; the first equal one leads
+      const int lane = tid & (kWave - 1), wave = tid / kWave;
+      for (int r = wave; r < n; r += kMemoThreads / kWave) {
+        if (cand_res[r] != -2) continue;
+        const uint32_t h = cand_hash[r];
+        const int32_t* mine = cand + r * kConfigWords;
+        int lead = r;
+        for (int j0 = 0; j0 < r && lead == r; j0 += kWave) {
+          const int j = j0 + lane;
+          uint64_t m = __ballot(j < r && cand_res[j] == -2 && cand_hash[j] == h);
+          while (m != 0u && lead == r) {
+            const int k = j0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
+            m &= m - 1;
+            if (coop_same(mine, cand + k * kConfigWords, lane)) lead = k;
+          }
+        }
+        if (lane == 0) cand_lead[r] = lead;
+      }
+    }
+    __syncthreads();
+    if (tid < n && cand_res[tid] == -2 && cand_lead[tid] == tid) {
+      const int id = atomicAdd(&pool_count, 1);
+      if (id < max_sets) {
+        pool_hash[id] = cand_hash[tid];
+        set_n[id] = cand_n[tid];
+        for (int i = 0; i < kMaxConfigs; ++i) set_tops[id][i] = cand_tops[tid][i];
+        cand_id[tid] = id;
+      } else {
+        cand_id[tid] = -3;
+      }
+    }
+    __syncthreads();
+    {
+      // transitions into T, one wave per request with the lanes over the
+      // interval's bytes; then new sets into the pool, one wave per set
+      const int lane = tid & (kWave - 1), wave = tid / kWave;
+      for (int r = wave; r < n; r += kMemoThreads / kWave) {
+        const int res = cand_res[r];
+        if (res == -4) continue;  // a duplicate of another request's interval
+        const int set = req_list[r] >> 8;
+        const int id = res == -2 ? cand_id[cand_lead[r]] : res;
+        uint8_t e;
+        if (id == -1 || id == -5) {
+          e = kTDead;
+        } else if (id == -3) {
+          e = kTOverflow;
+          if (lane == 0) overflowed = 1;
+        } else {
+          e = uint8_t(id);
+        }
+        const int lo = cand_lo[r], hi = cand_hi[r];
+        for (int c = lo + lane; c <= hi; c += kWave) T[set * 256 + c] = e;
+        if (lane == 0 && res != -5) atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
+      }
+      for (int r = wave; r < n; r += kMemoThreads / kWave) {
+        if (cand_res[r] != -2 || cand_lead[r] != r || cand_id[r] < 0) continue;
+        const int32_t* src = cand + r * kConfigWords;
+        int32_t* dst = pool + cand_id[r] * kConfigWords;
+        for (int k = lane; k < kConfigWords; k += kWave) dst[k] = src[k];
+        coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]],
+                           T + cand_id[r] * 256, lane);
+      }
+    }
+    __syncthreads();
+  };
+
+  // Empty the pool back to the row's own set (set 0) and T to "unknown".
+  auto reset_pool = [&]() {
+    for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
+    for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
+    if (tid < kMaxConfigs) {
+      const int n0 = row_cfg[0];
+      const int d = tid < n0 ? row_cfg[2 + tid] : 0;
+      set_tops[0][tid] = d > 0 ? row_cfg[kF + tid * kMaxDepth + d - 1] : -1;
+      if (tid == 0) set_n[0] = n0;
+    }
+    __syncthreads();
+    if (tid < kWave) coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
+    if (tid == 0) {
+      pool_count = 1;
+      pool_hash[0] = h0_sh;
+      overflowed = 0;
+    }
+    __syncthreads();
+  };
+
+  // Row-wide walk.  A first pass walks every token as far as T allows and
+  // queues the paused ones (token, set, position, length) in the workspace;
+  // each round then resolves all of the row's requests at once and walks the
+  // queue again into the other buffer.  A row needs as many rounds as its
+  // longest chain of new sets (7 on recursive JSON) rather than that many per
+  // tile.  A row whose sets overflow the pool, or that pauses a token of
+  // 65536 bytes or more, starts again in tile mode.
+  bool tiles = row_mode == 0;
+  if (!tiles) {
+    uint2* qin = ws.queue + b * 2 * V;
+    uint2* qout = qin + V;
+    const int lane = tid & (kWave - 1);
+    // queue entry e for the lanes with p set (every lane of the wave calls it)
+    auto enqueue = [&](bool p, uint2 e, uint2* q) {
+      const uint64_t m = __ballot(p);
+      if (m == 0u) return;
+      const int leader = __ffsll(static_cast<unsigned long long>(m)) - 1;
+      int base = 0;
+      if (lane == leader) base = atomicAdd(&qcount, __popcll(m));
+      base = __shfl(base, leader);
+      if (p) {
+        const int idx = base + __popcll(m & ((uint64_t(1) << lane) - 1u));
+        if (idx < V) q[idx] = e;
+      }
+    };
+    // token t from (cur, pos) until it ends, is rejected or meets a missing
+    // entry (requested; returns true)
+    auto walk = [&](int& cur, int& pos, int len, uint4 pk, int32_t t) -> bool {
+      while (cur < kWalkEnd) {
+        if (pos == len) {
+          cur = kAllowed;
+          break;
+        }
+        const int byte = pos < 16 ? packed_byte(pk, pos) : int(a.tok_bytes[a.tok_off[t] + pos]);
+        const uint8_t nx = T[cur * 256 + byte];
+        if (nx == kTUnknown) {
+          int lo, hi;
+          if (!set_interval(set_bnd[cur], set_hit[cur], byte, lo, hi)) {
+            cur = kRejected;  // no byte edge over the interval: the step empties the set
+            break;
+          }
+          const int w = cur * 8 + (lo >> 5);
+          const uint32_t bit = 1u << (lo & 31);
+          if ((req[w] & bit) == 0u) atomicOr(&req[w], bit);
+          return true;
+        }
+        if (nx == kTDead || nx == kTOverflow) {
+          cur = kRejected;
+        } else {
+          cur = nx;
+          ++pos;
+        }
+      }
+      return false;
+    };
+    // the tail of a token's walk: queue it if paused, else record an accept
+    auto settle = [&](bool paused, int cur, int pos, int len, int32_t k, int32_t t, uint2* q) {
+      if (paused && len > 0xFFFF) {
+        row_fail = 1;
+        paused = false;
+      }
+      enqueue(paused, make_uint2(uint32_t(k) | (uint32_t(cur) << 24), uint32_t(pos) | (uint32_t(len) << 16)), q);
+      if (cur == kAllowed) atomicOr(&vbits[t >> 5], 1u << (t & 31));
+    };
+
+    if (!dead_row) {
+      // every interval of set 0 first, so the first pass already steps past byte 0
+      if (tid < 8) req[tid] = (set_bnd[0][tid] | (tid == 0 ? 1u : 0u)) & set_hit[0][tid];
+      resolve();
+    }
+    if (tid == 0) {
+      qcount = 0;
+      row_fail = 0;
+    }
+    __syncthreads();
+    if (!overflowed) {
+      for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
+        int32_t kk[kMemoTok], tt[kMemoTok], pos[kMemoTok], len[kMemoTok];
+        int cur[kMemoTok];
+        uint4 pk[kMemoTok];
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const int64_t k = tile + int64_t(j) * kMemoThreads + tid;
+          const int2 m = k < V ? ws.tmeta[k] : make_int2(-1, 0);
+          pk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+          const int32_t t = m.x;
+          kk[j] = int32_t(k);
+          tt[j] = t;
+          pos[j] = len[j] = 0;
+          if (t < 0) {
+            cur[j] = kNone;
+          } else if (dead_row) {
+            cur[j] = kRejected;
+          } else if (t == a.eos) {
+            cur[j] = (flags & 2) ? kAllowed : kRejected;
+          } else {
+            len[j] = m.y;
+            cur[j] = len[j] == 0 ? ((flags & 4) ? kAllowed : kRejected) : 0;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const bool paused = walk(cur[j], pos[j], len[j], pk[j], tt[j]);
+          settle(paused, cur[j], pos[j], len[j], kk[j], tt[j], qin);
+        }
+      }
+    }
+    __syncthreads();
+    int qn = qcount;
+    while (qn > 0 && !overflowed && !row_fail) {
+      resolve();  // its first barrier orders every read of qcount before the reset below
+      if (overflowed) break;
+      if (tid == 0) qcount = 0;
+      __syncthreads();
+      for (int i0 = 0; i0 < qn; i0 += kMemoThreads * kMemoTok) {
+        uint2 e[kMemoTok];
+        uint4 pk[kMemoTok];
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const int i = i0 + j * kMemoThreads + tid;
+          e[j] = i < qn ? qin[i] : make_uint2(0xFFFFFFFFu, 0u);
+        }
+        int32_t tq[kMemoTok];
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const bool valid = e[j].x != 0xFFFFFFFFu;
+          pk[j] = valid ? ws.recs[e[j].x & 0xFFFFFFu] : make_uint4(0u, 0u, 0u, 0u);
+          tq[j] = valid ? ws.tmeta[e[j].x & 0xFFFFFFu].x : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const bool valid = e[j].x != 0xFFFFFFFFu;
+          const int32_t k = int32_t(e[j].x & 0xFFFFFFu);
+          int cur = valid ? int(e[j].x >> 24) : kNone;
+          int pos = int(e[j].y & 0xFFFFu);
+          const int len = int(e[j].y >> 16);
+          const bool paused = walk(cur, pos, len, pk[j], tq[j]);
+          settle(paused, cur, pos, len, k, tq[j], qout);
+        }
+      }
+      __syncthreads();
+      qn = qcount;
+      uint2* q = qin;
+      qin = qout;
+      qout = q;
+    }
+    if (overflowed || row_fail) {
+      // start again in tile mode from an empty pool, bitmap and request set
+      for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
+      for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0u;
+      reset_pool();
+      tiles = true;
+    }
+  }
+
   bool retry = false;  // the tile is being walked again after a pool reset
-  for (int64_t tile = 0; tile < V;) {
+  for (int64_t tile = tiles ? 0 : V; tile < V;) {
     // per token: length, position, state and its first 16 bytes; the state
     // is the current set id (< 256) while walking, else kAllowed / kRejected
     // / kNone. Token j of the thread is order[tile + j * kMemoThreads + tid].
@@ -638,18 +987,18 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 #pragma unroll
     for (int j = 0; j < kMemoTok; ++j) {
       const int64_t k = tile + int64_t(j) * kMemoThreads + tid;
-      const int64_t t = k < V ? (a.order ? a.order[k] : k) : k;
+      const int2 m = k < V ? ws.tmeta[k] : make_int2(-1, 0);
+      pk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+      const int32_t t = m.x;
       pos[j] = len[j] = 0;
-      pk[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (t >= V) {
+      if (t < 0) {
         cur[j] = kNone;
       } else if (dead_row) {
         cur[j] = kRejected;
       } else if (t == a.eos) {
         cur[j] = (flags & 2) ? kAllowed : kRejected;
       } else {
-        len[j] = a.tok_off[t + 1] - a.tok_off[t];
-        pk[j] = ws.tok16[t];
+        len[j] = m.y;
         cur[j] = len[j] == 0 ? ((flags & 4) ? kAllowed : kRejected) : 0;
       }
     }
@@ -665,7 +1014,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           const int byte = pos[j] < 16 ? packed_byte(pk[j], pos[j]) : long_byte(a, tile + int64_t(j) * kMemoThreads + tid, pos[j]);
           const uint8_t nx = T[cur[j] * 256 + byte];
           if (nx == kTUnknown) {
-            atomicOr(&req[cur[j] * 8 + (byte >> 5)], 1u << (byte & 31));
+            // request the byte's elementary interval by its first byte; with
+            // no byte edge over it the step empties the set
+            int lo, hi;
+            if (!set_interval(set_bnd[cur[j]], set_hit[cur[j]], byte, lo, hi)) {
+              cur[j] = kRejected;
+              break;
+            }
+            atomicOr(&req[cur[j] * 8 + (lo >> 5)], 1u << (lo & 31));
             waiting = true;
             break;
           }
@@ -679,139 +1035,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       }
       if (!__syncthreads_or(waiting)) break;
 
-      // resolve the requested transitions
-      if (tid == 0) nreq = 0;
-      __syncthreads();
-      for (int w = tid; w < kMemoSets * 8; w += kMemoThreads) {
-        uint32_t bits = req[w];
-        if (bits) {
-          req[w] = 0;
-          int at = atomicAdd(&nreq, __popc(bits));
-          while (bits) {
-            const int bit = __ffs(bits) - 1;
-            bits &= bits - 1;
-            if (at < kMemoReq) req_list[at] = ((w >> 3) << 8) | ((w & 7) * 32 + bit);
-            ++at;
-          }
-        }
-      }
-      __syncthreads();
-      const int n = nreq < kMemoReq ? nreq : kMemoReq;
-      if (tid < n) {
-        // every byte of the request's elementary interval [lo, hi] shares
-        // its result: the first request of an interval computes it and
-        // fills the whole interval
-        const int set = req_list[tid] >> 8, byte = req_list[tid] & 255;
-        int lo, hi;
-        const bool hit = set_interval(set_bnd[set], set_hit[set], byte, lo, hi);
-        cand_lo[tid] = int16_t(lo);
-        cand_hi[tid] = int16_t(hi);
-        if (!hit) {
-          cand_res[tid] = -5;  // rejected on the whole interval, nothing to compute
-        } else {
-          const uint32_t bit = 1u << (lo & 31);
-          const bool first = (atomicOr(&req[set * 8 + (lo >> 5)], bit) & bit) == 0;
-          cand_res[tid] = first ? 0 : -4;
-        }
-      }
-      __syncthreads();
-      {
-        // one wave per claimed transition, working sets in LDS
-        const int lane = tid & (kWave - 1), wave = tid / kWave;
-        int32_t* wsrc = work[wave][0];
-        int32_t* wdst = work[wave][1];
-        for (int r = wave; r < n; r += kMemoThreads / kWave) {
-          if (cand_res[r] < -3) continue;
-          const int set = req_list[r] >> 8, byte = req_list[r] & 255;
-          const int32_t* ps = pool + set * kConfigWords;
-          for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
-          wave_sync();
-          const bool ok = coop_advance_byte(g, wsrc, wdst, byte, lane);
-          int32_t* out = cand + r * kConfigWords;
-          for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
-          if (!ok) {
-            if (lane == 0) cand_res[r] = -1;
-          } else {
-            const uint32_t h = coop_hash(wdst, lane);
-            // the first pool set with this hash and these meaningful words;
-            // hashes compared 64 at a time
-            int found = -2;
-            const int pc = pool_count < max_sets ? pool_count : max_sets;
-            for (int k0 = 0; k0 < pc && found < 0; k0 += kWave) {
-              uint64_t m = __ballot(k0 + lane < pc && pool_hash[k0 + lane] == h);
-              while (m != 0u && found < 0) {
-                const int k = k0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
-                m &= m - 1;
-                if (coop_same(wdst, pool + k * kConfigWords, lane)) found = k;
-              }
-            }
-            if (lane < kMaxConfigs) {
-              const int nn = wdst[0];
-              const int d = lane < nn ? wdst[2 + lane] : 0;
-              cand_tops[r][lane] = d > 0 ? wdst[kF + lane * kMaxDepth + d - 1] : -1;
-              if (lane == 0) cand_n[r] = nn;
-            }
-            if (lane == 0) {
-              cand_hash[r] = h;
-              cand_res[r] = found;
-            }
-          }
-          wave_sync();
-        }
-      }
-      __syncthreads();
-      if (tid < n && cand_res[tid] == -2) {
-        const ConstFlatView mine{cand + tid * kConfigWords};
-        int lead = tid;
-        for (int j = 0; j < tid && lead == tid; ++j)
-          if (cand_res[j] == -2 && cand_hash[j] == cand_hash[tid] &&
-              same_set(ConstFlatView{cand + j * kConfigWords}, mine))
-            lead = j;
-        cand_lead[tid] = lead;
-        if (lead == tid) {
-          const int id = atomicAdd(&pool_count, 1);
-          if (id < max_sets) {
-            pool_hash[id] = cand_hash[tid];
-            set_n[id] = cand_n[tid];
-            for (int i = 0; i < kMaxConfigs; ++i) set_tops[id][i] = cand_tops[tid][i];
-            cand_id[tid] = id;
-          } else {
-            cand_id[tid] = -3;
-          }
-        }
-      }
-      __syncthreads();
-      {
-        // transitions into T, one wave per request with the lanes over the
-        // interval's bytes; then new sets into the pool, one wave per set
-        const int lane = tid & (kWave - 1), wave = tid / kWave;
-        for (int r = wave; r < n; r += kMemoThreads / kWave) {
-          const int res = cand_res[r];
-          if (res == -4) continue;  // a duplicate of another request's interval
-          const int set = req_list[r] >> 8;
-          const int id = res == -2 ? cand_id[cand_lead[r]] : res;
-          uint8_t e;
-          if (id == -1 || id == -5) {
-            e = kTDead;
-          } else if (id == -3) {
-            e = kTOverflow;
-            if (lane == 0) overflowed = 1;
-          } else {
-            e = uint8_t(id);
-          }
-          const int lo = cand_lo[r], hi = cand_hi[r];
-          for (int c = lo + lane; c <= hi; c += kWave) T[set * 256 + c] = e;
-          if (lane == 0 && res != -5) atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
-        }
-        for (int r = wave; r < n; r += kMemoThreads / kWave) {
-          if (cand_res[r] != -2 || cand_lead[r] != r || cand_id[r] < 0) continue;
-          const int32_t* src = cand + r * kConfigWords;
-          int32_t* dst = pool + cand_id[r] * kConfigWords;
-          for (int k = lane; k < kConfigWords; k += kWave) dst[k] = src[k];
-          coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]], lane);
-        }
-      }
-      __syncthreads();
+      resolve();
       if (overflowed) break;
     }
     if (overflowed) {
@@ -819,22 +1043,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       // tile again from an empty pool; a tile that fills the pool twice leaves
       // the whole row to the direct walk
       if (retry) break;
-      for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
-      for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
-      if (tid < kMaxConfigs) {
-        const int n0 = row_cfg[0];
-        const int d = tid < n0 ? row_cfg[2 + tid] : 0;
-        set_tops[0][tid] = d > 0 ? row_cfg[kF + tid * kMaxDepth + d - 1] : -1;
-        if (tid == 0) set_n[0] = n0;
-      }
-      __syncthreads();
-      if (tid < kWave) coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], tid);
-      if (tid == 0) {
-        pool_count = 1;
-        pool_hash[0] = h0_sh;
-        overflowed = 0;
-      }
-      __syncthreads();
+      reset_pool();
       retry = true;
       continue;
     }
@@ -1185,9 +1394,9 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
   if (workspace && toks->vocab_size <= kMemoMaxVocab) {
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
-    const MemoWs ws = memo_ws(workspace, rows);
+    const MemoWs ws = memo_ws(workspace, rows, toks->vocab_size);
     pack_tokens_kernel<<<unsigned((toks->vocab_size + 255) / 256), 256, 0, as_stream(stream)>>>(
-        toks->offsets, toks->bytes, toks->vocab_size, ws.tok16);
+        toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta);
     BPD_LAUNCHED();
     // BPD_PDA_MEMO_SETS lowers the interned-set limit (tests of the overflow path)
     int max_sets = kMemoSets;
@@ -1195,6 +1404,9 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
       const int v = std::atoi(e);
       if (v >= 1 && v < kMemoSets) max_sets = v;
     }
+    // BPD_PDA_MEMO_MODE=tile resolves per tile of tokens only (tests of that path)
+    const char* mode = std::getenv("BPD_PDA_MEMO_MODE");
+    const int row_mode = mode && std::strcmp(mode, "tile") == 0 ? 0 : 1;
     // stage the grammar tables in LDS when they fit beside the static arrays
     const size_t tab_bytes = (size_t(g->num_states) + 1) * 4 + size_t(g->num_edges) * 20 +
                              (size_t(g->num_states) * 2 + 3) / 4 * 4;
@@ -1205,7 +1417,7 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&pda_memo_mask_kernel)));
     const bool in_lds = fa.sharedSizeBytes + tab_bytes <= size_t(max_lds);
     pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
-        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows));
+        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), row_mode);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
   }
@@ -1262,7 +1474,7 @@ extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, 
     // the mask's workspace of the same batch: reuse its transition tables
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
-    const MemoWs ws = memo_ws(workspace, rows);
+    const MemoWs ws = memo_ws(workspace, rows, toks->vocab_size);
     const unsigned blocks = unsigned((rows + kCommitWaves - 1) / kCommitWaves);
     pda_memo_advance_kernel<<<blocks, kCommitWaves * kWave, 0, as_stream(stream)>>>(a, ws, memo_tag(g, toks, rows));
     BPD_LAUNCHED();

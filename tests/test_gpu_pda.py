@@ -15,6 +15,7 @@ from bpdecode_amd.grammar.device import (
 )
 from bpdecode_amd.grammar.gbnf import parse_gbnf
 from bpdecode_amd.grammar.pda import CompiledGrammar
+from bpdecode_amd.tokenizer import Vocabulary
 from oracle import pda as OP
 from tests._util import PDA_VOCAB as VOCAB
 from tests.golden.cases import GRAMMARS
@@ -139,14 +140,17 @@ def test_json_batch_api_b64(dev, json_case):
         assert np.array_equal(batch._configs.cpu().numpy(), mirror)
 
 
+@pytest.mark.parametrize("mode", ["row", "tile"])
 @pytest.mark.parametrize("limit", ["1", "3", "12", "40"])
-def test_json_memo_overflow_rows_match_oracle(dev, json_case, monkeypatch, limit):
-    """With the interned-set limit lowered, rows run out of sets: a tile that
-    fills the pool restarts from an empty pool, and a row whose tile fills it
-    twice is finished by the direct-walk kernel; masks stay identical."""
+def test_json_memo_overflow_rows_match_oracle(dev, json_case, monkeypatch, limit, mode):
+    """With the interned-set limit lowered, rows run out of sets: a row-wide
+    walk that fills the pool starts again tile by tile, a tile that fills it
+    restarts from an empty pool, and a row whose tile fills it twice is
+    finished by the direct-walk kernel; masks stay identical."""
     vocab, g, t = json_case
-    _log(f"case json V=151936 B=8 memo set limit {limit}")
+    _log(f"case json V=151936 B=8 memo set limit {limit} mode {mode}")
     monkeypatch.setenv("BPD_PDA_MEMO_SETS", limit)
+    monkeypatch.setenv("BPD_PDA_MEMO_MODE", mode)
     cfgs = _json_configs(g, 8, seed=21)
     gd = g.to(dev)
     pool = cfgs.to(dev)
@@ -158,6 +162,44 @@ def test_json_memo_overflow_rows_match_oracle(dev, json_case, monkeypatch, limit
     ref = lg.float().numpy().copy()
     OP.apply_mask(t, cfgs.numpy().copy(), ref)
     assert np.array_equal(got.float().cpu().numpy(), ref)
+
+
+def test_json_row_walk_equals_tile_walk(dev, json_case, monkeypatch):
+    """The row-wide walk (default) and the tile-by-tile walk of the memoised
+    kernel give the oracle's bits on 48 rows (string, number, after-value and
+    nested contexts)."""
+    vocab, g, t = json_case
+    _log("case json V=151936 B=48 row vs tile walk")
+    cfgs = _json_configs(g, 48, seed=61)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    want = OP.compute_mask(t, cfgs.numpy())
+    monkeypatch.setenv("BPD_PDA_MEMO_MODE", "row")
+    row = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+    monkeypatch.setenv("BPD_PDA_MEMO_MODE", "tile")
+    tile = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+    assert np.array_equal(row, want)
+    assert np.array_equal(tile, want)
+
+
+def test_json_long_token_rows(dev, monkeypatch):
+    """A token of 70,000 spaces (too long for the row walk's queue entries)
+    sends the rows it pauses in to the tile walk; every row still matches the
+    oracle, in both modes."""
+    raw = [bytes([i]) for i in range(256)] + [b" " * 70_000, b" \"\"", b"1, ", b"</s>"]
+    vocab = Vocabulary.from_tokens(raw, eos_id=len(raw) - 1)
+    comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
+    g = build_pda_tensors(comp, vocab, eps_reduce=True)
+    t = OP.Table(g)
+    cfgs = _json_configs(g, 24, seed=71)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    want = OP.compute_mask(t, cfgs.numpy())
+    for mode in ("row", "tile"):
+        _log(f"case json long token mode {mode}")
+        monkeypatch.setenv("BPD_PDA_MEMO_MODE", mode)
+        got = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want), mode
 
 
 def test_json_direct_walk_equals_memo(dev, json_case):
@@ -179,14 +221,16 @@ def test_json_direct_walk_equals_memo(dev, json_case):
     assert torch.equal(direct.cpu(), memo.cpu())
 
 
+@pytest.mark.parametrize("mode", ["row", "tile"])
 @pytest.mark.parametrize("limit", [None, "1", "12"])
-def test_json_commit_paths_match_oracle(dev, json_case, monkeypatch, limit):
+def test_json_commit_paths_match_oracle(dev, json_case, monkeypatch, limit, mode):
     """Commit after the mask of the same config-sets (transition tables
     reused; with the set limit lowered they hold overflow entries), after a
     mask of other config-sets (stale tables) and with no mask at all: raw
     config words and ok flags as the oracle's."""
     vocab, g, t = json_case
-    _log(f"case json commit paths limit={limit}")
+    _log(f"case json commit paths limit={limit} mode {mode}")
+    monkeypatch.setenv("BPD_PDA_MEMO_MODE", mode)
     if limit:
         monkeypatch.setenv("BPD_PDA_MEMO_SETS", limit)
     gd = g.to(dev)
