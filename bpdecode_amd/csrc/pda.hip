@@ -566,8 +566,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int16_t cand_hi[kMemoReq];
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
-  __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail;
+  __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail, loop_n;
   __shared__ uint32_t h0_sh;
+  __shared__ uint8_t loop0[256];  // T[0][c] == 0: byte c keeps set 0 (row-wide walk)
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
   const int tid = threadIdx.x;
@@ -894,8 +895,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     if (tid == 0) {
       qcount = 0;
       row_fail = 0;
+      loop_n = 0;
     }
     __syncthreads();
+    if (tid < 256) {
+      loop0[tid] = T[tid] == 0 ? 1 : 0;
+      if (T[tid] == 0) atomicAdd(&loop_n, 1);
+    }
+    __syncthreads();
+    // only a set that keeps itself on many bytes (a string or comment loop)
+    // is worth the prefix check below
+    const bool scan = loop_n >= 32;
     if (!overflowed) {
       for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
         int32_t kk[kMemoTok], tt[kMemoTok], pos[kMemoTok], len[kMemoTok];
@@ -920,6 +930,20 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             len[j] = m.y;
             cur[j] = len[j] == 0 ? ((flags & 4) ? kAllowed : kRejected) : 0;
           }
+        }
+        // the leading bytes that keep set 0 (a string loop's body) are
+        // checked together, with independent table reads, and the walk
+        // starts at the first other byte
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          if (!scan || cur[j] != 0) continue;
+          const int n = len[j] < 16 ? len[j] : 16;
+          uint32_t keep = 0u;
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (i < n) keep |= uint32_t(loop0[packed_byte(pk[j], i)]) << i;
+          const uint32_t other = ~keep & ((1u << n) - 1u);
+          pos[j] = other != 0u ? __ffs(other) - 1 : n;
         }
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
