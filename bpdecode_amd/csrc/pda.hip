@@ -847,34 +847,41 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (idx < V) q[idx] = e;
       }
     };
-    // token t from (cur, pos) until it ends, is rejected or meets a missing
-    // entry (requested; returns true)
-    auto walk = [&](int& cur, int& pos, int len, uint4 pk, int32_t t) -> bool {
-      while (cur < kWalkEnd) {
-        if (pos == len) {
-          cur = kAllowed;
-          break;
-        }
-        const int byte = pos < 16 ? packed_byte(pk, pos) : int(a.tok_bytes[a.tok_off[t] + pos]);
-        const uint8_t nx = T[cur * 256 + byte];
-        if (nx == kTUnknown) {
-          int lo, hi;
-          if (!set_interval(set_bnd[cur], set_hit[cur], byte, lo, hi)) {
-            cur = kRejected;  // no byte edge over the interval: the step empties the set
-            break;
-          }
-          const int w = cur * 8 + (lo >> 5);
-          const uint32_t bit = 1u << (lo & 31);
-          if ((req[w] & bit) == 0u) atomicOr(&req[w], bit);
+    // one step of a token from set cur by `byte`: false when the entry is
+    // missing (its interval requested, cur unchanged)
+    auto step = [&](int& cur, int& pos, int byte) -> bool {
+      const uint8_t nx = T[cur * 256 + byte];
+      if (nx == kTUnknown) {
+        int lo, hi;
+        if (!set_interval(set_bnd[cur], set_hit[cur], byte, lo, hi)) {
+          cur = kRejected;  // no byte edge over the interval: the step empties the set
           return true;
         }
-        if (nx == kTDead || nx == kTOverflow) {
-          cur = kRejected;
-        } else {
-          cur = nx;
-          ++pos;
-        }
+        const int w = cur * 8 + (lo >> 5);
+        const uint32_t bit = 1u << (lo & 31);
+        if ((req[w] & bit) == 0u) atomicOr(&req[w], bit);
+        return false;
       }
+      if (nx == kTDead || nx == kTOverflow) {
+        cur = kRejected;
+      } else {
+        cur = nx;
+        ++pos;
+      }
+      return true;
+    };
+    // token t from (cur, pos) until it ends, is rejected or meets a missing
+    // entry (requested; returns true).  Its first 16 bytes come from the
+    // record in registers: that loop has no memory wait other than the table
+    // read, so queue stores still in flight do not stall it; the bytes after
+    // them are read from tok_bytes in a second loop.
+    auto walk = [&](int& cur, int& pos, int len, uint4 pk, int32_t t) -> bool {
+      const int n16 = len < 16 ? len : 16;
+      while (cur < kWalkEnd && pos < n16)
+        if (!step(cur, pos, packed_byte(pk, pos))) return true;
+      while (cur < kWalkEnd && pos < len)
+        if (!step(cur, pos, int(a.tok_bytes[a.tok_off[t] + pos]))) return true;
+      if (cur < kWalkEnd) cur = kAllowed;
       return false;
     };
     // the tail of a token's walk: queue it if paused, else record an accept
@@ -907,17 +914,26 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     // is worth the prefix check below
     const bool scan = loop_n >= 32;
     if (!overflowed) {
-      for (int64_t tile = 0; tile < V; tile += int64_t(kMemoThreads) * kMemoTok) {
-        int32_t kk[kMemoTok], tt[kMemoTok], pos[kMemoTok], len[kMemoTok];
+      // the records of the next tile are loaded while this one is walked;
+      // queue entries are stored after all four walks of a tile
+      constexpr int64_t kTile = int64_t(kMemoThreads) * kMemoTok;
+      int2 nm[kMemoTok];
+      uint4 npk[kMemoTok];
+#pragma unroll
+      for (int j = 0; j < kMemoTok; ++j) {
+        const int64_t k = int64_t(j) * kMemoThreads + tid;
+        nm[j] = k < V ? ws.tmeta[k] : make_int2(-1, 0);
+        npk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+      }
+      for (int64_t tile = 0; tile < V; tile += kTile) {
+        int32_t tt[kMemoTok], pos[kMemoTok], len[kMemoTok];
         int cur[kMemoTok];
         uint4 pk[kMemoTok];
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
-          const int64_t k = tile + int64_t(j) * kMemoThreads + tid;
-          const int2 m = k < V ? ws.tmeta[k] : make_int2(-1, 0);
-          pk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+          const int2 m = nm[j];
+          pk[j] = npk[j];
           const int32_t t = m.x;
-          kk[j] = int32_t(k);
           tt[j] = t;
           pos[j] = len[j] = 0;
           if (t < 0) {
@@ -930,6 +946,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             len[j] = m.y;
             cur[j] = len[j] == 0 ? ((flags & 4) ? kAllowed : kRejected) : 0;
           }
+        }
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const int64_t k = tile + kTile + int64_t(j) * kMemoThreads + tid;
+          nm[j] = k < V ? ws.tmeta[k] : make_int2(-1, 0);
+          npk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
         }
         // the leading bytes that keep set 0 (a string loop's body) are
         // checked together, with independent table reads, and the walk
@@ -945,11 +967,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           const uint32_t other = ~keep & ((1u << n) - 1u);
           pos[j] = other != 0u ? __ffs(other) - 1 : n;
         }
+        bool paused[kMemoTok];
 #pragma unroll
-        for (int j = 0; j < kMemoTok; ++j) {
-          const bool paused = walk(cur[j], pos[j], len[j], pk[j], tt[j]);
-          settle(paused, cur[j], pos[j], len[j], kk[j], tt[j], qin);
-        }
+        for (int j = 0; j < kMemoTok; ++j) paused[j] = walk(cur[j], pos[j], len[j], pk[j], tt[j]);
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j)
+          settle(paused[j], cur[j], pos[j], len[j], int32_t(tile + int64_t(j) * kMemoThreads + tid), tt[j], qin);
       }
     }
     __syncthreads();
