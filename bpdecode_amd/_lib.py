@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
@@ -25,6 +25,7 @@ FLAG_STATE_RANGE, FLAG_TOKEN_RANGE = 1, 2
 PDA_MAX_CONFIGS = 8
 PDA_MAX_DEPTH = 32
 PDA_CONFIG_WORDS = 2 + PDA_MAX_CONFIGS + PDA_MAX_CONFIGS * PDA_MAX_DEPTH
+SOFT_MEMBER_CHUNK, SOFT_MEMBER_CAP_MAX = 4096, 1024  # BPD_SOFT_MEMBER_CHUNK / _CAP_MAX
 
 _DTYPE_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 _INDEX_CODE = {torch.int32: INDEX_I32, torch.int64: INDEX_I64}
@@ -58,7 +59,7 @@ class SoftClassesC(C.Structure):
         ("num_classes", i32), ("num_members", i32), ("num_pieces", i32), ("num_pairs", i32),
         ("class_off", vp), ("class_tok", vp), ("class_piece", vp), ("piece_off", vp),
         ("state_off", vp), ("pair_class", vp), ("pair_next", vp), ("token_class", vp),
-        ("token_class16", vp),
+        ("token_class16", vp), ("chunk_members", vp), ("chunk_cap", i32),
     ]
 
 

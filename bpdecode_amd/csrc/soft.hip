@@ -562,6 +562,87 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_classes_kernel(
   }
 }
 
+// Class statistics from the chunk's member list instead of the per-token
+// class map: the chunk is staged in LDS while its row logsumexp is formed,
+// then only the classed tokens (Cap fixed slots per chunk, (offset << 16 |
+// class), 0xFFFFFFFF empty; loaded with the logits) take part in the class
+// max and sum.  Same per-class arithmetic as prior_stats_classes_kernel.
+// Dynamic LDS: kStatChunk floats, then C class maxima and C sums.
+template <int Cap>
+__global__ __launch_bounds__(kPriorThreads) void prior_stats_members_kernel(
+    const float* __restrict__ logits, int64_t ld, int64_t V, const uint32_t* __restrict__ members,
+    int32_t C, PriorWs ws) {
+  static_assert(kStatChunk == BPD_SOFT_MEMBER_CHUNK, "member lists are cut at the statistics chunk");
+  extern __shared__ __align__(16) float smem[];
+  float4* xs = reinterpret_cast<float4*>(smem);
+  int32_t* cmax = reinterpret_cast<int32_t*>(smem + kStatChunk);
+  float* csum = smem + kStatChunk + C;
+  constexpr int kE = 4 * kStatLoads;
+  constexpr int kM = Cap / kPriorThreads;
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const float* row = logits + b * ld;
+  const int64_t base = int64_t(g) * kStatChunk;
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    cmax[c] = ord_of(-INFINITY);
+    csum[c] = 0.0f;
+  }
+  float x[kE];
+#pragma unroll
+  for (int u = 0; u < kStatLoads; ++u) {
+    const int64_t t = base + (int64_t(u) * kPriorThreads + threadIdx.x) * 4;
+    float4 xv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (t < V) xv = *reinterpret_cast<const float4*>(row + t);
+    xs[u * kPriorThreads + threadIdx.x] = xv;
+    x[4 * u] = xv.x;
+    x[4 * u + 1] = xv.y;
+    x[4 * u + 2] = xv.z;
+    x[4 * u + 3] = xv.w;
+  }
+  uint32_t mm[kM];
+#pragma unroll
+  for (int j = 0; j < kM; ++j) mm[j] = members[int64_t(g) * Cap + j * kPriorThreads + threadIdx.x];
+  // chunk logsumexp
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < kE; ++e) m = fmaxf(m, x[e]);
+  Lse acc{-INFINITY, 0.0f};
+  if (m != -INFINITY) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kE; ++e) sum += exp_shift(x[e], m);
+    acc = Lse{m, sum};
+  }
+  acc = block_lse<kPriorThreads>(acc);  // its barriers also publish the staged chunk and the LDS init
+  if (threadIdx.x == 0) {
+    ws.part[(b * G + g) * 2] = acc.m;
+    ws.part[(b * G + g) * 2 + 1] = acc.s;
+  }
+  // per-class max, then per-class sum of exp(x - max), over the members only
+  const float* xf = smem;
+  float v[kM];
+#pragma unroll
+  for (int j = 0; j < kM; ++j) {
+    v[j] = mm[j] != 0xFFFFFFFFu ? xf[mm[j] >> 16] : -INFINITY;
+    if (v[j] != -INFINITY) atomicMax(&cmax[mm[j] & 0xFFFFu], ord_of(v[j]));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kM; ++j) {
+    if (v[j] != -INFINITY) {
+      const int32_t c = int32_t(mm[j] & 0xFFFFu);
+      atomicAdd(&csum[c], exp_shift(v[j], float_of_ord(cmax[c])));
+    }
+  }
+  __syncthreads();
+  float* out = ws.mid + (b * G + g) * int64_t(C) * 2;
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    out[2 * c] = float_of_ord(cmax[c]);
+    out[2 * c + 1] = csum[c];
+  }
+}
+
 // Pieces stats, grid (G + Gp, rows): block g < G takes vocab chunk g
 // (partial row logsumexp), blocks G.. the class pieces (one wave per piece,
 // unnormalised piece logsumexp).
@@ -989,7 +1070,19 @@ extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_
                                                                          cls.token_class,       \
                                                                          cls.token_class16,     \
                                                                          cls.num_classes, ws)
-    if (narrow && nvec) BPD_PRIOR_STATS(true, true);
+    // BPD_SOFT_MEMBERS=0 keeps the class-map kernel (tests of that path)
+    const char* me = std::getenv("BPD_SOFT_MEMBERS");
+    const bool members = vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) && cls.chunk_members != nullptr &&
+                         cls.num_classes < 65535 && !(me && std::strcmp(me, "0") == 0) &&
+                         (cls.chunk_cap == 256 || cls.chunk_cap == 512 || cls.chunk_cap == 1024);
+    const size_t mlds = size_t(kStatChunk) * sizeof(float) + size_t(cls.num_classes) * 8;
+    if (members && cls.chunk_cap == 256)
+      prior_stats_members_kernel<256><<<grid, kPriorThreads, mlds, st>>>(logits, ld, vocab, cls.chunk_members, cls.num_classes, ws);
+    else if (members && cls.chunk_cap == 512)
+      prior_stats_members_kernel<512><<<grid, kPriorThreads, mlds, st>>>(logits, ld, vocab, cls.chunk_members, cls.num_classes, ws);
+    else if (members)
+      prior_stats_members_kernel<1024><<<grid, kPriorThreads, mlds, st>>>(logits, ld, vocab, cls.chunk_members, cls.num_classes, ws);
+    else if (narrow && nvec) BPD_PRIOR_STATS(true, true);
     else if (narrow) BPD_PRIOR_STATS(false, true);
     else if (vec) BPD_PRIOR_STATS(true, false);
     else BPD_PRIOR_STATS(false, false);
@@ -1133,6 +1226,29 @@ extern "C" int bpd_host_soft_classes(const int32_t* tok_next, int32_t num_states
   if (out->token_class16 && C < 65535)
     for (int64_t t = 0; t < V; ++t)
       out->token_class16[t] = cls[size_t(t)] < 0 ? uint16_t(0xFFFF) : uint16_t(cls[size_t(t)]);
+  out->chunk_cap = 0;
+  if (out->chunk_members && C < 65535) {
+    const int64_t G = (V + BPD_SOFT_MEMBER_CHUNK - 1) / BPD_SOFT_MEMBER_CHUNK;
+    int64_t most = 0;
+    for (int64_t g = 0; g < G; ++g) {
+      int64_t n = 0;
+      for (int64_t t = g * BPD_SOFT_MEMBER_CHUNK; t < V && t < (g + 1) * BPD_SOFT_MEMBER_CHUNK; ++t)
+        n += cls[size_t(t)] >= 0;
+      most = n > most ? n : most;
+    }
+    const int32_t cap = most <= 256 ? 256 : most <= 512 ? 512 : most <= BPD_SOFT_MEMBER_CAP_MAX ? 1024 : 0;
+    if (cap) {
+      for (int64_t g = 0; g < G; ++g) {
+        uint32_t* row = out->chunk_members + g * cap;
+        int32_t n = 0;
+        for (int64_t t = g * BPD_SOFT_MEMBER_CHUNK; t < V && t < (g + 1) * BPD_SOFT_MEMBER_CHUNK; ++t)
+          if (cls[size_t(t)] >= 0)
+            row[n++] = (uint32_t(t - g * BPD_SOFT_MEMBER_CHUNK) << 16) | uint32_t(cls[size_t(t)]);
+        for (; n < cap; ++n) row[n] = 0xFFFFFFFFu;
+      }
+      out->chunk_cap = cap;
+    }
+  }
   return BPD_OK;
 }
 

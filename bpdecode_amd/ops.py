@@ -55,7 +55,9 @@ class SoftClasses:
     ``pair_class/pair_next[state_off[s]:state_off[s + 1]]``; ``token_class``
     maps each token to its class (-1: rejected in every state), and
     ``token_class16`` is the same map as int16 (-1 read as 0xFFFF) when
-    there are fewer than 65535 classes."""
+    there are fewer than 65535 classes; ``chunk_members`` lists the classed
+    tokens of each 4096-token chunk in ``chunk_cap`` slots per chunk
+    (offset << 16 | class, -1 padded) when no chunk has more than 1024."""
 
     class_off: torch.Tensor
     class_tok: torch.Tensor
@@ -68,6 +70,8 @@ class SoftClasses:
     num_members: int = 0
     num_pairs: int = 0
     token_class16: torch.Tensor | None = None
+    chunk_members: torch.Tensor | None = None
+    chunk_cap: int = 0
 
     def __post_init__(self) -> None:
         self._c: _lib.SoftClassesC | None = None
@@ -84,13 +88,16 @@ class SoftClasses:
     def to(self, device) -> SoftClasses:
         return SoftClasses(*(getattr(self, n).to(device) for n in _SOFT_ARRAYS),
                            num_members=self.num_members, num_pairs=self.num_pairs,
-                           token_class16=None if self.token_class16 is None else self.token_class16.to(device))
+                           token_class16=None if self.token_class16 is None else self.token_class16.to(device),
+                           chunk_members=None if self.chunk_members is None else self.chunk_members.to(device),
+                           chunk_cap=self.chunk_cap)
 
     def c_struct(self) -> _lib.SoftClassesC:
         if self._c is None:
             self._c = _lib.SoftClassesC(self.num_classes, self.num_members, self.num_pieces,
                                         self.num_pairs, *(ptr(getattr(self, n)) for n in _SOFT_ARRAYS),
-                                        ptr(self.token_class16))
+                                        ptr(self.token_class16), ptr(self.chunk_members),
+                                        self.chunk_cap if self.chunk_members is not None else 0)
         return self._c
 
     def workspace(self, rows: int, device: torch.device, stream: int) -> tuple[torch.Tensor, int]:
@@ -120,9 +127,14 @@ class SoftClasses:
             setattr(c, n, ptr(arrays[n]))
         tc16 = torch.empty(V, dtype=torch.int16) if c.num_classes < 65535 else None
         c.token_class16 = ptr(tc16)
+        chunks = (V + _lib.SOFT_MEMBER_CHUNK - 1) // _lib.SOFT_MEMBER_CHUNK
+        members = torch.empty(chunks * _lib.SOFT_MEMBER_CAP_MAX, dtype=torch.int32)
+        c.chunk_members = ptr(members)
         check(lib().bpd_host_soft_classes(ptr(tn), S, V, C.byref(c)))
+        cap = int(c.chunk_cap)
         return cls(*(arrays[n][:sizes[n]] for n in _SOFT_ARRAYS), num_members=c.num_members,
-                   num_pairs=c.num_pairs, token_class16=tc16)
+                   num_pairs=c.num_pairs, token_class16=tc16,
+                   chunk_members=members[:chunks * cap].clone() if cap else None, chunk_cap=cap)
 
 
 @dataclass

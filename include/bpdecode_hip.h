@@ -329,7 +329,19 @@ typedef struct BpdSoftClasses {
   int32_t* pair_next;   /* [num_pairs] */
   int32_t* token_class; /* [vocab] */
   uint16_t* token_class16; /* [vocab] optional: token_class as uint16, 0xFFFF for -1 */
+  /* optional: the classed tokens of each BPD_SOFT_MEMBER_CHUNK-token chunk of
+   * the vocab, in token order, as (offset in chunk << 16 | class), padded
+   * with 0xFFFFFFFF to chunk_cap entries per chunk.  The caller provides
+   * ceil(vocab / BPD_SOFT_MEMBER_CHUNK) * BPD_SOFT_MEMBER_CAP_MAX entries; the
+   * builder sets chunk_cap (256, 512 or 1024), or 0 when a chunk holds more
+   * classed tokens than that or there are 65535 classes or more (the list is
+   * then unused). */
+  uint32_t* chunk_members;
+  int32_t chunk_cap;
 } BpdSoftClasses;
+
+#define BPD_SOFT_MEMBER_CHUNK 4096
+#define BPD_SOFT_MEMBER_CAP_MAX 1024
 
 int bpd_host_soft_classes(const int32_t* tok_next, int32_t num_states, int64_t vocab,
                           BpdSoftClasses* out);

@@ -202,6 +202,37 @@ def test_json_long_token_rows(dev, monkeypatch):
         assert np.array_equal(got, want), mode
 
 
+def test_json_bench_batch_every_row(dev, json_case):
+    """The benchmark's batch (256 rows, prefixes of 0-200 bytes at depths
+    0-8, the same seed): every row's mask and committed config-set against
+    the oracle, one step."""
+    vocab, g, t = json_case
+    _log("case json V=151936 B=256 bench rows, mask + commit")
+    rng = np.random.default_rng(5)
+    rows = []
+    while len(rows) < 256:
+        d = int(rng.integers(0, 9))
+        c = g.init_config()
+        if g.feed(c, synth.json_prefix(rng, d)):
+            rows.append(c)
+    cfgs = torch.stack(rows)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    lg = synth.logits(256, vocab.size, 3.0, torch.float32, seed=11)
+    got = lg.to(dev)
+    pda_mask_(got, gd, pool)
+    ref = lg.numpy().copy()
+    OP.apply_mask(t, cfgs.numpy().copy(), ref)
+    assert np.array_equal(got.cpu().numpy(), ref)
+    toks = torch.multinomial(torch.softmax(torch.from_numpy(ref), dim=-1), 1,
+                             generator=torch.Generator().manual_seed(12)).view(-1).to(torch.int32)
+    ok, _ = pda_step(pool, gd, toks.to(dev))
+    mirror = cfgs.numpy().copy()
+    ok_o = OP.advance(t, mirror, toks.numpy())
+    assert ok.cpu().tolist() == ok_o.tolist() and ok_o.all()
+    assert np.array_equal(pool.cpu().numpy(), mirror)
+
+
 def test_json_direct_walk_equals_memo(dev, json_case):
     """The C ABI without a workspace runs the direct per-token walk; with one,
     the memoised kernel: identical bits."""

@@ -123,10 +123,13 @@ def test_prior_unaligned_vocab(dev):
     assert torch.equal(w[:, V:].cpu(), wide[:, V:])
 
 
-def test_prior_email_serving(dev):
+@pytest.mark.parametrize("members", ["1", "0"])
+def test_prior_email_serving(dev, members, monkeypatch):
     """B=128, V=151,936, k=4 over the email DFA: four rows against the
     oracle, every row against the alpha-free identity (alpha = 0 leaves
-    log_softmax on tokens whose k-1 lookahead is finite)."""
+    log_softmax on tokens whose k-1 lookahead is finite); class statistics
+    from the chunk member lists and from the class map."""
+    monkeypatch.setenv("BPD_SOFT_MEMBERS", members)
     vocab = synth.serving_vocab(151_936, seed=1)
     fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
     tn = fsa.tok_next.numpy()
@@ -134,6 +137,7 @@ def test_prior_email_serving(dev):
     st = synth.random_walk_states(fsa.tok_next, fsa.start, fsa.eos_id, 128, 40, seed=5).to(torch.int32)
     x = synth.logits(128, V, std=3.0, dtype=torch.float32, seed=11)
     fd = fsa.to(dev)
+    assert fd.ensure_soft_classes().chunk_cap in (256, 512, 1024)
     got = x.to(dev)
     ops.apply_soft_prior_(got, fd, st.to(dev), 4, 1.0)
     got = got.cpu().double().numpy()
@@ -181,10 +185,11 @@ def test_prior_pieces_path_email(dev, monkeypatch):
     assert close(b, a)
 
 
-def test_prior_wide_class_map_and_extreme_logits(dev):
-    """The statistics read the uint16 class map when it is present and the
-    int32 one otherwise: same results.  Rows mixing -inf, very negative and
-    large logits keep every class sum exact (checked against the oracle)."""
+def test_prior_wide_class_map_and_extreme_logits(dev, monkeypatch):
+    """The statistics read the chunk member lists, else the uint16 class map
+    when it is present, else the int32 one: same results.  Rows mixing -inf,
+    very negative and large logits keep every class sum exact (checked
+    against the oracle)."""
     fsa = FsaTensors.build("-?[0-9]+(\\.[0-9]+)?", TOY_VOCAB).densify()
     S, V = fsa.tok_next.shape
     st = torch.tensor(list(range(S)) * 2, dtype=torch.int32)
@@ -201,6 +206,10 @@ def test_prior_wide_class_map_and_extreme_logits(dev):
     a = x.to(dev)
     ops.apply_soft_prior_(a, fd, st.to(dev), 4, 0.8)
     assert close(a.cpu().double().numpy(), want)
+    monkeypatch.setenv("BPD_SOFT_MEMBERS", "0")
+    m = x.to(dev)
+    ops.apply_soft_prior_(m, fd, st.to(dev), 4, 0.8)
+    assert close(m.cpu().double().numpy(), want)
     sc.token_class16, sc._c = None, None
     b = x.to(dev)
     ops.apply_soft_prior_(b, fd, st.to(dev), 4, 0.8)

@@ -38,6 +38,19 @@ def check_classes(tn: np.ndarray, sc: SoftClasses) -> None:
     assert (norm[:, cls < 0] == -1).all() and (cls[(norm >= 0).any(axis=0)] >= 0).all()
     assert np.array_equal(sc.token_class.numpy(), cls)
     assert sc.token_class16 is not None and np.array_equal(sc.token_class16.numpy().astype(np.int64), cls)
+    # member lists per 4096-token chunk: (offset << 16 | class) in token order, -1 padded
+    chunks = [np.nonzero(cls[g:g + 4096] >= 0)[0] for g in range(0, V, 4096)]
+    most = max(len(m) for m in chunks)
+    cap = next((c for c in (256, 512, 1024) if most <= c), 0)
+    assert sc.chunk_cap == cap
+    if cap == 0:
+        assert sc.chunk_members is None
+    else:
+        got = sc.chunk_members.numpy().view(np.uint32).reshape(len(chunks), cap)
+        for g, m in enumerate(chunks):
+            want = (m.astype(np.uint64) << 16) | cls[g * 4096 + m].astype(np.uint64)
+            assert np.array_equal(got[g, :len(m)], want.astype(np.uint32))
+            assert (got[g, len(m):] == 0xFFFFFFFF).all()
     po, cp = sc.piece_off.numpy(), sc.class_piece.numpy()
     assert po[0] == 0 and po[-1] == len(mem) and np.all(np.diff(po) > 0) and np.all(np.diff(po) <= 256)
     for c in range(sc.num_classes):
@@ -53,6 +66,22 @@ def check_classes(tn: np.ndarray, sc: SoftClasses) -> None:
 def test_classes_toy(pattern):
     fsa = FsaTensors.build(pattern, TOY_VOCAB).densify()
     check_classes(fsa.tok_next.numpy(), SoftClasses.build(fsa.tok_next))
+
+
+@pytest.mark.parametrize("per_chunk", [0, 1, 300, 1024, 1025, 4096])
+def test_chunk_member_capacity(per_chunk):
+    """Chunks holding up to 1024 classed tokens get member lists with 256,
+    512 or 1024 slots; a chunk with more turns the lists off."""
+    V = 9000
+    rng = np.random.default_rng(per_chunk)
+    tn = np.full((2, V), -1, dtype=np.int32)
+    for g in range(0, V, 4096):
+        n = min(per_chunk, min(V, g + 4096) - g)
+        pick = g + rng.choice(min(V, g + 4096) - g, size=n, replace=False)
+        tn[0, pick] = rng.integers(0, 2, size=n)
+        tn[1, pick] = 1
+    sc = SoftClasses.build(torch.from_numpy(tn))
+    check_classes(tn, sc)
 
 
 def test_classes_out_of_range_entries_read_as_rejected():
