@@ -534,6 +534,25 @@ __device__ inline bool set_interval(const uint32_t* bnd, const uint32_t* hit, in
   return (hit[byte >> 5] >> b) & 1u;
 }
 
+// First byte of the elementary interval of `byte` (as set_interval's lo),
+// from the set's interval-start bitmap read as two 16-byte words: the walk
+// asks for it on every missing entry, so it avoids set_interval's chain of
+// dependent reads.
+__device__ inline int interval_start(const uint32_t* bnd, int byte) {
+  const uint4 a = reinterpret_cast<const uint4*>(bnd)[0];
+  const uint4 b = reinterpret_cast<const uint4*>(bnd)[1];
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const int bw = byte >> 5, bb = byte & 31;
+  const uint32_t le = bb == 31 ? 0xFFFFFFFFu : ((2u << bb) - 1u);  // bits 0..bb
+  int lo = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t m = k < bw ? w[k] : (k == bw ? (w[k] & le) : 0u);
+    if (m != 0u) lo = k * 32 + 31 - __clz(m);
+  }
+  return lo;
+}
+
 // byte p of the token at walk position k (its first 16 bytes are packed)
 __device__ __forceinline__ int long_byte(const MaskArgs& a, int64_t k, int32_t p) {
   const int64_t t = a.order ? a.order[k] : k;
@@ -549,7 +568,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
-  __shared__ uint32_t set_bnd[kMemoSets][8];  // interval starts of each set's bytes
+  __shared__ __align__(16) uint32_t set_bnd[kMemoSets][8];  // interval starts of each set's bytes
   __shared__ uint32_t set_hit[kMemoSets][8];  // bytes some top's byte edge contains
   __shared__ int32_t cand_tops[kMemoReq][kMaxConfigs];
   __shared__ int32_t cand_n[kMemoReq];
@@ -852,11 +871,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     auto step = [&](int& cur, int& pos, int byte) -> bool {
       const uint8_t nx = T[cur * 256 + byte];
       if (nx == kTUnknown) {
-        int lo, hi;
-        if (!set_interval(set_bnd[cur], set_hit[cur], byte, lo, hi)) {
-          cur = kRejected;  // no byte edge over the interval: the step empties the set
+        if (((set_hit[cur][byte >> 5] >> (byte & 31)) & 1u) == 0u) {
+          cur = kRejected;  // no byte edge contains it: the step empties the set
           return true;
         }
+        const int lo = interval_start(set_bnd[cur], byte);
         const int w = cur * 8 + (lo >> 5);
         const uint32_t bit = 1u << (lo & 31);
         if ((req[w] & bit) == 0u) atomicOr(&req[w], bit);
@@ -1063,11 +1082,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           if (nx == kTUnknown) {
             // request the byte's elementary interval by its first byte; with
             // no byte edge over it the step empties the set
-            int lo, hi;
-            if (!set_interval(set_bnd[cur[j]], set_hit[cur[j]], byte, lo, hi)) {
+            if (((set_hit[cur[j]][byte >> 5] >> (byte & 31)) & 1u) == 0u) {
               cur[j] = kRejected;
               break;
             }
+            const int lo = interval_start(set_bnd[cur[j]], byte);
             atomicOr(&req[cur[j] * 8 + (lo >> 5)], 1u << (lo & 31));
             waiting = true;
             break;
