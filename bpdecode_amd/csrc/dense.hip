@@ -140,7 +140,11 @@ __global__ __launch_bounds__(kThreads) void dense_mask_vec_kernel(
 }
 
 // Mask from the packed allow-bit table: byte (col / 8) of a state's bit row
-// holds the verdicts of the lane's 8 columns.
+// holds the verdicts of the lane's 8 columns.  The verdicts come first: a
+// lane whose 8 columns are all rejected writes the fill without reading
+// them, one whose columns are all allowed touches nothing, and only the
+// mixed ones read, blend and write (the result is the same; on a DFA that
+// allows a few percent of the vocab most logits are never read).
 template <int E>
 __global__ __launch_bounds__(kThreads) void dense_mask_bits_kernel(
     uint8_t* __restrict__ logits, int64_t ld_bytes, const uint8_t* __restrict__ bits,
@@ -161,15 +165,6 @@ __global__ __launch_bounds__(kThreads) void dense_mask_bits_kernel(
 #pragma unroll
   for (int i = 0; i < kBitRows; ++i) {
     const int64_t r = r0 + i;
-    if (r < rows) {
-      const u32x4* p = reinterpret_cast<const u32x4*>(logits + r * ld_bytes + col * E);
-#pragma unroll
-      for (int k = 0; k < E / 2; ++k) lg[i][k] = p[k];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kBitRows; ++i) {
-    const int64_t r = r0 + i;
     slot[i] = (r < rows) ? (slots ? slots[r] : r) : -1;
   }
 #pragma unroll
@@ -180,10 +175,28 @@ __global__ __launch_bounds__(kThreads) void dense_mask_bits_kernel(
 #pragma unroll
   for (int i = 0; i < kBitRows; ++i) {
     const int64_t r = r0 + i;
+    if (r < rows && m[i] != 0u && m[i] != 0xFFu) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(logits + r * ld_bytes + col * E);
+#pragma unroll
+      for (int k = 0; k < E / 2; ++k) lg[i][k] = p[k];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kBitRows; ++i) {
+    const int64_t r = r0 + i;
     if (r >= rows) break;
     if (st[i] >= num_states && err && threadIdx.x == 0 && cs == 0) atomicOr(err, BPD_FLAG_STATE_RANGE);
-    u32x4* p = reinterpret_cast<u32x4*>(logits + r * ld_bytes + col * E);
     const uint32_t mm = m[i];
+    if (mm == 0xFFu) continue;
+    u32x4* p = reinterpret_cast<u32x4*>(logits + r * ld_bytes + col * E);
+    if (mm == 0u) {
+      const u32x4 f = (E == 2) ? u32x4{fill | (fill << 16), fill | (fill << 16),
+                                       fill | (fill << 16), fill | (fill << 16)}
+                               : u32x4{fill, fill, fill, fill};
+#pragma unroll
+      for (int k = 0; k < E / 2; ++k) p[k] = f;
+      continue;
+    }
     if (E == 2) {
       u32x4 v = lg[i][0];
       v.x = ((mm & 1u) ? (v.x & 0xFFFFu) : fill) | (((mm & 2u) ? (v.x >> 16) : fill) << 16);
