@@ -560,6 +560,26 @@ def bench_pda(args) -> int:
         }
         key = "parity_vs_reference_sampled_rows" if use_ref else "parity_vs_oracle_sampled_rows"
         out[key] = bool(np.array_equal(lg, masked[:n].numpy()))
+        if use_ref:
+            # the same reference call split over host threads by rows, on
+            # two rows per thread
+            threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", "16") or 16), os.cpu_count() or 1, 16))
+            npar = min(2 * threads, B)
+            subp = cfgs[:npar].numpy().copy()
+            lgp = raw[:npar].numpy().copy()
+            c0 = time.perf_counter()
+            OR.pda_apply_mask_threads(t, subp, lgp, threads)
+            par_s = time.perf_counter() - c0
+            out["cpu_baseline_rows_parallel"] = {
+                "value": round(par_s / npar * B * 1e6, 1),
+                "unit": "us/step",
+                "cores": threads,
+                "kind": "reference",
+                "sample": (f"mask of {npar} rows of the first timed step through the reference's "
+                           f"apply_mask_pda_batch, rows split over {threads} host threads "
+                           f"(oracle/_ref), scaled to B={B}"),
+                "parity_vs_device": bool(np.array_equal(lgp, masked[:npar].numpy())),
+            }
     print(json.dumps(out))
     return 0
 

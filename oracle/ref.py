@@ -56,6 +56,16 @@ def pda_apply_mask(t: Table, configs: np.ndarray, logits: np.ndarray, neg_inf=fl
     return logits
 
 
+def pda_apply_mask_threads(t: Table, configs: np.ndarray, logits: np.ndarray, threads: int,
+                           neg_inf=float("-inf")):
+    """apply_mask_pda_batch over `threads` host threads, rows split evenly."""
+    configs = np.ascontiguousarray(configs, dtype=np.int32)
+    lib().ref_pda_apply_mask_threads(*t.args(), C.c_int32(t.vocab), C.c_int32(t.eos), _p(t.toff),
+                                     _p(t.tb), _p(configs), C.c_int32(configs.shape[0]), _p(logits),
+                                     C.c_float(neg_inf), C.c_int32(threads))
+    return logits
+
+
 def pda_advance(t: Table, configs: np.ndarray, tokens) -> np.ndarray:
     tk = np.ascontiguousarray(tokens, dtype=np.int32)
     ok = np.zeros(tk.size, dtype=np.uint8)

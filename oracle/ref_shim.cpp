@@ -5,6 +5,7 @@
 // reference's structs (mask.hpp:18-35, pda.hpp:46-91) and calls its
 // functions; no reference code is restated here.
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "bpdecode/mask.hpp"
@@ -99,6 +100,25 @@ void ref_pda_apply_mask(TBL, int32_t vocab, int32_t eos, const int32_t* toff, co
                         const int32_t* configs, int32_t batch, float* logits, float neg_inf) {
   apply_mask_pda_batch(table(TPASS), tokens(vocab, eos, toff, tb),
                        reinterpret_cast<const PdaConfigSet*>(configs), batch, logits, neg_inf);
+}
+
+// The same call split over `threads` host threads by rows (each row's mask
+// is independent; the reference's tables are shared read-only): the
+// parallel CPU baseline.
+void ref_pda_apply_mask_threads(TBL, int32_t vocab, int32_t eos, const int32_t* toff,
+                                const uint8_t* tb, const int32_t* configs, int32_t batch,
+                                float* logits, float neg_inf, int32_t threads) {
+  const PdaTable g = table(TPASS);
+  const PdaTokens t = tokens(vocab, eos, toff, tb);
+  const PdaConfigSet* cs = reinterpret_cast<const PdaConfigSet*>(configs);
+  if (threads < 1) threads = 1;
+  std::vector<std::thread> pool;
+  const int32_t per = (batch + threads - 1) / threads;
+  for (int32_t r0 = 0; r0 < batch; r0 += per) {
+    const int32_t n = batch - r0 < per ? batch - r0 : per;
+    pool.emplace_back([&, r0, n] { apply_mask_pda_batch(g, t, cs + r0, n, logits + int64_t(r0) * vocab, neg_inf); });
+  }
+  for (auto& th : pool) th.join();
 }
 
 void ref_pda_advance(TBL, int32_t vocab, int32_t eos, const int32_t* toff, const uint8_t* tb,

@@ -131,6 +131,27 @@ def test_pda_oracle_matches_reference(idx, reduce):
         assert np.array_equal(a, b)
 
 
+@need_ref
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_reference_rows_over_threads_match_one_call(threads):
+    """The parallel CPU baseline (the reference call over row slices on host
+    threads) gives the single call's logits."""
+    g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(GRAMMARS[-1])), PVOCAB, eps_reduce=True)
+    t = OP.Table(g)
+    rng = np.random.default_rng(threads)
+    cfg = np.repeat(R.pda_init(t)[None], 7, 0)
+    for r in range(7):
+        for _ in range(r):
+            ma = R.pda_compute_mask(t, cfg[r:r + 1])[0]
+            allowed = [k for k in range(t.vocab) if ma[k >> 5] >> (k & 31) & 1 and k != t.eos]
+            if allowed:
+                R.pda_advance(t, cfg[r:r + 1], [int(rng.choice(allowed))])
+    x = rng.standard_normal((7, t.vocab)).astype(np.float32)
+    one = R.pda_apply_mask(t, cfg.copy(), x.copy())
+    par = R.pda_apply_mask_threads(t, cfg.copy(), x.copy(), threads)
+    assert np.array_equal(one, par)
+
+
 # ------------------------------------------------------ dense known answers
 def ab_fsa():
     # test_mask.cpp:14-39: "ab" over 2 classes; token 3 has an invalid class
