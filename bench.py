@@ -77,6 +77,17 @@ class HipEvents:
         return ms.value
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _profiled_traffic(name: str, kernel: str):
     """HBM bytes per launch of ``kernel`` from the committed rocprof counter
     summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration), or
@@ -328,6 +339,7 @@ def main(argv=None) -> int:
                       f"replayed {args.cpu_repeats}x through the reference's ATen op sequence "
                       f"(ops.py:271-276 mask, ops.py:301-306 commit) on CPU tensors",
             "host_cpus": os.cpu_count(),
+            "host_cpu_model": _cpu_model(),
         }
         out["parity_vs_oracle"] = parity
     print(json.dumps(out))
@@ -557,6 +569,7 @@ def bench_pda(args) -> int:
                           if use_ref else "oracle/pda_oracle.c (C restatement of pda_cpu.cpp, one thread)")
                        + f", scaled to B={B}"),
             "host_cpus": os.cpu_count(),
+            "host_cpu_model": _cpu_model(),
         }
         key = "parity_vs_reference_sampled_rows" if use_ref else "parity_vs_oracle_sampled_rows"
         out[key] = bool(np.array_equal(lg, masked[:n].numpy()))
@@ -673,6 +686,7 @@ def bench_soft(args) -> int:
             "sample": f"{n} rows through oracle/soft.py prior_lookahead (float64 numpy, dense "
                       f"[S, V] gathers per round), scaled to B={B}",
             "host_cpus": os.cpu_count(),
+            "host_cpu_model": _cpu_model(),
         }
         out["parity_vs_oracle_sampled_rows"] = ok
     print(json.dumps(out))
