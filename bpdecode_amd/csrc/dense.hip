@@ -33,7 +33,9 @@ constexpr int kThreads = 256;
 constexpr int kVec = 8;                          // columns per lane
 constexpr int64_t kSlab = int64_t(kThreads) * kVec;  // columns per block
 constexpr int kRows = 2;                         // rows per block (int32 table)
-constexpr int kBitRows = 4;                      // rows per block (bit table)
+// rows per block (bit table): 2, or 4 from 512 rows on, which keeps about
+// 9,600 blocks at V = 151,936 (measured best at 256 and 512 rows)
+constexpr int kBitRowsSmall = 2, kBitRowsLarge = 4, kBitRowsLargeFrom = 512;
 constexpr int kXcds = 8;
 
 __device__ __forceinline__ int32_t row_state(const int32_t* __restrict__ states,
@@ -145,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void dense_mask_vec_kernel(
 // them, one whose columns are all allowed touches nothing, and only the
 // mixed ones read, blend and write (the result is the same; on a DFA that
 // allows a few percent of the vocab most logits are never read).
-template <int E>
+template <int E, int kBitRows>
 __global__ __launch_bounds__(kThreads) void dense_mask_bits_kernel(
     uint8_t* __restrict__ logits, int64_t ld_bytes, const uint8_t* __restrict__ bits,
     int64_t row_bytes, int64_t vocab, int32_t num_states, const int32_t* __restrict__ states,
@@ -544,19 +546,21 @@ extern "C" int bpd_dense_apply_mask_bits(void* logits, int dtype, int64_t rows, 
                        (reinterpret_cast<uintptr_t>(logits) % 16 == 0);
   if (aligned) {
     const int64_t col_slabs = (vocab + kSlab - 1) / kSlab;
-    const int64_t row_slabs = (rows + kBitRows - 1) / kBitRows;
+    const int R = rows >= kBitRowsLargeFrom ? kBitRowsLarge : kBitRowsSmall;
+    const int64_t row_slabs = (rows + R - 1) / R;
     int64_t blocks = col_slabs * row_slabs;
     blocks = (blocks + kXcds - 1) / kXcds * kXcds;
     BPD_REQUIRE(blocks < (int64_t(1) << 31), "batch too large for one launch");
     const uint8_t* b8 = reinterpret_cast<const uint8_t*>(allow_bits);
-    if (E == 2)
-      dense_mask_bits_kernel<2><<<dim3(unsigned(blocks)), dim3(kThreads), 0, s>>>(
-          static_cast<uint8_t*>(logits), ld_bytes, b8, words * 4, vocab, num_states, states, slots,
-          rows, uint32_t(row_slabs), uint32_t(col_slabs), fill, err);
-    else
-      dense_mask_bits_kernel<4><<<dim3(unsigned(blocks)), dim3(kThreads), 0, s>>>(
-          static_cast<uint8_t*>(logits), ld_bytes, b8, words * 4, vocab, num_states, states, slots,
-          rows, uint32_t(row_slabs), uint32_t(col_slabs), fill, err);
+#define BPD_MASK_BITS(EB, RB)                                                                     \
+  dense_mask_bits_kernel<EB, RB><<<dim3(unsigned(blocks)), dim3(kThreads), 0, s>>>(              \
+      static_cast<uint8_t*>(logits), ld_bytes, b8, words * 4, vocab, num_states, states, slots,  \
+      rows, uint32_t(row_slabs), uint32_t(col_slabs), fill, err)
+    if (E == 2 && R == kBitRowsSmall) BPD_MASK_BITS(2, kBitRowsSmall);
+    else if (E == 2) BPD_MASK_BITS(2, kBitRowsLarge);
+    else if (R == kBitRowsSmall) BPD_MASK_BITS(4, kBitRowsSmall);
+    else BPD_MASK_BITS(4, kBitRowsLarge);
+#undef BPD_MASK_BITS
   } else {
     BPD_REQUIRE(rows < 65536, "unaligned path supports at most 65535 rows");
     const int64_t gx = std::min<int64_t>((vocab + kThreads - 1) / kThreads, 1024);
