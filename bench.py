@@ -292,8 +292,8 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
             "traffic": _profiled_traffic("dense_mask_bits_email_b256_v151936.traffic.json",
-                                         "dense_mask_bits_kernel<2>"),
-            "kernel": "dense_mask_bits_kernel<2>",
+                                         "dense_mask_bits_kernel<2, 2>"),
+            "kernel": "dense_mask_bits_kernel<2, 2>",
             "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1),
             "table_charged_as": "int32 tok_next rows (the kernel reads the packed allow-bit table)",
         },
@@ -442,7 +442,7 @@ def bench_schema(args) -> int:
         "row_vocab_entries_per_s": round(B * V / (mean_ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "dense_mask_bits_kernel<2>",
+                     "kernel": "dense_mask_bits_kernel<2, 4>",
                      "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1)},
         "parity_dense_vs_walk_every_step": parity,
     }
