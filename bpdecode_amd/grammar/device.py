@@ -33,6 +33,24 @@ PDA_CONFIG_FLAT = PDA_CONFIG_WORDS
 _EPS, _BYTE, _CALL = 0, 1, 2
 
 
+def _walk_order(off: torch.Tensor, tb: torch.Tensor, vocab: int) -> torch.Tensor:
+    """Walk order of the memoised device mask: token ids by byte length, then
+    by their first 16 bytes.  Consecutive lanes of a wave take consecutive
+    positions, so they walk equally long tokens that share prefixes: they
+    reach the same table entries and leave the walk together."""
+    import numpy as np
+
+    o = off.cpu().numpy().astype(np.int64)
+    b = tb.cpu().numpy()
+    start, length = o[:vocab], o[1 : vocab + 1] - o[:vocab]
+    keys = []
+    for i in range(15, -1, -1):
+        idx = np.minimum(start + i, max(b.size - 1, 0))
+        keys.append(np.where(i < length, b[idx] if b.size else 0, 0).astype(np.int16))
+    keys.append(length)  # primary key last
+    return torch.from_numpy(np.lexsort(keys).astype(np.int32))
+
+
 @dataclass
 class PdaTensors:
     num_states: int
@@ -125,9 +143,7 @@ class PdaTensors:
             tb = self.tok_bytes.contiguous()
             if tb.numel() == 0:
                 tb = torch.zeros(1, dtype=torch.uint8, device=self.device)
-            # walk order of the memoised device mask: shortest tokens first
-            lengths = off[1:] - off[:-1]
-            order = torch.argsort(lengths, stable=True).to(torch.int32)
+            order = _walk_order(off, tb, self.vocab_size).to(off.device)
             t = _lib.TokenBytesC(self.vocab_size, self.eos_id, ptr(off), ptr(tb), ptr(order))
             self._c["tokens"] = t
             self._c["tokens_keep"] = (off, tb, order)

@@ -196,9 +196,10 @@ typedef struct BpdTokenBytes {
   int32_t eos_id;
   const int32_t* offsets; /* [vocab_size + 1] */
   const uint8_t* bytes;   /* [offsets[vocab_size]] */
-  /* optional (NULL = id order): a permutation of the token ids by byte
-   * length, shortest first; the memoised device mask walks tokens in this
-   * order (lanes of a wave then walk equally long tokens) */
+  /* optional (NULL = id order): a permutation of the token ids; the
+   * memoised device mask walks tokens in this order, consecutive lanes of a
+   * wave at consecutive positions (any permutation gives the same verdicts;
+   * by length, then bytes, lanes walk similar tokens) */
   const int32_t* order;
 } BpdTokenBytes;
 
