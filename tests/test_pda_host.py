@@ -16,7 +16,7 @@ from bpdecode_amd import synth
 from bpdecode_amd.grammar.constraint import CFGConstraint
 from bpdecode_amd.grammar.device import (
     PDA_CONFIG_FLAT, CFGConstraintBatch, build_pda_tensors, pda_advance_state, pda_apply_mask_,
-    pda_compute_mask, pda_mask_, pda_step,
+    _walk_order, pda_compute_mask, pda_mask_, pda_step,
 )
 from bpdecode_amd.grammar.gbnf import parse_gbnf
 from bpdecode_amd.grammar.pda import PDA, CompiledGrammar
@@ -238,3 +238,22 @@ def test_logits_processor_device_backend_matches_cpu_backend():
         assert lp_cpu.is_complete(0) == lp_dev.is_complete(0)
         toks = [rng.choice((~torch.isneginf(s_cpu[r])).nonzero().flatten().tolist()) for r in range(2)]
         input_ids = torch.cat([input_ids, torch.tensor(toks).unsqueeze(1)], dim=1)
+
+
+def test_memo_walk_order_is_a_permutation_by_length_then_bytes():
+    # tokens of every length class, duplicates, an empty token and tokens
+    # longer than the 16 bytes the order looks at
+    rng = random.Random(3)
+    toks = [b"", b"b", b"a", b"ab", b"ab", b"aa", b"x" * 20 + b"b", b"x" * 20 + b"a"]
+    toks += [bytes(rng.choice(b"ab\"[]{}") for _ in range(rng.randint(1, 24))) for _ in range(300)]
+    off = torch.tensor([0] + list(itertools.accumulate(len(t) for t in toks)), dtype=torch.int32)
+    tb = torch.tensor(list(b"".join(toks)), dtype=torch.uint8)
+    order = _walk_order(off, tb, len(toks))
+    assert order.dtype == torch.int32
+    o = order.tolist()
+    assert sorted(o) == list(range(len(toks)))
+    keys = [(len(toks[t]), toks[t][:16]) for t in o]
+    assert keys == sorted(keys)
+    # an empty byte table (every token empty) still orders every id
+    z = _walk_order(torch.zeros(4, dtype=torch.int32), torch.zeros(1, dtype=torch.uint8), 3)
+    assert sorted(z.tolist()) == [0, 1, 2]
