@@ -202,6 +202,54 @@ def test_json_long_token_rows(dev, monkeypatch):
         assert np.array_equal(got, want), mode
 
 
+def _masks_with_order(gd, pool, order):
+    """Packed masks of the memoised kernel with the token walk order given
+    explicitly (None: token id order)."""
+    from bpdecode_amd._lib import TokenBytesC, check, lib, ptr
+
+    B = pool.shape[0]
+    V = gd.vocab_size
+    need = int(lib().bpd_pda_workspace_bytes(B, V))
+    ws = torch.empty(need, dtype=torch.uint8, device=pool.device)
+    out = torch.empty((B, (V + 31) // 32), dtype=torch.int32, device=pool.device)
+    o = None if order is None else order.to(torch.int32).to(pool.device)
+    toks = TokenBytesC(V, gd.eos_id, ptr(gd.tok_offsets), ptr(gd.tok_bytes), ptr(o) if o is not None else None)
+    stream = torch.cuda.current_stream(pool.device).cuda_stream
+    check(lib().bpd_pda_compute_mask(gd.c_table(), toks, ptr(pool), None, B, ptr(out), ptr(ws), need, stream))
+    return out.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("which", ["full", "small"])
+def test_json_walk_orders_give_the_same_masks(dev, json_case, which):
+    """Any permutation of the walk order gives the oracle's masks: the default
+    order (by length, then bytes), token id order, a random permutation and
+    the default reversed; the small vocabulary has empty tokens and the EOS
+    token in the middle of the id range."""
+    if which == "full":
+        vocab, g, t = json_case
+        cfgs = _json_configs(g, 32, seed=83)
+    else:
+        raw = [bytes([i]) for i in range(256)] + [b"", b"\"a", b"</s>", b"", b"1, ", b"[{\"", b"true]"]
+        vocab = Vocabulary.from_tokens(raw, eos_id=258)
+        g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF)), vocab, eps_reduce=True)
+        t = OP.Table(g)
+        cfgs = _json_configs(g, 32, seed=84)
+    _log(f"case json walk orders {which} V={vocab.size} B=32")
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    want = OP.compute_mask(t, cfgs.numpy())
+    default = gd.c_tokens()  # builds the default order
+    from bpdecode_amd.grammar.device import _walk_order
+
+    base = _walk_order(gd.tok_offsets, gd.tok_bytes, gd.vocab_size)
+    perm = torch.from_numpy(np.random.default_rng(9).permutation(gd.vocab_size))
+    assert default is not None
+    assert np.array_equal(pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32), want)
+    for name, order in (("default", base), ("id", None), ("random", perm), ("reversed", base.flip(0))):
+        got = _masks_with_order(gd, pool, order)
+        assert np.array_equal(got, want), name
+
+
 def test_json_bench_batch_every_row(dev, json_case):
     """The benchmark's batch (256 rows, prefixes of 0-200 bytes at depths
     0-8, the same seed): every row's mask and committed config-set against
