@@ -894,12 +894,30 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     // record in registers: that loop has no memory wait other than the table
     // read, so queue stores still in flight do not stall it; the bytes after
     // them are read from tok_bytes in a second loop.
+    // Each loop takes only entries that are interned sets and stops at the
+    // first other one (missing, dead or overflow: entries >= kTOverflow);
+    // step() then settles that entry once, outside the loop, so the loop
+    // body has no branch besides its exit.  A special entry never advances
+    // the token, so the walk ends there (paused or rejected).
     auto walk = [&](int& cur, int& pos, int len, uint4 pk, int32_t t) -> bool {
       const int n16 = len < 16 ? len : 16;
-      while (cur < kWalkEnd && pos < n16)
-        if (!step(cur, pos, packed_byte(pk, pos))) return true;
-      while (cur < kWalkEnd && pos < len)
-        if (!step(cur, pos, int(a.tok_bytes[a.tok_off[t] + pos]))) return true;
+      while (cur < kWalkEnd && pos < n16) {
+        const uint8_t nx = T[cur * 256 + packed_byte(pk, pos)];
+        if (nx >= kTOverflow) break;
+        cur = nx;
+        ++pos;
+      }
+      if (cur < kWalkEnd && pos < n16 && !step(cur, pos, packed_byte(pk, pos))) return true;
+      if (cur < kWalkEnd && pos < len) {
+        const uint8_t* tb = a.tok_bytes + a.tok_off[t];
+        while (cur < kWalkEnd && pos < len) {
+          const uint8_t nx = T[cur * 256 + tb[pos]];
+          if (nx >= kTOverflow) break;
+          cur = nx;
+          ++pos;
+        }
+        if (cur < kWalkEnd && pos < len && !step(cur, pos, int(tb[pos]))) return true;
+      }
       if (cur < kWalkEnd) cur = kAllowed;
       return false;
     };
