@@ -1158,30 +1158,21 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     for (int w = tid; w < vwords && w < a.words; w += kMemoThreads) a.bits[b * a.words + w] = vbits[w];
     return;
   }
-  // logits: fill the rejected tokens, 8 columns per thread and step
+  // logits: one column per lane, 64 consecutive columns per wave and step;
+  // the rejected columns of a step get the fill value with one masked,
+  // coalesced store (no per-column loop, so rows with many mixed groups of
+  // allowed and rejected tokens cost no more than fully rejected ones)
   uint8_t* rowp = a.logits + b * a.ld_bytes;
-  const bool vec = (reinterpret_cast<uintptr_t>(rowp) & 15u) == 0 && (a.ld_bytes & 15) == 0;
-  for (int64_t c0 = int64_t(tid) * 8; c0 < V; c0 += int64_t(kMemoThreads) * 8) {
-    const uint32_t m = (vbits[c0 >> 5] >> (c0 & 31)) & 0xFFu;
-    if (m == 0xFFu) continue;
-    const int nc = V - c0 < 8 ? int(V - c0) : 8;
-    if (m == 0u && nc == 8 && vec) {
-      if (a.elem == 2) {
-        const uint32_t f2 = (a.fill & 0xFFFFu) | (a.fill << 16);
-        *reinterpret_cast<uint4*>(rowp + c0 * 2) = make_uint4(f2, f2, f2, f2);
-      } else {
-        *reinterpret_cast<uint4*>(rowp + c0 * 4) = make_uint4(a.fill, a.fill, a.fill, a.fill);
-        *reinterpret_cast<uint4*>(rowp + c0 * 4 + 16) = make_uint4(a.fill, a.fill, a.fill, a.fill);
-      }
-      continue;
-    }
-    for (int i = 0; i < nc; ++i) {
-      if ((m >> i) & 1u) continue;
-      uint8_t* p = rowp + (c0 + i) * a.elem;
+  const int lane = tid & (kWave - 1);
+  const uint16_t fill16 = uint16_t(a.fill & 0xFFFFu);
+  for (int64_t c0 = int64_t(tid - lane); c0 < V; c0 += kMemoThreads) {
+    const int64_t c = c0 + lane;
+    const bool rejected = c < V && ((vbits[c >> 5] >> (c & 31)) & 1u) == 0u;
+    if (rejected) {
       if (a.elem == 2)
-        *reinterpret_cast<uint16_t*>(p) = uint16_t(a.fill);
+        *reinterpret_cast<uint16_t*>(rowp + c * 2) = fill16;
       else
-        *reinterpret_cast<uint32_t*>(p) = a.fill;
+        *reinterpret_cast<uint32_t*>(rowp + c * 4) = a.fill;
     }
   }
 }
