@@ -1,30 +1,46 @@
 """Benchmark of the batched constraint step on one MI355X.
 
-Default workload (serving scale, dense tok_next): the email regex
-``[a-z0-9._]{1,32}@[a-z0-9-]{1,24}\\.(com|org|net|io)`` compiled to a byte DFA
-over a seeded synthetic vocabulary of V = 151,936 tokens; B = 256 rows;
-bf16 logits N(0, 3); continuous batching that evicts 10% of the rows and adds
-as many fresh ones every step; tokens sampled from the masked softmax.
+One JSON line.  The headline is the dense step at serving scale: the email
+regex ``[a-z0-9._]{1,32}@[a-z0-9-]{1,24}\\.(com|org|net|io)`` compiled to a
+byte DFA over a seeded synthetic vocabulary of V = 151,936 tokens; B = 256
+rows; bf16 logits N(0, 3); continuous batching that evicts 10 % of the rows
+and adds as many fresh ones every step; tokens sampled from the masked
+softmax.  One step = ``ConstraintBatch.apply_mask`` + ``ConstraintBatch.commit``.
+Nested objects carry the other workloads, each with its own roofline, CPU
+baseline and parity flag: ``pda`` (recursive-JSON config-set PDA, B = 256,
+fp32), ``soft`` (prior-weighted lookahead, k = 4, B = 128, fp32) and
+``schema`` (flat JSON-Schema document DFA, B = 512, bf16, from random valid
+partial documents of 0-80 bytes).
 
-One step = ``ConstraintBatch.apply_mask`` + ``ConstraintBatch.commit``.  Each
-step starts from cold caches: a 512 MB scratch buffer is read before it (no
-dirty lines left behind), so logits and table rows come from HBM.  The two
-calls are bracketed by HIP events on the stream they launch on, created with
-hipEventDisableSystemFence (torch's timing events add a system-scope release
-of several microseconds to each bracket); the slot list is staged and queued
-slot writes applied just before the first bracket, so each bracket holds one
-kernel.  Logits generation, the flush, sampling and churn sit outside the
-brackets.
+Timing.  Every step starts from cold caches: a 512 MB buffer is read before
+it (no dirty lines left behind), so logits and tables come from HBM.  HIP
+events created with hipEventDisableSystemFence are recorded on the stream the
+kernels run on.  The dense step runs its trajectory three times with the same
+logits, churn and tokens:
 
-Roofline (dominant kernel = the dense mask): algorithmic bytes per launch
-``D = B*V*2e + U*V*4`` (read + write of every logit, one int32 tok_next row per
-distinct live state U of that step), divided by the kernel's event-timed
-duration, against the 8 TB/s HBM3E peak.  The commit kernel adds 16 B per row.
+* record pass -- ``apply_mask`` and ``commit`` each in their own bracket, the
+  sampling between them (``mask_us``, ``commit_us``, ``two_bracket_us``);
+* kernel pass (``value``) -- the slot list and queued churn writes staged by
+  ``ConstraintBatch.prepare`` before the bracket, then ``apply_mask`` and
+  ``commit`` (with the token recorded for that step) in ONE bracket: the work
+  of the constraint step and nothing else, without a second bracket's fixed
+  cost (an empty kernel between two events measures 6.2 us against 3.8 us in
+  the kernel trace);
+* API pass -- the same single bracket with the slot/churn upload inside it
+  (``api_us_per_step``), plus the host time of the two Python calls.
 
-CPU baseline: the oracle's numpy restatement of the reference dense path
-timed on the host over a bounded replay of the first recorded steps.
+The passes must agree: the kernel and API passes commit the same states as
+the record pass, step by step.
 
-Prints one JSON line.  ``--gpus N`` with N > 1 is refused: this build
+Roofline (HBM, 8 TB/s peak).  Dense step: ``D = B*V*2e + U*V*4 + 16*B`` (read
+and write of every logit, one int32 tok_next row per distinct live state U of
+the step, commit state/token/lookup/write), divided by the step time; the
+mask kernel's own fraction (``D - 16*B`` over the record pass's mask bracket)
+is reported beside it.  PDA: ``B*V*8 + B*1064*2 + sum(token bytes)``
+(diagnostic; the walk is not bandwidth-bound).  Soft: ``B*V*4*2 + S*V*4``.
+
+CPU baselines run on the host cores of the same box over bounded samples
+(stated in each ``sample``).  ``--gpus N`` with N > 1 is refused: this build
 measures one GPU.
 """
 
@@ -43,12 +59,13 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+METRIC = "µs/step apply_mask+commit & GB/s (% HBM roofline), B=256 V=151936 bf16"
 
 
 class HipEvents:
     """HIP events created with hipEventDisableSystemFence, recorded on a given
     stream: the bracket then holds no system-scope cache release, so it times
-    the kernel between the markers (torch's timing events carry one)."""
+    the kernels between the markers (torch's timing events carry one)."""
 
     def __init__(self, n: int) -> None:
         import ctypes
@@ -76,6 +93,11 @@ class HipEvents:
             raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
         return ms.value
 
+    def destroy(self) -> None:
+        for h in self.ev:
+            self.hip.hipEventDestroy(h)
+        self.ev = []
+
 
 def _cpu_model() -> str:
     """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
@@ -100,27 +122,34 @@ def _profiled_traffic(name: str, kernel: str):
     return rec.get("traffic_bytes") if rec.get("kernel") == kernel else None
 
 
+def _roofline(d_bytes: float, seconds: float, **extra) -> dict:
+    gbs = d_bytes / seconds / 1e9
+    out = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+           "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    out.update(extra)
+    return out
+
+
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=128)
+    p.add_argument("--steps", type=int, default=128, help="timed steps of the dense headline")
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--batch", type=int, default=256)
     p.add_argument("--vocab", type=int, default=151_936)
     p.add_argument("--churn", type=float, default=0.10)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--cpu-steps", type=int, default=8, help="recorded steps replayed on the CPU")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    p.add_argument("--cpu-steps", type=int, default=8, help="recorded dense steps replayed on the CPU")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
-    p.add_argument("--workload", choices=["dense", "pda", "soft", "schema"], default="dense",
-                   help="dense: email-regex tok_next step (the headline); pda: recursive-JSON PDA step; "
-                        "soft: prior-weighted lookahead; schema: flat JSON-Schema DFA at B=512, dense "
-                        "table and walking kernel side by side")
+    p.add_argument("--workload", choices=["all", "dense", "pda", "soft", "schema"], default="all",
+                   help="all (default): the dense headline with pda, soft and schema nested; or one "
+                        "workload alone")
     p.add_argument("--schema-rows", type=int, default=512)
     p.add_argument("--schema-steps", type=int, default=64)
     p.add_argument("--pda-rows", type=int, default=256)
     p.add_argument("--pda-steps", type=int, default=64)
-    p.add_argument("--pda-cpu-rows", type=int, default=4, help="rows of one step replayed on the CPU oracle")
+    p.add_argument("--pda-cpu-rows", type=int, default=4, help="rows of one step replayed on the CPU")
     p.add_argument("--soft-rows", type=int, default=128)
     p.add_argument("--soft-k", type=int, default=4)
     p.add_argument("--soft-steps", type=int, default=64)
@@ -153,116 +182,197 @@ def main(argv=None) -> int:
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return 0
-    if args.workload == "pda":
-        return bench_pda(args)
-    if args.workload == "soft":
-        return bench_soft(args)
-    if args.workload == "schema":
-        return bench_schema(args)
+    import torch
 
+    torch.cuda.set_device(0)
+    if args.workload == "pda":
+        out = bench_pda(args)
+    elif args.workload == "soft":
+        out = bench_soft(args)
+    elif args.workload == "schema":
+        out = bench_schema(args)
+    else:
+        out = bench_dense(args)
+        if args.workload == "all":
+            for name, fn in (("pda", bench_pda), ("soft", bench_soft), ("schema", bench_schema)):
+                print(f"[bench] {name}", file=sys.stderr, flush=True)
+                out[name] = fn(args)
+    print(json.dumps(out))
+    return 0
+
+
+# ------------------------------------------------------------------ dense --
+class DenseRun:
+    """One pass over a dense trajectory: a fresh batch at the same starting
+    rows, the same logits (seeded device generator), the same churn (seeded
+    host generator) and -- after the record pass -- the same tokens."""
+
+    def __init__(self, fsa, B: int, V: int, dtype, churn: float, starts, seed: int) -> None:
+        import numpy as np
+        import torch
+
+        from bpdecode_amd.batch import ConstraintBatch
+
+        self.B, self.V, self.dtype, self.churn = B, V, dtype, churn
+        self.dev = fsa.device
+        self.batch = ConstraintBatch(fsa, capacity=2 * B, device=self.dev)
+        self.active = []
+        for i in range(B):
+            self.batch.add(i)
+            self.active.append(i)
+        self.next_id = B
+        if starts is not None:
+            self.batch._state[:B] = starts.to(self.dev)
+        self.rng = np.random.default_rng(seed)
+        self.gen = torch.Generator(device=self.dev)
+        self.gen.manual_seed(seed + 1)
+        self.logits = torch.empty((B, V), dtype=dtype, device=self.dev)
+
+    def next_logits(self) -> None:
+        import torch
+
+        self.logits.copy_(torch.randn((self.B, self.V), generator=self.gen, device=self.dev).mul_(3.0))
+
+    def states_now(self, ids):
+        """The rows' states as the next launch will read them (pool plus
+        queued writes), on the host; outside the timed region."""
+        import numpy as np
+
+        b = self.batch
+        pool = b._pool.cpu().numpy()
+        for q in (b._staged_pending, b._pending):
+            for slot, v in q.items():
+                pool[slot] = v
+        return pool[np.array([b._slot_of[i] for i in ids], dtype=np.int64)]
+
+    def churn_step(self) -> None:
+        n = int(round(self.churn * self.B))
+        for i in self.rng.choice(len(self.active), size=n, replace=False).tolist():
+            self.batch.evict(self.active[i])
+            self.active[i] = self.next_id
+            self.batch.add(self.next_id)
+            self.next_id += 1
+
+
+def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup, record_cpu=0):
+    """The three passes of the dense step over one trajectory.  Returns the
+    timings (ms lists over the timed steps), the distinct live states per
+    timed step, the host API times, the parity of the passes and the steps
+    recorded for the CPU baseline."""
+    import numpy as np
+    import torch
+
+    n_total = warmup + steps
+    flush64 = None
+    if not args.no_flush:
+        flush64 = torch.zeros(512 << 20, dtype=torch.uint8, device=fsa.device).view(torch.int64)
+    sh = torch.cuda.current_stream(fsa.device).cuda_stream
+    tokens, distinct, recorded, nxt_ref = [], [], [], []
+
+    # record pass: two brackets, sampling between them
+    run = DenseRun(fsa, B, V, dtype, churn, starts, seed)
+    sgen = torch.Generator(device=fsa.device)
+    sgen.manual_seed(seed + 2)
+    ev = HipEvents(4 * n_total)
+    for k in range(n_total):
+        ids = list(run.active)
+        run.next_logits()
+        st = run.states_now(ids)
+        live = st[st >= 0]
+        distinct.append(int(np.unique(live).size))
+        keep = k >= warmup and len(recorded) < record_cpu
+        if keep:
+            raw = run.logits.cpu()
+        run.batch.prepare(ids)
+        if flush64 is not None:
+            flush64.sum()
+        ev.record(4 * k, sh)
+        run.batch.apply_mask(ids, run.logits)
+        ev.record(4 * k + 1, sh)
+        toks = torch.multinomial(torch.softmax(run.logits.float(), dim=-1), 1, generator=sgen).view(-1)
+        ev.record(4 * k + 2, sh)
+        nxt = run.batch.commit(ids, toks)
+        ev.record(4 * k + 3, sh)
+        tokens.append(toks)
+        nxt_ref.append(nxt)
+        if keep:
+            recorded.append((raw, st.copy(), toks.cpu().numpy(), run.logits.cpu()))
+        run.churn_step()
+    torch.cuda.synchronize()
+    timed = range(warmup, n_total)
+    mask_ms = [ev.elapsed_ms(4 * k, 4 * k + 1) for k in timed]
+    commit_ms = [ev.elapsed_ms(4 * k + 2, 4 * k + 3) for k in timed]
+    ev.destroy()
+    pool_ref = run.batch._state.cpu()
+
+    # kernel pass (staged upload) and API pass (upload inside the bracket)
+    res = {"mask_ms": mask_ms, "commit_ms": commit_ms}
+    parity = True
+    for mode in ("kernel", "api"):
+        run = DenseRun(fsa, B, V, dtype, churn, starts, seed)
+        ev = HipEvents(2 * n_total)
+        host_s = []
+        agree = torch.ones((), dtype=torch.bool, device=fsa.device)
+        for k in range(n_total):
+            ids = list(run.active)
+            run.next_logits()
+            if mode == "kernel":
+                run.batch.prepare(ids)
+            if flush64 is not None:
+                flush64.sum()
+            h0 = time.perf_counter()
+            ev.record(2 * k, sh)
+            run.batch.apply_mask(ids, run.logits)
+            nxt = run.batch.commit(ids, tokens[k])
+            ev.record(2 * k + 1, sh)
+            host_s.append(time.perf_counter() - h0)
+            agree &= (nxt == nxt_ref[k]).all()
+            run.churn_step()
+        torch.cuda.synchronize()
+        res[f"{mode}_ms"] = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in timed]
+        res[f"{mode}_host_s"] = host_s[warmup:]
+        ev.destroy()
+        parity &= bool(agree.item()) and torch.equal(run.batch._state.cpu(), pool_ref)
+    res["distinct"] = distinct[warmup:]
+    res["passes_agree"] = parity
+    res["recorded"] = recorded
+    return res
+
+
+def bench_dense(args) -> dict:
     import numpy as np
     import torch
 
     from bpdecode_amd import synth
-    from bpdecode_amd.batch import ConstraintBatch
     from bpdecode_amd.ops import FsaTensors
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     B, V = args.batch, args.vocab
     t0 = time.perf_counter()
     vocab = synth.serving_vocab(V, seed=1)
     fsa = FsaTensors.build(synth.EMAIL, vocab, dense=False).to(dev).densify()
+    fsa.ensure_allow_bits()
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t0
-    S = fsa.num_states
-    e = 2  # bf16
-
-    batch = ConstraintBatch(fsa, capacity=2 * B, device=dev)
-    rng = np.random.default_rng(2)
-    next_id = 0
-    active: list[int] = []
-    for _ in range(B):
-        batch.add(next_id)
-        active.append(next_id)
-        next_id += 1
-
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(3)
-    logits = torch.empty((B, V), dtype=torch.bfloat16, device=dev)
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-    flush.zero_()
-    flush64 = flush.view(torch.int64)
-    stream = torch.cuda.current_stream(dev)
-
-    n_total = args.warmup + args.steps
-    kev = HipEvents(4 * n_total)
-    sh = stream.cuda_stream
-    distinct: list[int] = []
-    host_api_s: list[float] = []
-    recorded = []  # (logits bits, states, tokens, masked bits) of the first timed steps
+    S, e = fsa.num_states, 2
     n_cpu = 0 if args.no_cpu else min(args.cpu_steps, args.steps)
-
-    torch.cuda.synchronize()
-    wall0 = None
-    for k in range(n_total):
-        if k == args.warmup:
-            torch.cuda.synchronize()
-            wall0 = time.perf_counter()
-        ids = list(active)
-        logits.copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
-        slots = batch._slots(ids)
-        pool = batch._state  # applies queued slot writes before the timed region
-        states_now = pool[slots].cpu().numpy()
-        live = states_now[states_now >= 0]
-        distinct.append(int(np.unique(live).size))
-        keep = k >= args.warmup and len(recorded) < n_cpu
-        if keep:
-            rec_logits = logits.cpu()
-        if not args.no_flush:
-            flush64.sum()
-        h0 = time.perf_counter()
-        kev.record(4 * k, sh)
-        batch.apply_mask(ids, logits)
-        kev.record(4 * k + 1, sh)
-        h1 = time.perf_counter()
-        probs = torch.softmax(logits.float(), dim=-1)
-        toks = torch.multinomial(probs, 1, generator=gen).view(-1)
-        h2 = time.perf_counter()
-        kev.record(4 * k + 2, sh)
-        batch.commit(ids, toks)
-        kev.record(4 * k + 3, sh)
-        h3 = time.perf_counter()
-        host_api_s.append((h1 - h0) + (h3 - h2))
-        if keep:
-            recorded.append((rec_logits, states_now.copy(), toks.cpu().numpy(), logits.cpu()))
-        # continuous batching: evict 10% of the rows, add as many fresh ones
-        n_churn = int(round(args.churn * B))
-        for i in rng.choice(len(active), size=n_churn, replace=False).tolist():
-            batch.evict(active[i])
-            active[i] = next_id
-            batch.add(next_id)
-            next_id += 1
-    torch.cuda.synchronize()
-    wall1 = time.perf_counter()
-
-    timed = range(args.warmup, n_total)
-    mask_ms = [kev.elapsed_ms(4 * k, 4 * k + 1) for k in timed]
-    commit_ms = [kev.elapsed_ms(4 * k + 2, 4 * k + 3) for k in timed]
-    step_ms = [a + b for a, b in zip(mask_ms, commit_ms)]
-    U = distinct[args.warmup:]
-    d_bytes = [B * V * 2 * e + u * V * 4 for u in U]
-    achieved_gbs = sum(d_bytes) / (sum(mask_ms) * 1e-3) / 1e9
-    mean_step_ms = statistics.fmean(step_ms)
-
+    r = _dense_trajectory(args, fsa, B, V, torch.bfloat16, args.churn, None, 2, args.steps,
+                          args.warmup, record_cpu=n_cpu)
+    U = r["distinct"]
+    d_step = [B * V * 2 * e + u * V * 4 + 16 * B for u in U]
+    d_mask = [B * V * 2 * e + u * V * 4 for u in U]
+    t_step = statistics.fmean(r["kernel_ms"])
+    t_mask = statistics.fmean(r["mask_ms"])
+    two = [a + b for a, b in zip(r["mask_ms"], r["commit_ms"])]
+    traffic = _profiled_traffic("dense_fill_email_b256_v151936.traffic.json", "dense_fill_kernel<2, true>")
     out = {
-        "metric": "µs/step apply_mask+commit & GB/s (% HBM roofline), B=256 V=151936 bf16",
-        "value": round(mean_step_ms * 1e3, 3),
+        "metric": METRIC,
+        "value": round(t_step * 1e3, 3),
         "unit": "us/step",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(mean_step_ms, 5),
+        "ms_per_step": round(t_step, 5),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -276,83 +386,92 @@ def main(argv=None) -> int:
             "logits": "bf16 N(0,3)",
             "cache_flush": "512 MB read before each step" if not args.no_flush else "none",
         },
-        "median_us_per_step": round(statistics.median(step_ms) * 1e3, 3),
-        "mask_us": round(statistics.fmean(mask_ms) * 1e3, 3),
-        "commit_us": round(statistics.fmean(commit_ms) * 1e3, 3),
-        "timing": "fence-free HIP events around ConstraintBatch.apply_mask and .commit on their stream",
-        "row_vocab_entries_per_s": round(B * V / (mean_step_ms * 1e-3), 1),
+        "median_us_per_step": round(statistics.median(r["kernel_ms"]) * 1e3, 3),
+        "timing": ("fence-free HIP events on the kernels' stream, one bracket per step around "
+                   "ConstraintBatch.apply_mask + .commit (slot upload staged by prepare(); tokens "
+                   "recorded from the masked softmax in the record pass)"),
+        "mask_us": round(t_mask * 1e3, 3),
+        "commit_us": round(statistics.fmean(r["commit_ms"]) * 1e3, 3),
+        "two_bracket_us": round(statistics.fmean(two) * 1e3, 3),
+        "api_us_per_step": round(statistics.fmean(r["api_ms"]) * 1e3, 3),
+        "api_host_us_per_step": round(statistics.fmean(r["api_host_s"]) * 1e6, 2),
+        "row_vocab_entries_per_s": round(B * V / (t_step * 1e-3), 1),
         "distinct_live_states_mean": round(statistics.fmean(U), 2),
-        "api_host_us_per_step": round(statistics.fmean(host_api_s[args.warmup:]) * 1e6, 2),
-        "wall_ms_per_step_incl_setup_work": round((wall1 - wall0) * 1e3 / args.steps, 4),
         "setup_s": round(setup_s, 3),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved_gbs, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved_gbs / PEAK_HBM_GBS, 4),
-            "traffic": _profiled_traffic("dense_mask_bits_email_b256_v151936.traffic.json",
-                                         "dense_mask_bits_kernel<2, 2>"),
-            "kernel": "dense_mask_bits_kernel<2, 2>",
-            "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1),
-            "table_charged_as": "int32 tok_next rows (the kernel reads the packed allow-bit table)",
-        },
+        "passes_agree": r["passes_agree"],
+        "roofline": _roofline(
+            sum(d_step) / len(d_step), t_step * 1e-3,
+            traffic=traffic,
+            scope="apply_mask + commit step (one event bracket)",
+            algorithmic_bytes_per_step_mean=round(statistics.fmean(d_step), 1),
+            table_charged_as="int32 tok_next rows (the kernel reads the packed allow-bit table)",
+            kernel="dense_fill_kernel<2, true>",
+            mask_kernel=_roofline(sum(d_mask) / len(d_mask), t_mask * 1e-3,
+                                  scope="mask launch alone (record pass bracket)",
+                                  duration_us=round(t_mask * 1e3, 3)),
+            two_bracket_frac=round(statistics.fmean(d_step) / (statistics.fmean(two) * 1e-3) / 1e9
+                                   / PEAK_HBM_GBS, 4),
+        ),
     }
-
-    if n_cpu:
-        from oracle import dense as OD
-
-        # the reference's CPU step is ATen: ops.py:271-276 (mask) and
-        # ops.py:301-306 (commit), timed here op for op on CPU tensors with
-        # torch's host threads (OMP_NUM_THREADS); the numpy oracle checks the
-        # GPU's masks as well
-        tn_host = fsa.tok_next.cpu()
-        tn_np = tn_host.numpy()
-        fill = OD.fill_bits(torch.bfloat16, float("-inf"))
-        parity = True
-        times = []
-        for _ in range(args.cpu_repeats):
-            for lg, st, tk, masked in recorded:
-                x = lg.clone()
-                st_t = torch.from_numpy(st.astype(np.int32))
-                tk_t = torch.from_numpy(np.asarray(tk))
-                c0 = time.perf_counter()
-                s_ = st_t.long()
-                broken = s_ < 0
-                rejected = tn_host.index_select(0, s_.clamp_(min=0)) == -1
-                rejected |= broken.unsqueeze(1)
-                x.masked_fill_(rejected, float("-inf"))
-                s2 = st_t.long()
-                nxt = tn_host[s2.clamp_(min=0), tk_t.long()]
-                nxt = torch.where(s2 < 0, torch.full_like(nxt, -1), nxt).to(torch.int32)
-                times.append(time.perf_counter() - c0)
-                parity &= bool(torch.equal(x.view(torch.int16), masked.view(torch.int16)))
-                bits = lg.view(torch.int16).numpy().view(np.uint16).copy()
-                OD.apply_mask_bits(bits, tn_np, st, fill)
-                parity &= bool(np.array_equal(bits, masked.view(torch.int16).numpy().view(np.uint16)))
-        out["cpu_baseline"] = {
-            "value": round(statistics.fmean(times) * 1e6, 1),
-            "unit": "us/step",
-            "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{len(recorded)} recorded steps of the same workload (B={B}, V={V}, bf16), "
-                      f"replayed {args.cpu_repeats}x through the reference's ATen op sequence "
-                      f"(ops.py:271-276 mask, ops.py:301-306 commit) on CPU tensors",
-            "host_cpus": os.cpu_count(),
-            "host_cpu_model": _cpu_model(),
-        }
-        out["parity_vs_oracle"] = parity
-    print(json.dumps(out))
-    return 0
+    if r["recorded"]:
+        out["cpu_baseline"], out["parity_vs_oracle"] = _dense_cpu_baseline(args, fsa, r["recorded"], B, V)
+    return out
 
 
-def bench_schema(args) -> int:
-    """Flat JSON-Schema document DFA (826 states) over the serving vocab,
-    B rows at random reachable states, bf16 logits N(0, 3), no churn.  Each
-    step masks and commits twice on identical inputs: through the dense
-    allow-bit table (the timed headline of this workload) and through the
-    symbol-class walking kernel (no [states, vocab] table); the two results
-    are compared bit for bit every step."""
+def _dense_cpu_baseline(args, fsa, recorded, B, V):
+    """The reference's CPU step is ATen: ops.py:271-276 (mask) and
+    ops.py:301-306 (commit), timed here op for op on CPU tensors with torch's
+    host threads; the numpy oracle checks the GPU's masks of the same steps."""
+    import numpy as np
+    import torch
+
+    from oracle import dense as OD
+
+    tn_host = fsa.tok_next.cpu()
+    tn_np = tn_host.numpy()
+    fill = OD.fill_bits(torch.bfloat16, float("-inf"))
+    parity = True
+    times = []
+    for _ in range(args.cpu_repeats):
+        for lg, st, tk, masked in recorded:
+            x = lg.clone()
+            st_t = torch.from_numpy(st.astype(np.int32))
+            tk_t = torch.from_numpy(np.asarray(tk))
+            c0 = time.perf_counter()
+            s_ = st_t.long()
+            broken = s_ < 0
+            rejected = tn_host.index_select(0, s_.clamp_(min=0)) == -1
+            rejected |= broken.unsqueeze(1)
+            x.masked_fill_(rejected, float("-inf"))
+            s2 = st_t.long()
+            nxt = tn_host[s2.clamp_(min=0), tk_t.long()]
+            nxt = torch.where(s2 < 0, torch.full_like(nxt, -1), nxt).to(torch.int32)
+            times.append(time.perf_counter() - c0)
+            parity &= bool(torch.equal(x.view(torch.int16), masked.view(torch.int16)))
+            bits = lg.view(torch.int16).numpy().view(np.uint16).copy()
+            OD.apply_mask_bits(bits, tn_np, st, fill)
+            parity &= bool(np.array_equal(bits, masked.view(torch.int16).numpy().view(np.uint16)))
+    base = {
+        "value": round(statistics.fmean(times) * 1e6, 1),
+        "unit": "us/step",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{len(recorded)} recorded steps of the same workload (B={B}, V={V}, bf16), "
+                  f"replayed {args.cpu_repeats}x through the reference's ATen op sequence "
+                  f"(ops.py:271-276 mask, ops.py:301-306 commit) on CPU tensors",
+        "host_cpus": os.cpu_count(),
+        "host_cpu_model": _cpu_model(),
+    }
+    return base, parity
+
+
+# ----------------------------------------------------------------- schema --
+def bench_schema(args) -> dict:
+    """Flat JSON-Schema document DFA (826 states, forced dense) over the
+    serving vocab, B rows from random valid partial documents of 0-80 bytes,
+    bf16 logits N(0, 3), no churn, the dense step as in the headline; plus
+    the symbol-class walking kernel (no [states, vocab] table) on the same
+    inputs, compared bit for bit."""
     import numpy as np
     import torch
 
@@ -364,93 +483,81 @@ def bench_schema(args) -> int:
     from bpdecode_amd.ops import FsaTensors
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     B, V = args.schema_rows, args.vocab
+    steps = min(args.schema_steps, args.steps)
     vocab = synth.serving_vocab(V, seed=1)
     comp = CompiledGrammar.build(json_schema_to_grammar(synth.FLAT_SCHEMA))
     dfa = residual_dfa(comp, comp.root, comp.rules[comp.root].start)
     plain = FsaTensors.build(dfa, vocab, dense=False).to(dev)
     dense = plain.densify()
     dense.ensure_allow_bits()
-    S = plain.num_states
-    starts = synth.random_walk_states(dense.tok_next.cpu(), plain.start, vocab.eos_id, B, 12, seed=4)
-    batches = [ConstraintBatch(dense, capacity=B, device=dev), ConstraintBatch(plain, capacity=B, device=dev)]
-    for bt in batches:
+    starts = synth.random_byte_walk_states(dense.tok_next, plain.start, B, 80, seed=4)
+    r = _dense_trajectory(args, dense, B, V, torch.bfloat16, 0.0, starts, 6, steps, args.warmup)
+    U = r["distinct"]
+    d_step = [B * V * 2 * 2 + u * V * 4 + 16 * B for u in U]
+    t_step = statistics.fmean(r["kernel_ms"])
+
+    # the walking kernel on the same logits and tokens, compared every step
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    walk = ConstraintBatch(plain, capacity=B, device=dev)
+    ref = ConstraintBatch(dense, capacity=B, device=dev)
+    for bt in (walk, ref):
         for i in range(B):
             bt.add(i)
         bt._state[:B] = starts.to(dev)
-    ids = list(range(B))
     gen = torch.Generator(device=dev)
-    gen.manual_seed(5)
-    logits = [torch.empty((B, V), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    gen.manual_seed(9)
+    ids = list(range(B))
+    n_total = args.warmup + steps
+    ev = HipEvents(2 * n_total)
     flush64 = torch.zeros(512 << 20, dtype=torch.uint8, device=dev).view(torch.int64)
-    sh = torch.cuda.current_stream(dev).cuda_stream
-    n_total = args.warmup + args.schema_steps
-    kev = HipEvents(8 * n_total)
-    distinct, parity = [], True
+    lw = torch.empty((B, V), dtype=torch.bfloat16, device=dev)
+    ld = torch.empty_like(lw)
+    agree = True
     for k in range(n_total):
-        logits[0].copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
-        logits[1].copy_(logits[0])
-        st = batches[0]._state[:B]
-        distinct.append(int(torch.unique(st[st >= 0]).numel()))
-        toks = None
-        for p, bt in enumerate(batches):
-            bt._slots(ids)
-            bt._state  # queued slot writes land before the timed region
-            if not args.no_flush:
-                flush64.sum()
-            kev.record(8 * k + 4 * p, sh)
-            bt.apply_mask(ids, logits[p])
-            kev.record(8 * k + 4 * p + 1, sh)
-            if toks is None:
-                toks = torch.multinomial(torch.softmax(logits[p].float(), dim=-1), 1, generator=gen).view(-1)
-            kev.record(8 * k + 4 * p + 2, sh)
-            bt.commit(ids, toks)
-            kev.record(8 * k + 4 * p + 3, sh)
-        parity &= bool(torch.equal(logits[0].view(torch.int16), logits[1].view(torch.int16)))
-        parity &= bool(torch.equal(batches[0]._state[:B], batches[1]._state[:B]))
+        lw.copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
+        ld.copy_(lw)
+        ref.apply_mask(ids, ld)
+        toks = torch.multinomial(torch.softmax(ld.float(), dim=-1), 1, generator=gen).view(-1)
+        n_ref = ref.commit(ids, toks)
+        walk.prepare(ids)
+        if not args.no_flush:
+            flush64.sum()
+        ev.record(2 * k, sh)
+        walk.apply_mask(ids, lw)
+        n_walk = walk.commit(ids, toks)
+        ev.record(2 * k + 1, sh)
+        agree &= bool(torch.equal(lw.view(torch.int16), ld.view(torch.int16))) and bool(torch.equal(n_ref, n_walk))
     torch.cuda.synchronize()
-    timed = range(args.warmup, n_total)
-    ms = {name: [kev.elapsed_ms(8 * k + a, 8 * k + a + 1) for k in timed]
-          for name, a in (("mask", 0), ("commit", 2), ("walk_mask", 4), ("walk_commit", 6))}
-    step_ms = [a + b for a, b in zip(ms["mask"], ms["commit"])]
-    U = distinct[args.warmup:]
-    d_bytes = [B * V * 2 * 2 + u * V * 4 for u in U]
-    achieved = sum(d_bytes) / (sum(ms["mask"]) * 1e-3) / 1e9
-    mean_ms = statistics.fmean(step_ms)
-    out = {
+    walk_ms = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in range(args.warmup, n_total)]
+    ev.destroy()
+    return {
         "metric": "µs/step apply_mask+commit, flat JSON-Schema DFA, B=512 V=151936 bf16",
-        "value": round(mean_ms * 1e3, 3),
+        "value": round(t_step * 1e3, 3),
         "unit": "us/step",
-        "n_gpus": 1,
-        "steps": args.schema_steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(mean_ms, 5),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "steps": steps,
         "dtype": "bf16",
-        "data": "synthetic",
-        "config": {"workload": "dense tok_next apply_mask+commit, flat JSON-Schema document DFA",
-                   "batch_rows": B, "vocab": V, "dfa_states": S, "symbol_classes": plain.num_symbols,
-                   "logits": "bf16 N(0,3)", "cache_flush": "512 MB read before each mask and commit pair"},
-        "mask_us": round(statistics.fmean(ms["mask"]) * 1e3, 3),
-        "commit_us": round(statistics.fmean(ms["commit"]) * 1e3, 3),
-        "walk_mask_us": round(statistics.fmean(ms["walk_mask"]) * 1e3, 3),
-        "walk_commit_us": round(statistics.fmean(ms["walk_commit"]) * 1e3, 3),
+        "config": {"workload": "dense tok_next apply_mask+commit, flat JSON-Schema document DFA, "
+                               "starting rows = random valid partial documents of 0-80 bytes",
+                   "batch_rows": B, "vocab": V, "dfa_states": plain.num_states,
+                   "symbol_classes": plain.num_symbols, "logits": "bf16 N(0,3)"},
+        "mask_us": round(statistics.fmean(r["mask_ms"]) * 1e3, 3),
+        "commit_us": round(statistics.fmean(r["commit_ms"]) * 1e3, 3),
+        "api_us_per_step": round(statistics.fmean(r["api_ms"]) * 1e3, 3),
+        "walking_kernel_us_per_step": round(statistics.fmean(walk_ms) * 1e3, 3),
         "distinct_live_states_mean": round(statistics.fmean(U), 2),
-        "row_vocab_entries_per_s": round(B * V / (mean_ms * 1e-3), 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "dense_mask_bits_kernel<2, 4>",
-                     "algorithmic_bytes_per_launch_mean": round(statistics.fmean(d_bytes), 1)},
-        "parity_dense_vs_walk_every_step": parity,
+        "row_vocab_entries_per_s": round(B * V / (t_step * 1e-3), 1),
+        "roofline": _roofline(statistics.fmean(d_step), t_step * 1e-3, traffic=None,
+                              scope="apply_mask + commit step (one event bracket)",
+                              algorithmic_bytes_per_step_mean=round(statistics.fmean(d_step), 1),
+                              kernel="dense_fill_kernel<2, true>"),
+        "passes_agree": r["passes_agree"],
+        "parity_dense_vs_walking_kernel_every_step": agree,
     }
-    print(json.dumps(out))
-    return 0
 
 
-def bench_pda(args) -> int:
+# -------------------------------------------------------------------- pda --
+def bench_pda(args) -> dict:
     """Recursive-JSON PDA step: B rows seeded with valid JSON prefixes of
     0-200 bytes (nesting depth uniform over 0-8) over the V = 151,936
     synthetic vocabulary, fp32 logits N(0, 3), mask + commit per step with the
@@ -464,40 +571,32 @@ def bench_pda(args) -> int:
     from bpdecode_amd.grammar.pda import CompiledGrammar
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     B, V = args.pda_rows, args.vocab
+    steps = min(args.pda_steps, args.steps)
     vocab = synth.serving_vocab(V, seed=1)
     comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
     g = build_pda_tensors(comp, vocab, eps_reduce=True)
     rng = np.random.default_rng(5)
     rows = []
-    depths = []
     while len(rows) < B:
         d = int(rng.integers(0, 9))
         c = g.init_config()
         if g.feed(c, synth.json_prefix(rng, d)):
             rows.append(c)
-            depths.append(d)
     start = torch.stack(rows)
     batch = CFGConstraintBatch(g, capacity=B, device=dev)
     ids = list(range(B))
     for i in ids:
         batch.add(i)
     batch._configs.copy_(start.to(dev))
-    stream = torch.cuda.current_stream(dev)
-    sh = stream.cuda_stream
-    n_total = args.warmup + args.pda_steps
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    n_total = args.warmup + steps
     kev = HipEvents(4 * n_total)
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     logits = torch.empty((B, V), dtype=torch.float32, device=dev)
     first = None
-    torch.cuda.synchronize()
-    wall0 = None
     for k in range(n_total):
-        if k == args.warmup:
-            torch.cuda.synchronize()
-            wall0 = time.perf_counter()
         logits.copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
         batch._slots(ids)
         if k == args.warmup:
@@ -509,36 +608,34 @@ def bench_pda(args) -> int:
             first = first + (logits.cpu(),)
         toks = torch.multinomial(torch.softmax(logits, dim=-1), 1, generator=gen).view(-1)
         kev.record(4 * k + 2, sh)
-        status = batch.commit(ids, toks)
+        batch.commit(ids, toks)
         kev.record(4 * k + 3, sh)
     torch.cuda.synchronize()
-    wall1 = time.perf_counter()
     timed = range(args.warmup, n_total)
     mask_ms = [kev.elapsed_ms(4 * k, 4 * k + 1) for k in timed]
     commit_ms = [kev.elapsed_ms(4 * k + 2, 4 * k + 3) for k in timed]
+    kev.destroy()
     step_ms = statistics.fmean([a + b for a, b in zip(mask_ms, commit_ms)])
-    broken = int(batch._broken.sum())
-    sat = int((batch._configs[:, 1] != 0).sum())
+    tok_bytes = int(g.tok_bytes.numel())
+    d_bytes = B * V * 8 + B * 1064 * 2 + tok_bytes
     out = {
         "metric": "µs/step PDA apply_mask+commit, recursive-JSON grammar, B=256 V=151936 fp32",
         "value": round(step_ms * 1e3, 2),
         "unit": "us/step",
-        "n_gpus": 1,
-        "steps": args.pda_steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 4),
-        "higher_is_better": False,
+        "steps": steps,
         "dtype": "fp32",
-        "data": "synthetic",
         "config": {"workload": "config-set PDA mask+commit, recursive JSON GBNF (epsilon-reduced tables)",
                    "batch_rows": B, "vocab": V, "pda_states": g.num_states,
                    "prefix_depths": "uniform 0-8", "logits": "fp32 N(0,3)"},
         "mask_us": round(statistics.fmean(mask_ms) * 1e3, 2),
         "commit_us": round(statistics.fmean(commit_ms) * 1e3, 2),
         "row_vocab_entries_per_s": round(B * V / (step_ms * 1e-3), 1),
-        "broken_rows_at_end": broken,
-        "saturated_rows_at_end": sat,
-        "wall_ms_per_step_incl_setup_work": round((wall1 - wall0) * 1e3 / args.pda_steps, 3),
+        "broken_rows_at_end": int(batch._broken.sum()),
+        "saturated_rows_at_end": int((batch._configs[:, 1] != 0).sum()),
+        "roofline": _roofline(d_bytes, step_ms * 1e-3, traffic=None,
+                              scope="mask + commit step; diagnostic only (the walk is bound by its "
+                                    "instructions, not by HBM)",
+                              algorithmic_bytes=d_bytes, kernel="pda_memo_mask_kernel"),
     }
     if not args.no_cpu and args.pda_cpu_rows:
         from oracle import pda as OP
@@ -571,11 +668,9 @@ def bench_pda(args) -> int:
             "host_cpus": os.cpu_count(),
             "host_cpu_model": _cpu_model(),
         }
-        key = "parity_vs_reference_sampled_rows" if use_ref else "parity_vs_oracle_sampled_rows"
-        out[key] = bool(np.array_equal(lg, masked[:n].numpy()))
+        out["parity_vs_reference_sampled_rows" if use_ref else "parity_vs_oracle_sampled_rows"] = bool(
+            np.array_equal(lg, masked[:n].numpy()))
         if use_ref:
-            # the same reference call split over host threads by rows, on
-            # two rows per thread
             threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", "16") or 16), os.cpu_count() or 1, 16))
             npar = min(2 * threads, B)
             subp = cfgs[:npar].numpy().copy()
@@ -593,11 +688,11 @@ def bench_pda(args) -> int:
                            f"(oracle/_ref), scaled to B={B}"),
                 "parity_vs_device": bool(np.array_equal(lgp, masked[:npar].numpy())),
             }
-    print(json.dumps(out))
-    return 0
+    return out
 
 
-def bench_soft(args) -> int:
+# ------------------------------------------------------------------- soft --
+def bench_soft(args) -> dict:
     """Prior-weighted soft lookahead over the email DFA: B rows at random
     reachable states, fp32 logits N(0, 3), k-step lookahead with the row's
     softmax as the token prior; one step = one in-place rewrite of the
@@ -609,8 +704,8 @@ def bench_soft(args) -> int:
     from bpdecode_amd.ops import FsaTensors
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     B, V, K = args.soft_rows, args.vocab, args.soft_k
+    steps = min(args.soft_steps, args.steps)
     vocab = synth.serving_vocab(V, seed=1)
     fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
     S = fsa.num_states
@@ -620,10 +715,9 @@ def bench_soft(args) -> int:
     st = states.to(dev)
     src = synth.logits(B, V, std=3.0, dtype=torch.float32, seed=11, device=dev)
     work = torch.empty_like(src)
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if not args.no_flush else None
-    flush64 = flush.view(torch.int64) if flush is not None else None
+    flush64 = None if args.no_flush else torch.zeros(512 << 20, dtype=torch.uint8, device=dev).view(torch.int64)
     sh = torch.cuda.current_stream(dev).cuda_stream
-    n_total = args.warmup + args.soft_steps
+    n_total = args.warmup + steps
     kev = HipEvents(2 * n_total)
     for k in range(n_total):
         work.copy_(src)
@@ -634,34 +728,23 @@ def bench_soft(args) -> int:
         kev.record(2 * k + 1, sh)
     torch.cuda.synchronize()
     times = [kev.elapsed_ms(2 * k, 2 * k + 1) for k in range(args.warmup, n_total)]
+    kev.destroy()
     step_ms = statistics.fmean(times)
-    U = int(torch.unique(states[states >= 0]).numel())
-    members = int(sc.class_tok.numel())
-    # algorithmic bytes of one step: the stats kernel reads the logits and
-    # gathers the class members' logits; the output kernel reads the logits
-    # and the token -> class map and writes the logits
-    d_bytes = 3 * B * V * 4 + B * members * 4 + V * 4
+    d_bytes = B * V * 4 * 2 + S * V * 4
     out = {
         "metric": "µs/step prior-weighted soft lookahead (k=4), email DFA, B=128 V=151936 fp32",
         "value": round(step_ms * 1e3, 2),
         "unit": "us/step",
-        "n_gpus": 1,
-        "steps": args.soft_steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 4),
-        "higher_is_better": False,
-        "vs_baseline": None,
+        "steps": steps,
         "dtype": "fp32",
-        "data": "synthetic",
         "config": {"workload": "soft lookahead with the row softmax as token prior, email DFA",
                    "batch_rows": B, "vocab": V, "k": K, "dfa_states": S,
-                   "token_classes": sc.num_classes, "class_members": members,
-                   "distinct_row_states": U, "logits": "fp32 N(0,3)"},
-        "roofline": {"bound": "hbm", "achieved": round(d_bytes / (step_ms * 1e-3) / 1e9, 1),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(d_bytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "scope": "whole step (3 kernels)",
-                     "algorithmic_bytes": d_bytes},
+                   "token_classes": sc.num_classes, "class_members": int(sc.class_tok.numel()),
+                   "distinct_row_states": int(torch.unique(states[states >= 0]).numel()),
+                   "logits": "fp32 N(0,3)"},
+        "roofline": _roofline(d_bytes, step_ms * 1e-3, traffic=None,
+                              scope="whole step (statistics, rounds and output kernels)",
+                              algorithmic_bytes=d_bytes, bytes_formula="B*V*4*2 + S*V*4"),
         "row_vocab_entries_per_s": round(B * V / (step_ms * 1e-3), 1),
     }
     if not args.no_cpu and args.soft_cpu_rows:
@@ -689,8 +772,7 @@ def bench_soft(args) -> int:
             "host_cpu_model": _cpu_model(),
         }
         out["parity_vs_oracle_sampled_rows"] = ok
-    print(json.dumps(out))
-    return 0
+    return out
 
 
 if __name__ == "__main__":

@@ -16,11 +16,12 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
-DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-INDEX_I32, INDEX_I64 = 0, 1
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
+INDEX_I32, INDEX_I64, INDEX_I64_LOW32 = 0, 1, 2
+MAX_FUSED_PENDING = 256  # BPD_MAX_FUSED_PENDING
 FLAG_STATE_RANGE, FLAG_TOKEN_RANGE = 1, 2
 PDA_MAX_CONFIGS = 8
 PDA_MAX_DEPTH = 32
@@ -28,6 +29,7 @@ PDA_CONFIG_WORDS = 2 + PDA_MAX_CONFIGS + PDA_MAX_CONFIGS * PDA_MAX_DEPTH
 SOFT_MEMBER_CHUNK, SOFT_MEMBER_CAP_MAX = 4096, 1024  # BPD_SOFT_MEMBER_CHUNK / _CAP_MAX
 
 _DTYPE_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+_DENSE_DTYPE_CODE = {**_DTYPE_CODE, torch.float64: DTYPE_F64}
 _INDEX_CODE = {torch.int32: INDEX_I32, torch.int64: INDEX_I64}
 
 vp, i32, i64, f64, f32, sz = C.c_void_p, C.c_int32, C.c_int64, C.c_double, C.c_float, C.c_size_t
@@ -66,9 +68,10 @@ class SoftClassesC(C.Structure):
 _SIGNATURES = {
     "bpd_last_error": (C.c_char_p, []),
     "bpd_abi_version": (cint, []),
-    "bpd_dense_apply_mask": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f64, vp, vp]),
-    "bpd_dense_apply_mask_bits": (cint, [vp, cint, i64, i64, i64, vp, i64, i32, vp, vp, f64, vp, vp]),
-    "bpd_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, cint, i64, vp, cint, vp, vp]),
+    "bpd_dense_apply_mask": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, vp, i64, f64, vp, vp]),
+    "bpd_dense_apply_mask_bits": (cint, [vp, cint, i64, i64, i64, vp, i64, i32, vp, vp, vp, i64, f64,
+                                         vp, vp]),
+    "bpd_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, i64, vp, cint, i64, vp, cint, vp, vp]),
     "bpd_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp, vp, vp]),
     "bpd_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp, vp]),
     "bpd_fsa_apply_mask": (cint, [C.POINTER(FsaTableC), vp, cint, i64, i64, vp, vp, f64, vp, vp]),
@@ -148,22 +151,32 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def dtype_code(dt: torch.dtype) -> int:
-    code = _DTYPE_CODE.get(dt)
+def dtype_code(dt: torch.dtype, dense: bool = False) -> int:
+    """Logits dtype code; ``dense`` admits float64 (the tok_next mask only)."""
+    code = (_DENSE_DTYPE_CODE if dense else _DTYPE_CODE).get(dt)
     if code is None:
-        raise RuntimeError(f"logits dtype {dt} is not supported (float32, float16, bfloat16)")
+        names = "float32, float16, bfloat16" + (", float64" if dense else "")
+        raise RuntimeError(f"logits dtype {dt} is not supported ({names})")
     return code
 
 
-def index_code(dt: torch.dtype) -> int:
+def index_code(dt: torch.dtype, low32: bool = False) -> int:
+    """Token dtype code; ``low32`` reads int64 ids as their low 32 bits (the
+    ``tokens.to(torch.int32)`` the reference's batch classes apply)."""
     code = _INDEX_CODE.get(dt)
     if code is None:
         raise RuntimeError(f"token ids must be int32 or int64, got {dt}")
-    return code
+    return INDEX_I64_LOW32 if (low32 and code == INDEX_I64) else code
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream_of(device: torch.device) -> int:
     """Raw hipStream_t of torch's current stream on ``device``."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -1,11 +1,12 @@
 """Continuous-batching constraint state (batch.py of the reference).
 
 :class:`ConstraintBatch` keeps one int32 DFA state per slot in a device pool.
-``apply_mask`` and ``commit`` are one kernel launch each: the slot gather
-``pool[slots]`` is fused into the mask kernel, and the commit kernel gathers,
-advances and scatters back in one pass.  Slot writes from ``add`` / ``evict``
-/ ``reset`` are queued on the host and applied in one scatter before the pool
-is next read, so per-request churn costs no launches of its own.
+On the device, ``apply_mask`` and ``commit`` are one kernel launch each: the
+slot gather ``pool[slots]`` is fused into the mask kernel, and the commit
+kernel gathers, advances and scatters back in one pass.  Slot writes from
+``add`` / ``evict`` / ``reset`` are queued on the host; the next mask or
+commit launch carries them (uploaded with the slot list in one copy) and
+applies them itself, so per-request churn costs no launch of its own.
 """
 
 from __future__ import annotations
@@ -15,8 +16,9 @@ from collections.abc import Hashable, Sequence
 
 import torch
 
-from . import ops
-from .ops import FsaTensors, advance_state, apply_mask_, apply_soft_
+from . import _lib, ops
+from ._lib import check, lib
+from .ops import DENSE_AUTO_LIMIT, FsaTensors, advance_state, apply_mask_, apply_soft_
 from .tokenizer import Vocabulary
 
 FREE = -2  # slot holds no sequence
@@ -90,9 +92,12 @@ class GrammarCache:
         if hit is not None:
             self._cache.move_to_end(pattern)
             return hit
-        fsa = FsaTensors.build(pattern, self._vocab).to(self._device)
-        if fsa.tok_next is None and self._device.type == "cuda":
-            fsa = fsa.densify()  # built on the device by the table-builder kernel
+        # the reference's auto rule (ops.py:137-139): dense when
+        # states * vocab <= DENSE_AUTO_LIMIT, else the symbol-class walk;
+        # on the device the table is built by the table-builder kernel
+        fsa = FsaTensors.build(pattern, self._vocab, dense=False).to(self._device)
+        if fsa.num_states * fsa.vocab_size <= DENSE_AUTO_LIMIT:
+            fsa = fsa.densify()
         self._cache[pattern] = fsa
         if len(self._cache) > self._max:
             self._cache.popitem(last=False)
@@ -111,6 +116,12 @@ def index_tensor(values: Sequence[int], device: torch.device) -> torch.Tensor:
     return host.to(device, non_blocking=True)
 
 
+_DENSE_CODES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16,
+                torch.bfloat16: _lib.DTYPE_BF16, torch.float64: _lib.DTYPE_F64}
+_TOKEN_CODES = {torch.int32: _lib.INDEX_I32, torch.int64: _lib.INDEX_I64_LOW32}
+_COMMIT_FUSED_ROWS = 4096  # the one-block commit kernel takes queued writes up to this many rows
+
+
 class ConstraintBatch:
     """Fixed-capacity pool of grammar states sharing one :class:`FsaTensors`
     (batch.py:118-226 of the reference)."""
@@ -125,17 +136,45 @@ class ConstraintBatch:
         self._slot_of: dict[Hashable, int] = {}
         self._free: list[int] = list(reversed(range(capacity)))
         self._version = 0
-        self._slot_key: tuple | None = None
+        self._ids: list | None = None  # seq ids the cached slot tensor holds
+        self._ids_version = -1
+        self._slot_vals: list[int] = []
         self._slot_tensor: torch.Tensor | None = None
+        # an upload staged by prepare(): (slots, queued-writes tensor, count)
+        # and the queued writes it carries (still visible to state_of)
+        self._staged: tuple | None = None
+        self._staged_pending: dict[int, int] = {}
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device) if self.device.type == "cuda" else None
         if mask_cache is True:
             mask_cache = MaskCache(self.fsa)
         self.cache: MaskCache | None = mask_cache or None
-        if self.device.type == "cuda" and self.fsa.tok_next is not None:
+        on_dev = self.device.type == "cuda" and self.fsa.tok_next is not None
+        if on_dev:
             self.fsa.ensure_allow_bits()
+        # arguments of the device dense path that do not change per call
+        self._dense = on_dev
+        if on_dev:
+            tn, bits = self.fsa.tok_next, self.fsa.allow_bits
+            if tn.dtype != torch.int32 or not tn.is_contiguous():
+                self.fsa.tok_next = tn = tn.to(torch.int32).contiguous()
+            self._S, self._V = int(tn.shape[0]), int(tn.shape[1])
+            self._W = int(bits.shape[1])
+            self._tn_ptr, self._bits_ptr = tn.data_ptr(), bits.data_ptr()
+            self._pool_ptr, self._err_ptr = self._pool.data_ptr(), self._err.data_ptr()
 
     # --- pool -----------------------------------------------------------
+    def _unstage(self) -> None:
+        """Return staged queued writes to the queue (newer writes win)."""
+        if self._staged is not None:
+            if self._staged_pending:
+                merged = dict(self._staged_pending)
+                merged.update(self._pending)
+                self._pending = merged
+            self._staged = None
+            self._staged_pending = {}
+
     def _flush(self) -> None:
+        self._unstage()
         if self._pending:
             idx = index_tensor(list(self._pending.keys()), self.device)
             val = torch.tensor(list(self._pending.values()), dtype=torch.int32)
@@ -176,18 +215,96 @@ class ConstraintBatch:
         return seq_id in self._slot_of
 
     # --- per step ----------------------------------------------------------
+    def _same_ids(self, seq_ids: Sequence[Hashable]) -> bool:
+        if self._ids_version != self._version or self._ids is None:
+            return False
+        return self._ids == (seq_ids if type(seq_ids) is list else list(seq_ids))
+
+    def _remember(self, seq_ids: Sequence[Hashable], slot_vals: list[int], tensor: torch.Tensor) -> None:
+        self._ids = list(seq_ids)
+        self._ids_version = self._version
+        self._slot_vals = slot_vals
+        self._slot_tensor = tensor
+
     def _slots(self, seq_ids: Sequence[Hashable]) -> torch.Tensor:
-        key = (self._version, tuple(seq_ids))
-        if key != self._slot_key:
+        """int64 slot per row on the device (uploaded when the ids or the
+        slot map changed)."""
+        if not self._same_ids(seq_ids):
             slot_of = self._slot_of
-            self._slot_tensor = index_tensor([slot_of[s] for s in seq_ids], self.device)
-            self._slot_key = key
+            vals = [slot_of[s] for s in seq_ids]
+            self._remember(seq_ids, vals, index_tensor(vals, self.device))
         return self._slot_tensor
+
+    def _slots_fused(self, seq_ids: Sequence[Hashable], fuse: bool):
+        """(slots, pending tensor or None, count) for a device launch.  With
+        ``fuse`` the queued pool writes travel in the slot upload (one pinned
+        copy) and the launch applies them; the caller then calls
+        :meth:`_launched`.  Otherwise they are flushed first.  An upload
+        staged by :meth:`prepare` for the same ids, with nothing queued since,
+        is used as it is."""
+        staged = self._staged
+        if staged is not None:
+            if fuse and not self._pending and self._same_ids(seq_ids):
+                return staged
+            self._unstage()
+        n = len(self._pending)
+        if n == 0:
+            return self._slots(seq_ids), None, 0
+        if not fuse or n > _lib.MAX_FUSED_PENDING or len(seq_ids) == 0:
+            self._flush()
+            return self._slots(seq_ids), None, 0
+        if self._same_ids(seq_ids):
+            vals = self._slot_vals
+        else:
+            slot_of = self._slot_of
+            vals = [slot_of[s] for s in seq_ids]
+        B = len(vals)
+        host = torch.empty(B + 2 * n, dtype=torch.int64, pin_memory=True)
+        arr = host.numpy()
+        arr[:B] = vals
+        arr[B:B + n] = list(self._pending.keys())
+        arr[B + n:] = list(self._pending.values())
+        dev = host.to(self.device, non_blocking=True)
+        self._remember(seq_ids, vals, dev[:B])
+        self._staged = (dev[:B], dev[B:], n)
+        self._staged_pending = self._pending
+        self._pending = {}
+        return self._staged
+
+    def _launched(self) -> None:
+        """The staged queued writes were applied by a launch."""
+        self._staged = None
+        self._staged_pending = {}
+
+    def prepare(self, seq_ids: Sequence[Hashable]) -> None:
+        """Stage the device-side inputs of the next ``apply_mask`` /
+        ``commit`` for ``seq_ids``: the slot list and the queued pool writes
+        go to the device in one copy now (e.g. while the model computes the
+        logits), and the next launch for the same ids applies them.  Calling
+        it is optional; later add / evict / reset calls are merged in."""
+        if self._dense:
+            self._slots_fused(seq_ids, True)
+        else:
+            self._slots(seq_ids)
 
     def apply_mask(self, seq_ids: Sequence[Hashable], logits: torch.Tensor,
                    neg_inf: float = float("-inf")) -> torch.Tensor:
         """In place: every grammar-disallowed logit of ``logits``
         [len(seq_ids), vocab] becomes ``neg_inf``."""
+        if self._dense and self.cache is None and self._fast_logits(logits, len(seq_ids)):
+            code = _DENSE_CODES.get(logits.dtype)
+            if code is None:
+                raise RuntimeError(f"logits dtype {logits.dtype} is not supported")
+            B = len(seq_ids)
+            slots, pend, n = self._slots_fused(seq_ids, True)
+            ld = logits.stride(0) if B > 1 else self._V
+            check(lib().bpd_dense_apply_mask_bits(
+                logits.data_ptr(), code, B, self._V, ld, self._bits_ptr, self._W, self._S,
+                self._pool_ptr, slots.data_ptr(), None if pend is None else pend.data_ptr(), n,
+                float(neg_inf), self._err_ptr, _lib.stream_of(self.device)))
+            if n:
+                self._launched()
+            return logits
         slots = self._slots(seq_ids)
         pool = self._state
         if self.cache is not None:
@@ -201,6 +318,15 @@ class ConstraintBatch:
         else:
             apply_mask_(logits, self.fsa, pool[slots], neg_inf)
         return logits
+
+    def _fast_logits(self, logits: torch.Tensor, rows: int) -> bool:
+        """Logits the device dense path takes as they are: [rows, vocab] on
+        this device with unit column stride."""
+        if logits.dim() != 2 or logits.device != self.device:
+            return False
+        B, V = logits.shape
+        return B == rows and V == self._V and (logits.stride(1) == 1 or V <= 1) and (
+            B <= 1 or logits.stride(0) >= V)
 
     def apply_soft(self, seq_ids: Sequence[Hashable], logits: torch.Tensor, alpha: float = 1.0):
         """In place: ``logits += alpha * lookahead[state]`` (and mask)."""
@@ -222,14 +348,31 @@ class ConstraintBatch:
 
     def commit(self, seq_ids: Sequence[Hashable], tokens: torch.Tensor) -> torch.Tensor:
         """Advance each sequence by its sampled token; returns the new states
-        (``BROKEN`` where the token was off a valid path)."""
+        (``BROKEN`` where the token was off a valid path).  int64 ids count
+        by their low 32 bits, as the reference's ``tokens.to(torch.int32)``
+        does."""
+        B = len(seq_ids)
+        if (self._dense and tokens.device == self.device and tokens.dim() == 1
+                and tokens.numel() == B and tokens.is_contiguous()):
+            code = _TOKEN_CODES.get(tokens.dtype)
+            if code is not None:
+                slots, pend, n = self._slots_fused(seq_ids, B <= _COMMIT_FUSED_ROWS)
+                out = torch.empty(B, dtype=torch.int32, device=self.device)
+                check(lib().bpd_dense_advance(
+                    self._tn_ptr, self._S, self._V, self._pool_ptr, slots.data_ptr(),
+                    None if pend is None else pend.data_ptr(), n, tokens.data_ptr(), code, B,
+                    out.data_ptr(), 1, self._err_ptr, _lib.stream_of(self.device)))
+                if n:
+                    self._launched()
+                return out
         slots = self._slots(seq_ids)
         pool = self._state
         if self.fsa.tok_next is not None:
-            return ops.dense_advance(self.fsa.tok_next, pool, tokens, slots, True, self._err)
+            return ops.dense_advance(self.fsa.tok_next, pool, tokens, slots, True, self._err, low32=True)
+        tk = tokens.to(torch.int32) if tokens.dtype == torch.int64 else tokens
         if pool.device.type == "cuda":
-            return ops.fsa_advance(self.fsa, pool, tokens, slots, True, self._err)
-        nxt = advance_state(self.fsa, pool[slots], tokens.to(torch.int32))
+            return ops.fsa_advance(self.fsa, pool, tk, slots, True, self._err)
+        nxt = advance_state(self.fsa, pool[slots], tk)
         pool[slots] = nxt
         return nxt
 
@@ -248,6 +391,8 @@ class ConstraintBatch:
         slot = self._slot_of[seq_id]
         if slot in self._pending:
             return self._pending[slot]
+        if slot in self._staged_pending:
+            return self._staged_pending[slot]
         return int(self._pool[slot])
 
     def is_complete(self, seq_id: Hashable) -> bool:

@@ -152,8 +152,7 @@ __global__ __launch_bounds__(kFsaAdvThreads) void fsa_advance_kernel(
   const int64_t b = int64_t(blockIdx.x) * kFsaAdvThreads + threadIdx.x;
   if (b >= rows) return;
   const int32_t s = states[slots ? slots[b] : b];
-  int64_t t = tok_dtype == BPD_INDEX_I64 ? int64_t(int32_t(static_cast<const int64_t*>(tokens)[b]))
-                                         : int64_t(static_cast<const int32_t*>(tokens)[b]);
+  int64_t t = read_token(tokens, tok_dtype, b);
   if (t < 0) t += f.V;
   int32_t res = -1;
   if (t < 0 || t >= f.V) {
@@ -269,8 +268,7 @@ extern "C" int bpd_fsa_advance(const BpdFsaTable* table, int32_t* states, const 
                                const void* tokens, int token_dtype, int64_t rows, int32_t* next_out,
                                int write_back, int32_t* err, void* stream) {
   if (int rc = check_fsa(table)) return rc;
-  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64, "unknown token dtype code %d",
-              token_dtype);
+  BPD_REQUIRE(token_dtype_ok(token_dtype), "unknown token dtype code %d", token_dtype);
   BPD_REQUIRE(table->vocab > 0, "empty vocabulary");
   BPD_REQUIRE(rows >= 0, "negative row count");
   if (rows == 0) return BPD_OK;

@@ -24,8 +24,7 @@ void set_error(const char* fmt, ...) {
 namespace {
 
 inline int64_t host_token(const void* tokens, int dtype, int64_t b) {
-  return dtype == BPD_INDEX_I64 ? int64_t(int32_t(static_cast<const int64_t*>(tokens)[b]))
-                                : int64_t(static_cast<const int32_t*>(tokens)[b]);
+  return read_token(tokens, dtype, b);
 }
 
 template <typename T>
@@ -51,25 +50,28 @@ using namespace bpd;
 
 extern "C" const char* bpd_last_error(void) { return g_error; }
 
-extern "C" int bpd_abi_version(void) { return 4; }
+extern "C" int bpd_abi_version(void) { return 5; }
 
 extern "C" int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab,
                                          int64_t ld, const int32_t* tok_next,
                                          int32_t num_states, const int32_t* states,
                                          const int64_t* slots, double neg_inf) {
-  const int E = elem_bytes(dtype);
+  const int E = dense_elem_bytes(dtype);
   BPD_REQUIRE(E != 0, "unknown logits dtype code %d", dtype);
   BPD_REQUIRE(rows >= 0 && vocab >= 0 && ld >= vocab, "bad logits shape");
   BPD_REQUIRE(num_states > 0, "empty tok_next table");
-  uint32_t fill = 0;
-  if (int rc = fill_bits(dtype, neg_inf, &fill)) return rc;
+  uint64_t fill = 0;
+  if (int rc = fill_bits64(dtype, neg_inf, &fill)) return rc;
   for (int64_t b = 0; b < rows; ++b) {
     const int32_t s = states[slots ? slots[b] : b];
     BPD_REQUIRE(s < num_states, "index %d is out of bounds for dimension 0 with size %d", s,
                 num_states);
   }
-  if (E == 4)
-    mask_rows(static_cast<uint32_t*>(logits), rows, vocab, ld, tok_next, states, slots, fill);
+  if (E == 8)
+    mask_rows(static_cast<uint64_t*>(logits), rows, vocab, ld, tok_next, states, slots, fill);
+  else if (E == 4)
+    mask_rows(static_cast<uint32_t*>(logits), rows, vocab, ld, tok_next, states, slots,
+              static_cast<uint32_t>(fill));
   else
     mask_rows(static_cast<uint16_t*>(logits), rows, vocab, ld, tok_next, states, slots,
               static_cast<uint16_t>(fill));
@@ -80,8 +82,7 @@ extern "C" int bpd_host_dense_advance(const int32_t* tok_next, int32_t num_state
                                       int32_t* states, const int64_t* slots, const void* tokens,
                                       int token_dtype, int64_t rows, int32_t* next_out,
                                       int write_back) {
-  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64,
-              "unknown token dtype code %d", token_dtype);
+  BPD_REQUIRE(token_dtype_ok(token_dtype), "unknown token dtype code %d", token_dtype);
   BPD_REQUIRE(num_states > 0 && vocab > 0 && rows >= 0, "bad shape");
   BPD_REQUIRE(next_out || write_back, "advance with neither next_out nor write_back");
   // validate everything before any write, as an indexing error in the

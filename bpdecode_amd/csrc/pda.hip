@@ -1214,9 +1214,7 @@ __global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a)
   if (b >= a.rows) return;
   const int64_t row = a.slots ? a.slots[b] : b;
   int32_t* cfg = a.configs + row * kConfigWords;
-  const int64_t t = a.tok_dtype == BPD_INDEX_I64
-                        ? int64_t(int32_t(static_cast<const int64_t*>(a.tokens)[b]))
-                        : int64_t(static_cast<const int32_t*>(a.tokens)[b]);
+  const int64_t t = read_token(a.tokens, a.tok_dtype, b);
   bool ok;
   if (t < 0 || t >= a.vocab) {
     if (a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
@@ -1274,9 +1272,7 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
   int32_t* y = bufs[wave][1];
   for (int k = lane; k < kConfigWords; k += kWave) x[k] = cfg[k];
   wave_sync();
-  const int64_t t = a.tok_dtype == BPD_INDEX_I64
-                        ? int64_t(int32_t(static_cast<const int64_t*>(a.tokens)[b]))
-                        : int64_t(static_cast<const int32_t*>(a.tokens)[b]);
+  const int64_t t = read_token(a.tokens, a.tok_dtype, b);
   bool ok;
   if (t < 0 || t >= a.vocab) {
     if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
@@ -1526,8 +1522,7 @@ extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, 
                                int32_t* err, void* workspace, size_t workspace_bytes,
                                void* stream) {
   if (int rc = check_tables(g, toks)) return rc;
-  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64,
-              "unknown token dtype code %d", token_dtype);
+  BPD_REQUIRE(token_dtype_ok(token_dtype), "unknown token dtype code %d", token_dtype);
   BPD_REQUIRE(rows >= 0, "negative row count");
   if (rows == 0) return BPD_OK;
   AdvanceArgs a{};
@@ -1615,12 +1610,10 @@ extern "C" int bpd_host_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* t
                                     int token_dtype, int64_t rows, uint8_t* ok, uint8_t* broken,
                                     int32_t* status) {
   if (int rc = check_tables(g, toks)) return rc;
-  BPD_REQUIRE(token_dtype == BPD_INDEX_I32 || token_dtype == BPD_INDEX_I64,
-              "unknown token dtype code %d", token_dtype);
+  BPD_REQUIRE(token_dtype_ok(token_dtype), "unknown token dtype code %d", token_dtype);
   const PdaTableView gv = table_view(*g);
   auto token_at = [&](int64_t b) -> int64_t {
-    return token_dtype == BPD_INDEX_I64 ? int64_t(int32_t(static_cast<const int64_t*>(tokens)[b]))
-                                        : int64_t(static_cast<const int32_t*>(tokens)[b]);
+    return read_token(tokens, token_dtype, b);
   };
   for (int64_t b = 0; b < rows; ++b) {
     const int64_t t = token_at(b);

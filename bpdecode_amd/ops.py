@@ -346,10 +346,19 @@ def build_lookahead(fsa: FsaTensors, k: int) -> torch.Tensor:
 
 
 # ------------------------------------------------- dense kernels (+slots) --
-def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err=None):
+def _pending_args(pending: torch.Tensor | None) -> tuple[int | None, int]:
+    """(pointer, count) of a queued-writes tensor: int64 [2 * n] on the
+    device, n slots followed by their values."""
+    if pending is None or pending.numel() == 0:
+        return None, 0
+    return pending.data_ptr(), pending.numel() // 2
+
+
+def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err=None, pending=None):
     """``logits`` masked in place against ``tok_next`` rows; the state of row
     b is ``states[slots[b]]`` when ``slots`` is given (int64), else
-    ``states[b]``."""
+    ``states[b]``.  Any float dtype (float64 included).  ``pending``: queued
+    pool writes applied by the same launch (device only)."""
     dev = _same_device(logits, tok_next, states, slots)
     work, copied = _unit_stride_rows(logits)
     B, V = work.shape
@@ -359,17 +368,20 @@ def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err
     nb = B if slots is None else slots.numel()
     if nb != B:
         raise RuntimeError("one slot per logits row")
-    st = _i32(states)
+    st = states if (pending is not None and states.dtype == torch.int32) else _i32(states)
     if slots is None and st.numel() != B:
         raise RuntimeError(f"one state per logits row (got {st.numel()} states for {B} rows)")
     sl = None if slots is None else slots.to(torch.int64).contiguous()
     tn = tok_next if tok_next.dtype == torch.int32 and tok_next.is_contiguous() else _i32(tok_next)
-    code = _lib.dtype_code(work.dtype)
+    code = _lib.dtype_code(work.dtype, dense=True)
     ld = work.stride(0) if B > 1 else V
     if dev.type == "cuda":
+        pp, np_ = _pending_args(pending)
         check(lib().bpd_dense_apply_mask(ptr(work), code, B, V, ld, ptr(tn), S, ptr(st), ptr(sl),
-                                         float(neg_inf), ptr(err), _lib.stream_of(dev)))
+                                         pp, np_, float(neg_inf), ptr(err), _lib.stream_of(dev)))
     else:
+        if pending is not None and pending.numel():
+            raise RuntimeError("queued writes are applied by device launches only")
         check(lib().bpd_host_dense_apply_mask(ptr(work), code, B, V, ld, ptr(tn), S, ptr(st),
                                               ptr(sl), float(neg_inf)))
     if copied:
@@ -377,7 +389,8 @@ def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err
     return logits
 
 
-def dense_mask_bits_(logits, allow_bits, states, slots=None, neg_inf=float("-inf"), err=None):
+def dense_mask_bits_(logits, allow_bits, states, slots=None, neg_inf=float("-inf"), err=None,
+                     pending=None):
     """Device mask from the packed allow-bit table (same result as
     :func:`dense_mask_`)."""
     dev = _same_device(logits, allow_bits, states, slots)
@@ -390,32 +403,38 @@ def dense_mask_bits_(logits, allow_bits, states, slots=None, neg_inf=float("-inf
         raise RuntimeError(f"logits have {V} columns but the allow-bit table has {W} words per row")
     if slots is not None and slots.numel() != B:
         raise RuntimeError("one slot per logits row")
-    st = _i32(states)
+    st = states if (pending is not None and states.dtype == torch.int32) else _i32(states)
     if slots is None and st.numel() != B:
         raise RuntimeError(f"one state per logits row (got {st.numel()} states for {B} rows)")
     sl = None if slots is None else slots.to(torch.int64).contiguous()
-    code = _lib.dtype_code(work.dtype)
+    code = _lib.dtype_code(work.dtype, dense=True)
     ld = work.stride(0) if B > 1 else V
+    pp, np_ = _pending_args(pending)
     check(lib().bpd_dense_apply_mask_bits(ptr(work), code, B, V, ld, ptr(allow_bits), W, S, ptr(st),
-                                          ptr(sl), float(neg_inf), ptr(err), _lib.stream_of(dev)))
+                                          ptr(sl), pp, np_, float(neg_inf), ptr(err),
+                                          _lib.stream_of(dev)))
     if copied:
         logits.copy_(work)
     return logits
 
 
-def dense_advance(tok_next, states, tokens, slots=None, write_back=False, err=None):
+def dense_advance(tok_next, states, tokens, slots=None, write_back=False, err=None, pending=None,
+                  low32=False):
     """Next state per row; with ``write_back`` the pool ``states`` is updated
-    at the rows' slots as well.  Host-side token ids for a device table are
-    range-checked on the host (raising as torch indexing does) and copied
-    over; device-side ids out of range yield ``-1`` and set
-    ``BPD_FLAG_TOKEN_RANGE`` in ``err``."""
+    at the rows' slots as well.  int64 ids are indexed in full (ops.py:301-306
+    indexes with ``token_ids.long()``), or by their low 32 bits with
+    ``low32`` (the ``tokens.to(torch.int32)`` of batch.py:213).  Host-side
+    token ids for a device table are range-checked on the host (raising as
+    torch indexing does) and copied over; device-side ids out of range yield
+    ``-1`` and set ``BPD_FLAG_TOKEN_RANGE`` in ``err``."""
     S, V = tok_next.shape
     tk = tokens.contiguous()
     if tk.dtype not in (torch.int32, torch.int64):
         tk = tk.to(torch.int64)
     if tk.device != tok_next.device and tk.device.type == "cpu":
         if tk.numel():
-            lo, hi = int(tk.to(torch.int32).min()), int(tk.to(torch.int32).max())
+            vals = tk.to(torch.int32) if (low32 and tk.dtype == torch.int64) else tk
+            lo, hi = int(vals.min()), int(vals.max())
             bad = hi if hi >= V else (lo if lo < -V else None)
             if bad is not None:
                 raise IndexError(f"index {bad} is out of bounds for dimension 1 with size {V}")
@@ -432,11 +451,14 @@ def dense_advance(tok_next, states, tokens, slots=None, write_back=False, err=No
     sl = None if slots is None else slots.to(torch.int64).contiguous()
     tn = tok_next if tok_next.dtype == torch.int32 and tok_next.is_contiguous() else _i32(tok_next)
     out = torch.empty(B, dtype=torch.int32, device=dev)
-    code = _lib.index_code(tk.dtype)
+    code = _lib.index_code(tk.dtype, low32=low32)
     if dev.type == "cuda":
-        check(lib().bpd_dense_advance(ptr(tn), S, V, ptr(st), ptr(sl), ptr(tk), code, B, ptr(out),
-                                      int(write_back), ptr(err), _lib.stream_of(dev)))
+        pp, np_ = _pending_args(pending)
+        check(lib().bpd_dense_advance(ptr(tn), S, V, ptr(st), ptr(sl), pp, np_, ptr(tk), code, B,
+                                      ptr(out), int(write_back), ptr(err), _lib.stream_of(dev)))
     else:
+        if pending is not None and pending.numel():
+            raise RuntimeError("queued writes are applied by device launches only")
         check(lib().bpd_host_dense_advance(ptr(tn), S, V, ptr(st), ptr(sl), ptr(tk), code, B,
                                            ptr(out), int(write_back)))
     return out.view(tokens.shape) if tokens.dim() else out.reshape(())

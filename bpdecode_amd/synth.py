@@ -113,6 +113,29 @@ def random_walk_states(tok_next: torch.Tensor, start: int, eos_id: int, rows: in
     return torch.from_numpy(out)
 
 
+def random_byte_walk_states(tok_next: torch.Tensor, start: int, rows: int, max_bytes: int,
+                            seed: int) -> torch.Tensor:
+    """Per row: the state after a random valid partial document of
+    ``U[0, max_bytes]`` bytes -- each byte drawn uniformly among the
+    single-byte tokens (ids 0-255) the current state allows (stopping early
+    where none is allowed)."""
+    rng = np.random.default_rng(seed)
+    tn = tok_next.cpu().numpy()[:, :256]
+    allowed = {}
+    out = np.empty(rows, dtype=np.int32)
+    for r in range(rows):
+        s = start
+        for _ in range(int(rng.integers(0, max_bytes + 1))):
+            ids = allowed.get(s)
+            if ids is None:
+                ids = allowed[s] = np.nonzero(tn[s] >= 0)[0]
+            if ids.size == 0:
+                break
+            s = int(tn[s, ids[int(rng.integers(0, ids.size))]])
+        out[r] = s
+    return torch.from_numpy(out)
+
+
 def logits(rows: int, vocab: int, std: float, dtype: torch.dtype, seed: int, device="cpu") -> torch.Tensor:
     g = torch.Generator(device="cpu").manual_seed(seed)
     x = torch.randn(rows, vocab, generator=g) * std

@@ -17,6 +17,11 @@
  *   states    int32 pool; FREE = -2, BROKEN = -1.  With `slots` non-NULL the
  *             state of row b is states[slots[b]] (slots int64), otherwise
  *             states[b].
+ *   pending   int64 [2 * num_pending]: queued pool writes (num_pending
+ *             distinct slots, then their values).  An entry point that takes
+ *             them applies them before it reads the pool: a row whose slot
+ *             is queued reads the queued value, and every queued value is
+ *             stored into the pool by the same launch.
  *   logits    [rows, ld] elements of `dtype`, unit column stride.
  *   configs   int32 [*, BPD_PDA_CONFIG_WORDS] = {num_configs, saturated,
  *             depth[8], stack[8][32]} (padding-free PdaConfigSet).
@@ -41,9 +46,14 @@ extern "C" {
 #define BPD_DTYPE_F32 0
 #define BPD_DTYPE_F16 1
 #define BPD_DTYPE_BF16 2
+#define BPD_DTYPE_F64 3 /* dense tok_next mask only (bpd_dense_apply_mask*) */
 
 #define BPD_INDEX_I32 0
 #define BPD_INDEX_I64 1
+#define BPD_INDEX_I64_LOW32 2 /* int64 ids read as their low 32 bits, as tensor.to(torch.int32) */
+
+/* Queued state-pool writes a dense mask or commit launch applies itself. */
+#define BPD_MAX_FUSED_PENDING 256
 
 /* Bits OR-ed into the optional `err` word by kernels (device int32). */
 #define BPD_FLAG_STATE_RANGE 1 /* a state >= num_states was read */
@@ -63,15 +73,19 @@ int bpd_abi_version(void);
 /* ---------------------------------------------------------------- dense --
  * bpd_dense_apply_mask: logits[b, t] = neg_inf (converted to dtype as ATen's
  * checked scalar conversion does) iff state(b) < 0 or
- * tok_next[state(b), t] == -1; other entries are left bit-identical.
+ * tok_next[state(b), t] == -1; other entries are left bit-identical (never
+ * read or written).  dtype: float32, float16, bfloat16 or float64; logits
+ * need only element alignment.  A state >= num_states masks the row and sets
+ * BPD_FLAG_STATE_RANGE in `err`.  Queued pool writes (`pending`, at most
+ * BPD_MAX_FUSED_PENDING) are applied first.
  * Replaces the tok_next branch of ops.apply_mask_ (ops.py:271-276), which
  * ConstraintBatch.apply_mask (batch.py:176-190) calls after gathering
  * states = _state[slots]; the gather is fused here via `slots`.
  */
 int bpd_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
-                         const int32_t* tok_next, int32_t num_states,
-                         const int32_t* states, const int64_t* slots, double neg_inf,
-                         int32_t* err, void* stream);
+                         const int32_t* tok_next, int32_t num_states, int32_t* states,
+                         const int64_t* slots, const int64_t* pending, int64_t num_pending,
+                         double neg_inf, int32_t* err, void* stream);
 
 /* bpd_dense_apply_mask_bits: the same mask from the packed allow-bit table
  * (uint32 [num_states, words], words = ceil(vocab/32), bit t of row s set iff
@@ -81,20 +95,25 @@ int bpd_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, i
  * (ops.py:271-276 via batch.py:176-190). */
 int bpd_dense_apply_mask_bits(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                               const uint32_t* allow_bits, int64_t words, int32_t num_states,
-                              const int32_t* states, const int64_t* slots, double neg_inf,
-                              int32_t* err, void* stream);
+                              int32_t* states, const int64_t* slots, const int64_t* pending,
+                              int64_t num_pending, double neg_inf, int32_t* err, void* stream);
 
 /* bpd_dense_advance: nxt = state(b) < 0 ? -1 : tok_next[state(b), t(b)], where
- * t(b) = (int32)tokens[b] and a negative t indexes from the end as torch
- * advanced indexing does.  Writes next_out[b] (if non-NULL) and, with
+ * t(b) is tokens[b] read per token_dtype (BPD_INDEX_I32, BPD_INDEX_I64, or
+ * BPD_INDEX_I64_LOW32 for the int32 cast ConstraintBatch.commit applies,
+ * batch.py:213) and a negative t indexes from the end as torch advanced
+ * indexing does; an id out of [-vocab, vocab) yields -1 and sets
+ * BPD_FLAG_TOKEN_RANGE.  Writes next_out[b] (if non-NULL) and, with
  * write_back, stores nxt into the pool slot it was read from; all reads
- * happen before any write-back.  Replaces ops.advance_state's tok_next branch
- * (ops.py:301-306) plus ConstraintBatch.commit's scatter (batch.py:206-215).
+ * happen before any write-back.  Queued pool writes (`pending`, needs
+ * write_back and rows <= 4096) are applied first.  Replaces
+ * ops.advance_state's tok_next branch (ops.py:301-306) plus
+ * ConstraintBatch.commit's scatter (batch.py:206-215).
  */
 int bpd_dense_advance(const int32_t* tok_next, int32_t num_states, int64_t vocab,
-                      int32_t* states, const int64_t* slots, const void* tokens,
-                      int token_dtype, int64_t rows, int32_t* next_out, int write_back,
-                      int32_t* err, void* stream);
+                      int32_t* states, const int64_t* slots, const int64_t* pending,
+                      int64_t num_pending, const void* tokens, int token_dtype, int64_t rows,
+                      int32_t* next_out, int write_back, int32_t* err, void* stream);
 
 /* bpd_dense_compute_mask: packed allow bits from tok_next (bit t of row b set
  * iff state(b) >= 0 and tok_next[state(b), t] != -1).  Dense counterpart of

@@ -10,7 +10,9 @@ numpy restatement of the reference's dense tok_next path:
   state is negative or ``tok_next[state, t] == -1``; rejected entries take the
   fill value's bit pattern, others keep their bits.
 * :func:`advance`  ops.py:301-306: ``-1`` for a negative state else
-  ``tok_next[state, t]`` with torch's negative-index wrap.
+  ``tok_next[state, t]`` with torch's negative-index wrap; int64 ids index
+  in full (``token_ids.long()``), or by their low 32 bits with ``low32``
+  (the ``tokens.to(torch.int32)`` of batch.py:213 / device.py:278).
 * :func:`compute_mask_bits`  packed LSB-first allow bits.
 The fill value's bit pattern is taken from ATen's own scalar conversion (the
 reference's masked_fill_ arithmetic), including its overflow error.
@@ -22,7 +24,7 @@ import numpy as np
 import torch
 
 _TORCH_BITS = {torch.float32: (torch.int32, np.uint32), torch.float16: (torch.int16, np.uint16),
-               torch.bfloat16: (torch.int16, np.uint16)}
+               torch.bfloat16: (torch.int16, np.uint16), torch.float64: (torch.int64, np.uint64)}
 
 
 def fill_bits(dtype: torch.dtype, value: float) -> int:
@@ -70,9 +72,10 @@ def apply_mask(logits: torch.Tensor, tok_next, states, neg_inf: float = float("-
     return logits
 
 
-def advance(tok_next: np.ndarray, states, tokens) -> np.ndarray:
+def advance(tok_next: np.ndarray, states, tokens, low32: bool = True) -> np.ndarray:
     s = np.asarray(states, dtype=np.int64)
-    t = np.asarray(tokens).astype(np.int32).astype(np.int64)
+    t = np.asarray(tokens)
+    t = (t.astype(np.int32) if low32 else t).astype(np.int64)
     V = tok_next.shape[1]
     if t.size and (t.max() >= V or t.min() < -V):
         raise IndexError("token index out of range")
