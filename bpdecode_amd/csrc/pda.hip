@@ -14,6 +14,7 @@
 // walk starts from the row's set in global memory and every byte step writes
 // a freshly cleared set, so the 266 words written back on acceptance are
 // exactly those the reference produces.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -179,10 +180,11 @@ constexpr uint8_t kTDead = 0xFF;
 constexpr uint8_t kTOverflow = 0xFD;
 
 struct MemoWs {
+  uint32_t* header;   // [64]: word 0 = generation of the last mask launch on this workspace
   int32_t* pool;      // [rows, kMemoSets, kConfigWords]
   int32_t* cand;      // [rows, kMemoReq, kConfigWords]
   int32_t* overflow;  // [rows]
-  int32_t* meta;      // [rows, 4]: valid, tag low, tag high, unused
+  int32_t* meta;      // [rows, 4]: valid, tag low, tag high, generation
   uint32_t* table;    // [rows, kMemoSets * 64]: the row's transition table after the mask
   uint4* recs;        // [vocab] first 16 bytes of the token at walk position k, zero padded
   int2* tmeta;        // [vocab] (token id, length) of the token at walk position k
@@ -194,14 +196,15 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
-  return sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
+  return 256 + sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
          v * sizeof(int2) + r * 2 * v * sizeof(uint2);
 }
 
 MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   MemoWs w;
   const size_t r = size_t(rows);
-  w.pool = static_cast<int32_t*>(base);
+  w.header = static_cast<uint32_t*>(base);
+  w.pool = reinterpret_cast<int32_t*>(static_cast<char*>(base) + 256);
   w.cand = w.pool + r * kMemoSets * kConfigWords;
   w.overflow = w.cand + r * kMemoReq * kConfigWords;
   char* p = reinterpret_cast<char*>(w.overflow) + align256(r * 4);
@@ -215,6 +218,20 @@ MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   p += size_t(vocab) * sizeof(int2);
   w.queue = reinterpret_cast<uint2*>(p);
   return w;
+}
+
+// Generation of a mask launch: the launch stamps it on every row it writes
+// and in the workspace header, and the commit reuses a row's tables only when
+// the row's stamp equals the header's -- the rows were written by the last
+// mask launch on the workspace.  (The layout depends on the row count, so a
+// later launch with fewer rows overwrites parts of a larger batch's pool
+// while that batch's row metadata stays intact.)  Process-wide, never 0.
+std::atomic<uint32_t> g_mask_generation{1};
+
+uint32_t next_generation() {
+  uint32_t g = g_mask_generation.fetch_add(1);
+  if (g == 0) g = g_mask_generation.fetch_add(1);
+  return g;
 }
 
 // Identity of the grammar and token tables a workspace's transition tables
@@ -564,7 +581,7 @@ constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
                                                                      int table_in_lds, uint64_t tag,
-                                                                     int row_mode) {
+                                                                     uint32_t gen, int row_mode) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
@@ -1152,6 +1169,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     ws.meta[b * 4 + 0] = dead_row ? 0 : 1;
     ws.meta[b * 4 + 1] = int32_t(uint32_t(tag));
     ws.meta[b * 4 + 2] = int32_t(uint32_t(tag >> 32));
+    ws.meta[b * 4 + 3] = int32_t(gen);
+    ws.header[0] = gen;
   }
   if (overflowed) return;  // the direct walk writes this row
   if (!a.logits) {
@@ -1290,7 +1309,8 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
       int cur = -1;  // -1: use the direct walk
       const int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
       if (ws.pool && ws.meta[b * 4] == 1 && ws.meta[b * 4 + 1] == int32_t(uint32_t(tag)) &&
-          ws.meta[b * 4 + 2] == int32_t(uint32_t(tag >> 32)) && coop_same(x, pool, lane)) {
+          ws.meta[b * 4 + 2] == int32_t(uint32_t(tag >> 32)) &&
+          uint32_t(ws.meta[b * 4 + 3]) == ws.header[0] && coop_same(x, pool, lane)) {
         const uint8_t* T = reinterpret_cast<const uint8_t*>(ws.table + b * (kMemoSets * 64));
         cur = 0;
         for (int32_t i = s; i + 1 < e; ++i) {
@@ -1488,7 +1508,7 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&pda_memo_mask_kernel)));
     const bool in_lds = fa.sharedSizeBytes + tab_bytes <= size_t(max_lds);
     pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
-        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), row_mode);
+        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), next_generation(), row_mode);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
   }

@@ -345,16 +345,18 @@ def pda_compute_mask(g: PdaTensors, configs, slots=None) -> torch.Tensor:
     return out
 
 
-def pda_step(configs, g: PdaTensors, token_ids, slots=None, broken=None, err=None):
+def pda_step(configs, g: PdaTensors, token_ids, slots=None, broken=None, err=None, low32=False):
     """Advance ``configs[slots[b]]`` by ``token_ids[b]`` in place; returns
-    ``(ok uint8 [B], status int32 [B])``."""
+    ``(ok uint8 [B], status int32 [B])``.  ``low32`` reads int64 ids by their
+    low 32 bits (the ``tokens.to(torch.int32)`` of device.py:278)."""
     _check_configs(configs)
     tk = token_ids.contiguous()
     if tk.dtype not in (torch.int32, torch.int64):
         raise RuntimeError("token_ids must be int32")
     if tk.device != g.device and tk.device.type == "cpu":
-        if tk.numel() and (int(tk.min()) < 0 or int(tk.max()) >= g.vocab_size):
-            bad = int(tk.max()) if int(tk.max()) >= g.vocab_size else int(tk.min())
+        vals = tk.to(torch.int32) if (low32 and tk.dtype == torch.int64) else tk
+        if vals.numel() and (int(vals.min()) < 0 or int(vals.max()) >= g.vocab_size):
+            bad = int(vals.max()) if int(vals.max()) >= g.vocab_size else int(vals.min())
             raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {g.vocab_size}")
         tk = tk.to(g.device)
     dev = _same_device(g, configs, tk, slots, broken)
@@ -364,7 +366,7 @@ def pda_step(configs, g: PdaTensors, token_ids, slots=None, broken=None, err=Non
     sl = None if slots is None else slots.to(torch.int64).contiguous()
     ok = torch.empty(B, dtype=torch.uint8, device=dev)
     status = torch.empty(B, dtype=torch.int32, device=dev)
-    code = _lib.index_code(tk.dtype)
+    code = _lib.index_code(tk.dtype, low32=low32)
     if dev.type == "cuda":
         stream = _lib.stream_of(dev)
         ws, ws_bytes = g.mask_workspace(B, dev, stream)
@@ -459,7 +461,7 @@ class CFGConstraintBatch:
     def commit(self, seq_ids, tokens):
         slots = self._slots(seq_ids)
         tk = tokens if tokens.dtype in (torch.int32, torch.int64) else tokens.to(torch.int32)
-        _, status = pda_step(self._configs, self.g, tk, slots, self._broken, self._err)
+        _, status = pda_step(self._configs, self.g, tk, slots, self._broken, self._err, low32=True)
         return status
 
     def is_complete(self, seq_id: Hashable) -> bool:

@@ -90,3 +90,18 @@ def advance(t: Table, configs: np.ndarray, tokens) -> np.ndarray:
     lib().oracle_pda_advance(*t.args(), C.c_int32(t.eos), _p(t.toff), _p(t.tb), _p(configs),
                              _p(tk), C.c_int32(tk.size), _p(ok))
     return ok
+
+
+def compute_mask_threads(t: Table, configs: np.ndarray, threads: int) -> np.ndarray:
+    """:func:`compute_mask` with the rows split over host threads (the C call
+    releases the GIL); the same bits."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    configs = np.ascontiguousarray(configs, dtype=np.int32)
+    B = configs.shape[0]
+    threads = max(1, min(threads, B))
+    cuts = np.linspace(0, B, threads + 1).astype(int)
+    parts = [configs[a:b] for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
+    with ThreadPoolExecutor(max_workers=len(parts)) as ex:
+        out = list(ex.map(lambda c: compute_mask(t, c), parts))
+    return np.concatenate(out, axis=0)

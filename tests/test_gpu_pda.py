@@ -5,6 +5,8 @@ recursive JSON grammar at V = 151,936."""
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -362,3 +364,145 @@ def test_grammar_logits_processor_on_device(dev, eps_reduce):
             assert lp_cpu.is_complete(r) == lp_dev.is_complete(r)
         toks = [rng.choice((~torch.isneginf(s_cpu[r])).nonzero().flatten().tolist()) for r in range(3)]
         input_ids = torch.cat([input_ids, torch.tensor(toks).unsqueeze(1)], dim=1)
+
+
+def _unpack_allowed(bits: np.ndarray, V: int, dev) -> torch.Tensor:
+    """bool [B, V] on the device from packed LSB-first allow bits."""
+    b = torch.from_numpy(np.ascontiguousarray(bits).view(np.int32)).to(dev)
+    sh = torch.arange(32, device=dev, dtype=torch.int32)
+    return ((b.unsqueeze(-1) >> sh) & 1).bool().reshape(b.shape[0], -1)[:, :V]
+
+
+def _bench_rows(g, B):
+    """The benchmark's starting rows: JSON prefixes of 0-200 bytes, nesting
+    depth uniform over 0-8, seed 5."""
+    rng = np.random.default_rng(5)
+    rows = []
+    while len(rows) < B:
+        d = int(rng.integers(0, 9))
+        c = g.init_config()
+        if g.feed(c, synth.json_prefix(rng, d)):
+            rows.append(c)
+    return torch.stack(rows)
+
+
+def _oracle_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+@pytest.mark.timeout(900)
+def test_json_bench_trajectory_64_steps(dev, json_case):
+    """The recursive-JSON workload in full: B = 256 rows from the bench's
+    prefixes, V = 151,936, fp32 logits N(0, 3), 64 mask + commit steps with
+    tokens sampled from the oracle's masked softmax; every row's mask and raw
+    266-word config-set against the C oracle at every step."""
+    vocab, g, t = json_case
+    V, B = vocab.size, 256
+    _log("case json V=151936 B=256 trajectory 64 steps")
+    start = _bench_rows(g, B)
+    batch = CFGConstraintBatch(g, capacity=B, device=dev)
+    ids = list(range(B))
+    for i in ids:
+        batch.add(i)
+    batch._configs.copy_(start.to(dev))
+    mirror = start.numpy().copy()
+    gen = torch.Generator(device=dev).manual_seed(7)
+    threads = _oracle_threads()
+    for step in range(64):
+        lg = torch.randn((B, V), generator=gen, device=dev).mul_(3.0)
+        got = lg.clone()
+        batch.apply_mask(ids, got)
+        allowed = _unpack_allowed(OP.compute_mask_threads(t, mirror, threads), V, dev)
+        want = lg.masked_fill(~allowed, float("-inf"))
+        assert torch.equal(got, want), step
+        toks = torch.multinomial(torch.softmax(want, dim=-1), 1, generator=gen).view(-1)
+        status = batch.commit(ids, toks)
+        ok = OP.advance(t, mirror, toks.cpu().numpy())
+        assert ok.all() and status.cpu().tolist() == [1] * B, step
+        assert np.array_equal(batch._configs.cpu().numpy(), mirror), step
+        if step % 16 == 0:
+            _log(f"  step {step} ok")
+
+
+@pytest.mark.timeout(900)
+def test_json_reference_flattening_full_vocab(dev):
+    """The reference's own flattening of the recursive JSON grammar (no
+    epsilon reduction: it saturates the 8-config bound) at V = 151,936:
+    saturated config-sets go through the memoised kernel at full size.
+    Masks and raw config words against the C oracle, 8 steps."""
+    vocab = synth.serving_vocab(151_936, seed=1)
+    comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
+    g = build_pda_tensors(comp, vocab)  # the default: the reference's flattening
+    t = OP.Table(g)
+    V, B = vocab.size, 48
+    _log("case json reference flattening V=151936 B=48 8 steps")
+    rng = np.random.default_rng(21)
+    rows, saturated = [], 0
+    while len(rows) < B:
+        c = g.init_config()
+        if g.feed(c, synth.json_prefix(rng, int(rng.integers(0, 4)), max_len=60)):
+            rows.append(c)
+    start = torch.stack(rows)
+    gd = g.to(dev)
+    pool = start.to(dev)
+    mirror = start.numpy().copy()
+    gen = torch.Generator(device=dev).manual_seed(22)
+    threads = _oracle_threads()
+    for step in range(8):
+        saturated += int((mirror[:, 1] != 0).sum())
+        bits = OP.compute_mask_threads(t, mirror, threads)
+        got = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, bits), step
+        lg = torch.randn((B, V), generator=gen, device=dev)
+        want = lg.masked_fill(~_unpack_allowed(bits, V, dev), float("-inf"))
+        toks = torch.multinomial(torch.softmax(want, dim=-1), 1, generator=gen).view(-1).to(torch.int32)
+        ok, _ = pda_step(pool, gd, toks)
+        ok_o = OP.advance(t, mirror, toks.cpu().numpy())
+        assert ok.cpu().numpy().tolist() == ok_o.tolist(), step
+        assert np.array_equal(pool.cpu().numpy(), mirror), step
+    assert saturated > 0, "no saturated config-set met"
+
+
+def test_commit_after_smaller_mask_same_workspace(dev, json_case):
+    """mask(16 rows), then mask(4 rows of the same config-sets) on the same
+    workspace, then commit(16): the second launch overwrote parts of the
+    first one's interned sets, so the commit must not reuse the 16-row
+    tables it left.  Raw config words and ok flags against the oracle."""
+    vocab, g, t = json_case
+    _log("case json commit after a smaller mask")
+    gd = g.to(dev)
+    cfgs = _json_configs(g, 16, seed=51)
+    pool = cfgs.to(dev)
+    pda_compute_mask(gd, pool)
+    pda_compute_mask(gd, pool[:4].clone())
+    bits = OP.compute_mask(t, cfgs.numpy())
+    rng = np.random.default_rng(52)
+    toks = []
+    for r in range(16):
+        a = np.nonzero(np.unpackbits(bits[r].view(np.uint8), bitorder="little")[:vocab.size])[0]
+        a = a[a != vocab.eos_id]
+        toks.append(int(a[np.argmax([len(vocab.token_bytes[i]) for i in a])]) if len(a) else 0)
+    mirror = cfgs.numpy().copy()
+    ok_o = OP.advance(t, mirror, np.array(toks, dtype=np.int32))
+    ok, _ = pda_step(pool, gd, torch.tensor(toks, dtype=torch.int32, device=dev))
+    assert ok.cpu().numpy().tolist() == ok_o.tolist()
+    assert np.array_equal(pool.cpu().numpy(), mirror)
+
+
+def test_cfg_batch_commit_reads_int64_low_bits(dev, json_case):
+    """CFGConstraintBatch.commit converts int64 ids with tokens.to(int32) as
+    the reference does (device.py:278): 2**32 + t commits token t."""
+    vocab, g, t = json_case
+    cfgs = _json_configs(g, 4, seed=61)
+    batch = CFGConstraintBatch(g, capacity=4, device=dev)
+    for i in range(4):
+        batch.add(i)
+    batch._configs.copy_(cfgs.to(dev))
+    bits = OP.compute_mask(t, cfgs.numpy())
+    toks = [int(np.nonzero(np.unpackbits(bits[r].view(np.uint8), bitorder="little")[:vocab.size])[0][0])
+            for r in range(4)]
+    status = batch.commit(list(range(4)), torch.tensor([2**32 + k for k in toks], dtype=torch.int64, device=dev))
+    mirror = cfgs.numpy().copy()
+    ok_o = OP.advance(t, mirror, np.array(toks, dtype=np.int32))
+    assert ok_o.all() and status.cpu().tolist() == [1, 1, 1, 1]
+    assert np.array_equal(batch._configs.cpu().numpy(), mirror)
