@@ -27,6 +27,7 @@ PDA_MAX_CONFIGS = 8
 PDA_MAX_DEPTH = 32
 PDA_CONFIG_WORDS = 2 + PDA_MAX_CONFIGS + PDA_MAX_CONFIGS * PDA_MAX_DEPTH
 SOFT_MEMBER_CHUNK, SOFT_MEMBER_CAP_MAX = 4096, 1024  # BPD_SOFT_MEMBER_CHUNK / _CAP_MAX
+SOFT_PRIOR_SCRATCH_BYTES = 16 << 20  # BPD_SOFT_PRIOR_SCRATCH_BYTES
 
 _DTYPE_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 _DENSE_DTYPE_CODE = {**_DTYPE_CODE, torch.float64: DTYPE_F64}
@@ -103,6 +104,8 @@ _SIGNATURES = {
     "bpd_soft_prior_workspace_bytes": (sz, [i64, i64, i32, i32]),
     "bpd_soft_prior": (cint, [vp, i64, i64, i64, i32, vp, vp, i32, vp, vp, C.POINTER(SoftClassesC),
                               i32, f32, vp, sz, vp, vp]),
+    "bpd_soft_prior_noalloc": (cint, [vp, i64, i64, i64, i32, vp, vp, i32, vp, vp,
+                                      C.POINTER(SoftClassesC), i32, f32, vp, vp]),
     "bpd_host_soft_prior": (cint, [vp, i64, i64, i64, vp, i32, vp, vp, i32, vp, vp, i32, f32]),
     "bpd_host_soft_build_lookahead": (cint, [vp, i32, i64, vp, vp, i32, i32, vp]),
     "bpd_host_soft_apply": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f32]),

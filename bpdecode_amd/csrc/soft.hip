@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <unordered_map>
 #include <vector>
 
@@ -1030,11 +1031,14 @@ extern "C" size_t bpd_soft_prior_workspace_bytes(int64_t rows, int64_t vocab, in
   return a > b ? a : b;
 }
 
-extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld,
-                              int32_t num_states, const uint8_t* accept, const uint8_t* live,
-                              int32_t eos_id, const int32_t* states, const int64_t* slots,
-                              const BpdSoftClasses* classes, int32_t k, float alpha,
-                              void* workspace, size_t workspace_bytes, int32_t* err, void* stream) {
+namespace {
+
+// The prior lookahead on a caller-provided workspace (both entry points).
+int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int32_t num_states,
+                    const uint8_t* accept, const uint8_t* live, int32_t eos_id,
+                    const int32_t* states, const int64_t* slots, const BpdSoftClasses* classes,
+                    int32_t k, float alpha, void* workspace, size_t workspace_bytes, int32_t* err,
+                    void* stream) {
   BPD_REQUIRE(rows >= 0 && vocab > 0 && ld >= vocab, "bad logits shape");
   BPD_REQUIRE(num_states > 0 && num_states <= kPriorMaxStates, "1..%d states", kPriorMaxStates);
   BPD_REQUIRE(classes, "null classes");
@@ -1122,6 +1126,71 @@ extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_
 #undef BPD_PRIOR_OUT
   BPD_LAUNCHED();
   return BPD_OK;
+}
+
+}  // namespace
+
+extern "C" int bpd_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld,
+                              int32_t num_states, const uint8_t* accept, const uint8_t* live,
+                              int32_t eos_id, const int32_t* states, const int64_t* slots,
+                              const BpdSoftClasses* classes, int32_t k, float alpha,
+                              void* workspace, size_t workspace_bytes, int32_t* err, void* stream) {
+  return soft_prior_impl(logits, rows, vocab, ld, num_states, accept, live, eos_id, states, slots,
+                         classes, k, alpha, workspace, workspace_bytes, err, stream);
+}
+
+// Workspace of the allocation-free entry point: a file-scope device array,
+// one copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel or a copy: its device address comes from
+// hipGetSymbolAddress, once per device, on the first call there.
+static __device__ __align__(256) unsigned char scratch[BPD_SOFT_PRIOR_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to.
+int scratch_address(void* stream, void** out) {
+  hipDevice_t dev = 0;
+  BPD_HIP(hipStreamGetDevice(as_stream(stream), &dev));
+  BPD_REQUIRE(dev >= 0 && dev < kScratchDevices, "device %d out of range", int(dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    BPD_HIP(hipGetDevice(&cur));
+    if (cur != dev) BPD_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) BPD_HIP(hipSetDevice(cur));
+    if (e != hipSuccess)
+      BPD_FAIL(BPD_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    BPD_REQUIRE(p != nullptr, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BPD_OK;
+}
+}  // namespace
+
+extern "C" int bpd_soft_prior_noalloc(float* logits, int64_t rows, int64_t vocab, int64_t ld,
+                                      int32_t num_states, const uint8_t* accept,
+                                      const uint8_t* live, int32_t eos_id, const int32_t* states,
+                                      const int64_t* slots, const BpdSoftClasses* classes,
+                                      int32_t k, float alpha, int32_t* err, void* stream) {
+  BPD_REQUIRE(classes, "null classes");
+  BPD_REQUIRE(rows >= 0 && vocab > 0, "bad logits shape");
+  const size_t need = bpd_soft_prior_workspace_bytes(rows, vocab, classes->num_classes,
+                                                     classes->num_pieces);
+  BPD_REQUIRE(need <= size_t(BPD_SOFT_PRIOR_SCRATCH_BYTES),
+              "%lld rows x %d classes need %zu bytes of workspace, more than the %d-byte scratch of "
+              "the allocation-free entry point",
+              (long long)rows, classes->num_classes, need, BPD_SOFT_PRIOR_SCRATCH_BYTES);
+  if (rows == 0) return BPD_OK;
+  void* ws = nullptr;
+  if (int rc = scratch_address(stream, &ws)) return rc;
+  return soft_prior_impl(logits, rows, vocab, ld, num_states, accept, live, eos_id, states, slots,
+                         classes, k, alpha, ws, size_t(BPD_SOFT_PRIOR_SCRATCH_BYTES), err, stream);
 }
 
 // Token classes of the prior recurrence (once per grammar, host side).

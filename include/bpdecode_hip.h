@@ -377,6 +377,27 @@ int bpd_host_soft_prior(float* logits, int64_t rows, int64_t vocab, int64_t ld,
                         const uint8_t* live, int32_t eos_id, const int32_t* states,
                         const int64_t* slots, int32_t k, float alpha);
 
+/* bpd_soft_prior_noalloc: bpd_soft_prior without a workspace argument and
+ * without any allocation: its workspace is a file-scope device array of
+ * BPD_SOFT_PRIOR_SCRATCH_BYTES per GPU (held until the process ends; its
+ * address is looked up once per device on the first call there).  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory -- code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc.  Calls needing more workspace than the array holds
+ * (bpd_soft_prior_workspace_bytes > BPD_SOFT_PRIOR_SCRATCH_BYTES, e.g. more
+ * than 428 rows at the email DFA's 126 classes over a 151,936-token
+ * vocabulary) fail with BPD_ERR_INVALID.
+ * Results equal bpd_soft_prior's.  Every call on one GPU uses the same array:
+ * calls that overlap on one GPU (several streams or threads) race and must
+ * be serialised by the caller.  Nothing in the array has to start at zero
+ * (each launch writes every word it reads), so it is never cleared. */
+#define BPD_SOFT_PRIOR_SCRATCH_BYTES (16 << 20)
+int bpd_soft_prior_noalloc(float* logits, int64_t rows, int64_t vocab, int64_t ld,
+                           int32_t num_states, const uint8_t* accept, const uint8_t* live,
+                           int32_t eos_id, const int32_t* states, const int64_t* slots,
+                           const BpdSoftClasses* classes, int32_t k, float alpha, int32_t* err,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif
