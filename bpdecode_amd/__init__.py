@@ -6,12 +6,14 @@ GrammarCache, MaskCache), ``ops`` (FsaTensors and the mask / commit / soft
 operators), ``grammar`` (GBNF, JSON Schema, the device PDA and
 CFGConstraintBatch), ``hf`` / ``vllm`` adapters, and the host front-end
 (regex -> DFA, vocabularies).  All per-step computation runs in
-``libbpdecode_hip.so``.
+``libbpdecode_hip.so``.  The reference's per-sequence CPU constraints
+(RegexConstraint, TokenDFA, CFGConstraint and its unbounded PDA) are not part
+of this build: the batch classes serve CPU tensors through the library's host
+entry points.
 """
 
 from __future__ import annotations
 
-from .automaton import TokenDFA
 from .fsa import (
     FsaTable,
     TokenSymbols,
@@ -23,16 +25,14 @@ from .fsa import (
     step,
     token_symbols,
 )
-from .interface import BaseConstraint, Constraint
-from .reference import RegexConstraint
 from .regex import DFA, RegexSyntaxError, compile_regex
 from .tokenizer import DEFAULT_MODEL, Vocabulary
 
 __version__ = "0.1.0"
 
 __all__ = [
-    "BaseConstraint", "Constraint", "DEFAULT_MODEL", "DFA", "FsaTable", "RegexConstraint",
-    "RegexSyntaxError", "TokenDFA", "TokenSymbols", "Vocabulary", "advance_state_batch",
+    "DEFAULT_MODEL", "DFA", "FsaTable", "RegexSyntaxError", "TokenSymbols", "Vocabulary",
+    "advance_state_batch",
     "apply_mask", "build_reachability", "compile_regex", "compute_mask", "fsa_from_dfa", "step",
     "token_symbols", "__version__",
 ]

@@ -78,6 +78,17 @@ class MaskCache:
         return logits
 
 
+def build_bundle(pattern, vocab: Vocabulary, device: torch.device) -> FsaTensors:
+    """Grammar bundle of a regex (or DFA) on ``device`` by the reference's
+    density rule (ops.py:137-139): dense when states * vocab <= 32e6, the
+    symbol-class walk above it.  The table is built where the bundle lives
+    (the table-builder kernel on the device)."""
+    fsa = FsaTensors.build(pattern, vocab, dense=False).to(device)
+    if fsa.num_states * fsa.vocab_size <= DENSE_AUTO_LIMIT:
+        fsa = fsa.densify()
+    return fsa
+
+
 class GrammarCache:
     """LRU of compiled grammars for one vocabulary and device."""
 
@@ -92,12 +103,7 @@ class GrammarCache:
         if hit is not None:
             self._cache.move_to_end(pattern)
             return hit
-        # the reference's auto rule (ops.py:137-139): dense when
-        # states * vocab <= DENSE_AUTO_LIMIT, else the symbol-class walk;
-        # on the device the table is built by the table-builder kernel
-        fsa = FsaTensors.build(pattern, self._vocab, dense=False).to(self._device)
-        if fsa.num_states * fsa.vocab_size <= DENSE_AUTO_LIMIT:
-            fsa = fsa.densify()
+        fsa = build_bundle(pattern, self._vocab, self._device)
         self._cache[pattern] = fsa
         if len(self._cache) > self._max:
             self._cache.popitem(last=False)
@@ -207,6 +213,14 @@ class ConstraintBatch:
 
     def reset(self, seq_id: Hashable) -> None:
         self._pending[self._slot_of[seq_id]] = self.fsa.start
+
+    def move(self, src: Hashable, dst: Hashable) -> None:
+        """Sequence ``src`` continues as ``dst`` in the same slot (its state
+        is kept; nothing is written on the device)."""
+        if dst in self._slot_of:
+            raise KeyError(f"sequence {dst!r} already in the batch")
+        self._slot_of[dst] = self._slot_of.pop(src)
+        self._version += 1
 
     def __len__(self) -> int:
         return len(self._slot_of)

@@ -3,13 +3,12 @@ NFAs, the flattened device tables and the batched PDA step."""
 
 from __future__ import annotations
 
-from .constraint import CFGConstraint
 from .gbnf import GBNFSyntaxError, parse_gbnf
 from .ir import Grammar, Ref
 from .json_schema import JsonSchemaError, json_schema_to_grammar
-from .pda import PDA, CompiledGrammar, PDAOverflow
+from .pda import CompiledGrammar
 
 __all__ = [
-    "CFGConstraint", "CompiledGrammar", "GBNFSyntaxError", "Grammar", "JsonSchemaError",
-    "PDA", "PDAOverflow", "Ref", "json_schema_to_grammar", "parse_gbnf",
+    "CompiledGrammar", "GBNFSyntaxError", "Grammar", "JsonSchemaError", "Ref",
+    "json_schema_to_grammar", "parse_gbnf",
 ]

@@ -53,23 +53,38 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+# grammar bundles are long-lived: wrap (and, for the walking kernels, merge
+# the symbol classes of) each one once, keyed by the identity and version of
+# its tensors
+_FSA_CACHE: dict = {}
+_PDA_CACHE: dict = {}
+
+
+def _tensor_key(*parts) -> tuple:
+    return tuple((p.data_ptr(), p.numel(), p.dtype, p.device, p._version) if p is not None else None
+                 for p in parts)
+
+
 def _fsa(trans, accept, live, num_symbols, dead, offsets, symbols, eos_id) -> ops.FsaTensors:
-    return ops.FsaTensors(
+    key = _tensor_key(trans, accept, live, offsets, symbols) + (int(num_symbols), int(dead), int(eos_id))
+    hit = _FSA_CACHE.get(key)
+    if hit is not None:
+        return hit[0]
+    fsa = ops.FsaTensors(
         trans=trans.to(torch.int32), accept=accept.to(torch.uint8), live=live.to(torch.uint8),
         num_symbols=int(num_symbols), dead=int(dead), offsets=offsets.to(torch.int32),
         symbols=symbols.to(torch.int32), eos_id=int(eos_id),
     )
-
-
-# grammar bundles are long-lived: validate and wrap each one once
-_PDA_CACHE: dict = {}
+    if len(_FSA_CACHE) > 64:
+        _FSA_CACHE.clear()
+    _FSA_CACHE[key] = (fsa, (trans, accept, live, offsets, symbols))
+    return fsa
 
 
 def _pda(accept, live, eo, ek, elo, ehi, ed, ec, root_start, root_accept,
          tok_offsets=None, tok_bytes=None, eos_id=-1) -> _gdev.PdaTensors:
     parts = (accept, live, eo, ek, elo, ehi, ed, ec, tok_offsets, tok_bytes)
-    key = tuple((p.data_ptr(), p.numel(), p.device, p._version) if p is not None else None
-                for p in parts) + (int(root_start), int(root_accept), int(eos_id))
+    key = _tensor_key(*parts) + (int(root_start), int(root_accept), int(eos_id))
     hit = _PDA_CACHE.get(key)
     if hit is not None:
         return hit

@@ -11,10 +11,9 @@ import torch
 from bpdecode_amd import ops
 from bpdecode_amd.batch import BROKEN, FREE, ConstraintBatch, GrammarCache, MaskCache
 from bpdecode_amd.ops import FsaTensors
-from bpdecode_amd.reference import RegexConstraint
 from bpdecode_amd.tokenizer import Vocabulary
 from oracle import dense as OD
-from tests._util import TOY_PATTERNS, TOY_VOCAB, bits_of, oracle_table
+from tests._util import TOY_PATTERNS, TOY_VOCAB, OracleWalk, bits_of, oracle_table
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 
@@ -136,13 +135,13 @@ def test_lifecycle_slots_are_reused():
 ])
 def test_matches_single_sequence_reference(pattern, seq, mask_cache):
     batch = ConstraintBatch(GrammarCache(VOCAB).get(pattern), capacity=4, mask_cache=mask_cache)
-    ref = RegexConstraint(pattern, VOCAB)
+    ref = OracleWalk(FsaTensors.build(pattern, VOCAB))
     batch.add("s")
     for tok in seq:
         logits = torch.zeros(1, VOCAB.size)
         batch.apply_mask(["s"], logits)
         got = {i for i in range(VOCAB.size) if logits[0, i].item() == 0.0}
-        assert got == {i for i in range(VOCAB.size) if ref.accepts(i)}
+        assert got == ref.allowed()
         batch.commit(["s"], torch.tensor([tok], dtype=torch.int32))
         ref.advance(tok)
         assert batch.is_complete("s") == ref.is_complete()

@@ -2,11 +2,10 @@
 compile_regex, the JSON-Schema residual DFA and the flattened PDA tables of
 build_pda_tensors, against vectors written by tests/golden/make_golden.py from
 the reference's own front-end.  Also the UTF-8 range lowering against the
-Python codec and grammar membership against an independent matcher."""
+Python codec."""
 
 from __future__ import annotations
 
-import itertools
 from pathlib import Path
 
 import numpy as np
@@ -15,9 +14,8 @@ import pytest
 from bpdecode_amd.fsa import fsa_from_dfa
 from bpdecode_amd.grammar.device import build_pda_tensors
 from bpdecode_amd.grammar.gbnf import GBNFSyntaxError, parse_gbnf
-from bpdecode_amd.grammar.ir import Alt, CharSet, Concat, Empty, Opt, Plus, Ref, Star
 from bpdecode_amd.grammar.json_schema import json_schema_to_grammar
-from bpdecode_amd.grammar.pda import PDA, CompiledGrammar
+from bpdecode_amd.grammar.pda import CompiledGrammar
 from bpdecode_amd.grammar.regular import frame_is_regular, residual_dfa
 from bpdecode_amd.regex import RegexSyntaxError, compile_regex
 from bpdecode_amd.regex.utf8 import utf8_sequences
@@ -85,63 +83,3 @@ def test_syntax_errors():
     for bad in ['root ::= "a', "root ::= [a", "root = x", "root ::= (x"]:
         with pytest.raises((GBNFSyntaxError, KeyError)):
             parse_gbnf(bad)
-
-
-def member(grammar, text):
-    """Independent recursive matcher (no NFA): the set of end positions."""
-    rules = grammar.rules
-    busy = set()
-
-    def m(e, pos):
-        if isinstance(e, Empty):
-            return {pos}
-        if isinstance(e, CharSet):
-            return {pos + 1} if pos < len(text) and e.matches(ord(text[pos])) else set()
-        if isinstance(e, Ref):
-            key = (e.name, pos)
-            if key in busy:
-                return set()
-            busy.add(key)
-            try:
-                return m(rules[e.name], pos)
-            finally:
-                busy.discard(key)
-        if isinstance(e, Concat):
-            cur = {pos}
-            for p in e.parts:
-                cur = set().union(*(m(p, q) for q in cur)) if cur else set()
-            return cur
-        if isinstance(e, Alt):
-            return set().union(*(m(o, pos) for o in e.options))
-        if isinstance(e, Opt):
-            return {pos} | m(e.node, pos)
-        reached = set() if isinstance(e, Plus) else {pos}
-        frontier = {pos}
-        while frontier:
-            nxt = set()
-            for p in frontier:
-                for q in m(e.node, p):
-                    if q not in reached:
-                        reached.add(q)
-                        nxt.add(q)
-            frontier = nxt
-        return reached
-
-    return len(text) in m(rules[grammar.root], 0)
-
-
-@pytest.mark.parametrize("src,alpha", [
-    ('root ::= "(" root ")" | "x"', "()x"),
-    ('root ::= field ("," field)*\nfield ::= [a-z]+', "ab,"),
-    ('root  ::= "[" (val ("," val)*)? "]"\nval   ::= "[" (val ("," val)*)? "]" | [0-9]+', "[]0,"),
-    ('root ::= sign? [0-9]+ frac?\nsign ::= "-"\nfrac ::= "." [0-9]+', "-.0"),
-])
-def test_unbounded_pda_membership(src, alpha):
-    grammar = parse_gbnf(src)
-    comp = CompiledGrammar.build(grammar)
-    for n in range(6):
-        for combo in itertools.product(alpha, repeat=n):
-            s = "".join(combo)
-            pda = PDA(comp)
-            got = all(pda.advance_byte(ord(c)) for c in s) and not pda.dead() and pda.is_complete()
-            assert got == member(grammar, s), s

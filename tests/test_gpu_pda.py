@@ -339,30 +339,37 @@ def test_json_commit_paths_match_oracle(dev, json_case, monkeypatch, limit, mode
 
 @pytest.mark.parametrize("eps_reduce", [False, True])
 def test_grammar_logits_processor_on_device(dev, eps_reduce):
-    """GrammarLogitsProcessor(device=cuda) — the HF calling convention over
-    the device PDA kernels — masks exactly as the memoised CPU backend,
-    step after step, on a recursive grammar (bf16 scores on the device,
-    fp32 on the host)."""
+    """GrammarLogitsProcessor(device=cuda) -- the HF calling convention over
+    the device PDA kernels, bf16 scores masked in place -- against the C
+    oracle step after step on a recursive grammar, and equal to the host
+    backend on fp32 scores."""
     import random
 
     from bpdecode_amd.hf import GrammarLogitsProcessor
 
     _log(f"case GrammarLogitsProcessor device eps_reduce={eps_reduce}")
     grammar = 'root ::= "(" root ")" | "[" "1"? "]" | "x" | "{a" ":0," root "}"'
-    lp_cpu = GrammarLogitsProcessor(grammar, VOCAB, backend="cpu")
+    lp_cpu = GrammarLogitsProcessor(grammar, VOCAB, backend="cpu", eps_reduce=eps_reduce)
     lp_dev = GrammarLogitsProcessor(grammar, VOCAB, device=dev, eps_reduce=eps_reduce)
-    assert lp_dev.backend == "device"
+    assert lp_dev.backend == "device" and lp_cpu.backend == "cpu"
+    t = OP.Table(build_pda_tensors(CompiledGrammar.build(parse_gbnf(grammar)), VOCAB, eps_reduce=eps_reduce))
+    mirror = np.repeat(OP.init(t)[None], 3, axis=0)
     input_ids = torch.zeros(3, 1, dtype=torch.long)
     rng = random.Random(7)
-    for _ in range(10):
+    for step in range(10):
         s_cpu = torch.zeros(3, VOCAB.size)
         s_dev = torch.zeros(3, VOCAB.size, dtype=torch.bfloat16, device=dev)
+        ptr0 = s_dev.data_ptr()
         lp_cpu(input_ids, s_cpu)
-        lp_dev(input_ids.to(dev), s_dev)
-        assert torch.equal(torch.isneginf(s_cpu), torch.isneginf(s_dev.cpu()))
+        assert lp_dev(input_ids.to(dev), s_dev).data_ptr() == ptr0
+        want = np.zeros((3, VOCAB.size), np.float32)
+        OP.apply_mask(t, mirror, want)
+        assert torch.equal(torch.isneginf(s_dev.cpu()), torch.from_numpy(np.isneginf(want))), step
+        assert torch.equal(torch.isneginf(s_cpu), torch.isneginf(s_dev.cpu())), step
         for r in range(3):
             assert lp_cpu.is_complete(r) == lp_dev.is_complete(r)
         toks = [rng.choice((~torch.isneginf(s_cpu[r])).nonzero().flatten().tolist()) for r in range(3)]
+        assert OP.advance(t, mirror, toks).all()
         input_ids = torch.cat([input_ids, torch.tensor(toks).unsqueeze(1)], dim=1)
 
 

@@ -1,7 +1,8 @@
 """PDA path through the library's host entry points against the C oracle
 (raw config words included), and the CFGConstraintBatch / processor
 scenarios of the reference's test_pda_device.py and
-test_grammar_device_batch.py against the unbounded host PDA."""
+test_grammar_device_batch.py against the C oracle, with complete strings
+checked against an independent recursive matcher of the grammar."""
 
 from __future__ import annotations
 
@@ -13,16 +14,16 @@ import pytest
 import torch
 
 from bpdecode_amd import synth
-from bpdecode_amd.grammar.constraint import CFGConstraint
 from bpdecode_amd.grammar.device import (
     PDA_CONFIG_FLAT, CFGConstraintBatch, build_pda_tensors, pda_advance_state, pda_apply_mask_,
     _walk_order, pda_compute_mask, pda_mask_, pda_step,
 )
 from bpdecode_amd.grammar.gbnf import parse_gbnf
-from bpdecode_amd.grammar.pda import PDA, CompiledGrammar
+from bpdecode_amd.grammar.pda import CompiledGrammar
 from bpdecode_amd.hf import GrammarLogitsProcessor
 from oracle import pda as OP
 from tests._util import PDA_VOCAB as VOCAB
+from tests._util import member
 from tests.golden.cases import GRAMMARS
 
 
@@ -110,59 +111,67 @@ def _allowed_ops(g, cfg):
     return {i for i in range(VOCAB.size) if logits[0, i].item() == 0.0}
 
 
-def _allowed_ref(pda, vocab):
-    out = set()
-    for t in range(vocab.size):
-        if t == vocab.eos_id:
-            if pda.is_complete():
-                out.add(t)
-            continue
-        snap = pda.configs
-        ok = all(pda.advance_byte(b) for b in vocab.token_bytes[t]) and not pda.dead()
-        pda.set_configs(snap)
-        if ok:
-            out.add(t)
-    return out
+def _allowed_oracle(t, cfg: np.ndarray) -> set[int]:
+    bits = OP.compute_mask(t, cfg.reshape(1, -1))[0]
+    return {k for k in range(VOCAB.size) if bits[k >> 5] >> (k & 31) & 1}
+
+
+def _text(toks) -> str:
+    return b"".join(VOCAB.token_bytes[k] for k in toks).decode("latin-1")
 
 
 @pytest.mark.parametrize("src", REF_GRAMMARS)
-def test_random_walk_matches_unbounded_pda(src):
-    comp = CompiledGrammar.build(parse_gbnf(src))
-    g = build_pda_tensors(comp, VOCAB)
-    pda = PDA(comp)
+def test_random_walk_matches_oracle(src):
+    """test_pda_device.py:62-87: a random walk through allowed tokens, the
+    operators' allowed set equal to the C oracle's at every step and EOS
+    allowed exactly when the text so far is in the language."""
+    grammar = parse_gbnf(src)
+    g = build_pda_tensors(CompiledGrammar.build(grammar), VOCAB)
+    t = OP.Table(g)
     cfg = g.init_batch(1)
+    mirror = OP.init(t).reshape(1, -1).copy()
     rng = random.Random(0)
+    walked = []
     for _ in range(15):
-        want = _allowed_ref(pda, VOCAB)
+        want = _allowed_oracle(t, mirror)
         assert _allowed_ops(g, cfg) == want
+        assert (VOCAB.eos_id in want) == member(grammar, _text(walked))
         choices = sorted(want - {VOCAB.eos_id})
         if not choices:
             break
         tok = rng.choice(choices)
-        assert all(pda.advance_byte(b) for b in VOCAB.token_bytes[tok])
         assert bool(pda_advance_state(cfg, g, torch.tensor([tok], dtype=torch.int32)).item())
+        assert OP.advance(t, mirror, [tok]).all()
+        assert np.array_equal(cfg.numpy(), mirror)
+        walked.append(tok)
 
 
 @pytest.mark.parametrize("src", REF_GRAMMARS)
 def test_exhaustive_short_strings_agree(src):
-    comp = CompiledGrammar.build(parse_gbnf(src))
-    g = build_pda_tensors(comp, VOCAB)
+    """test_pda_device.py:90-120: every token string up to length 3 -- the
+    operators' ok flags and config words equal the C oracle's, and a
+    string they accept whole is complete exactly when the matcher says it is
+    in the language."""
+    grammar = parse_gbnf(src)
+    g = build_pda_tensors(CompiledGrammar.build(grammar), VOCAB)
+    t = OP.Table(g)
     alphabet = [i for i in range(13) if i != VOCAB.eos_id]
     tested = 0
     for n in range(4):
         for combo in itertools.product(alphabet, repeat=n):
-            pda = PDA(comp)
             cfg = g.init_batch(1)
+            mirror = OP.init(t).reshape(1, -1).copy()
             dead = False
             for tok in combo:
-                ok_ref = all(pda.advance_byte(b) for b in VOCAB.token_bytes[tok]) and not pda.dead()
                 ok_dev = bool(pda_advance_state(cfg, g, torch.tensor([tok], dtype=torch.int32)).item())
+                ok_ref = bool(OP.advance(t, mirror, [tok])[0])
                 assert ok_ref == ok_dev, (src, combo)
+                assert np.array_equal(cfg.numpy(), mirror)
                 if not ok_ref:
                     dead = True
                     break
             if not dead:
-                assert pda.is_complete() == (VOCAB.eos_id in _allowed_ops(g, cfg))
+                assert member(grammar, _text(combo)) == (VOCAB.eos_id in _allowed_ops(g, cfg))
                 tested += 1
     assert tested > 0
 
@@ -180,26 +189,33 @@ def test_reject_leaves_config_unchanged_and_flat_size():
 
 
 @pytest.mark.parametrize("src", REF_GRAMMARS[:2])
-def test_batch_matches_cfgconstraint_random_walk(src):
-    comp = CompiledGrammar.build(parse_gbnf(src))
-    g = build_pda_tensors(comp, VOCAB)
+def test_batch_matches_oracle_random_walk(src):
+    """test_grammar_device_batch.py:34-80: CFGConstraintBatch on CPU
+    tensors, rows walking independently, against the C oracle per row."""
+    grammar = parse_gbnf(src)
+    g = build_pda_tensors(CompiledGrammar.build(grammar), VOCAB)
+    t = OP.Table(g)
     n = 3
     batch = CFGConstraintBatch(g, capacity=n)
-    refs = [CFGConstraint.from_compiled(comp, VOCAB) for _ in range(n)]
+    mirror = np.repeat(OP.init(t)[None], n, axis=0)
+    texts = [[] for _ in range(n)]
     for i in range(n):
         batch.add(i)
     rng = random.Random(0)
     for _ in range(12):
         logits = torch.zeros(n, VOCAB.size)
         batch.apply_mask(list(range(n)), logits)
+        allowed = [_allowed_oracle(t, mirror[i]) for i in range(n)]
         for i in range(n):
-            got = {t for t in range(VOCAB.size) if logits[i, t].item() == 0.0}
-            assert got == {t for t in range(VOCAB.size) if refs[i].accepts(t)}
-            assert batch.is_complete(i) == refs[i].is_complete()
-        toks = [rng.choice(sorted(t for t in range(VOCAB.size) if refs[i].accepts(t))) for i in range(n)]
+            got = {k for k in range(VOCAB.size) if logits[i, k].item() == 0.0}
+            assert got == allowed[i]
+            assert batch.is_complete(i) == member(grammar, _text(texts[i]))
+        toks = [rng.choice(sorted(allowed[i] - {VOCAB.eos_id}) or [VOCAB.eos_id]) for i in range(n)]
         batch.commit(list(range(n)), torch.tensor(toks, dtype=torch.int32))
+        assert OP.advance(t, mirror, toks).all()
         for i in range(n):
-            refs[i].advance(toks[i])
+            if toks[i] != VOCAB.eos_id:
+                texts[i].append(toks[i])
 
 
 def test_batch_lifecycle_and_broken_rows():
@@ -223,20 +239,28 @@ def test_batch_lifecycle_and_broken_rows():
 
 
 def test_logits_processor_device_backend_matches_cpu_backend():
-    grammar = 'root ::= "(" root ")" | "x" | "y"'
-    lp_cpu = GrammarLogitsProcessor(grammar, VOCAB, backend="cpu")
-    lp_dev = GrammarLogitsProcessor(grammar, VOCAB, device="cpu", backend="device")
+    """test_grammar_hf.py: both backends in generate()'s calling convention
+    (bf16 and fp32 scores) against the C oracle, row by row."""
+    src = 'root ::= "(" root ")" | "x" | "y"'
+    lp_cpu = GrammarLogitsProcessor(src, VOCAB, backend="cpu")
+    lp_dev = GrammarLogitsProcessor(src, VOCAB, device="cpu", backend="device")
     assert lp_cpu.backend == "cpu" and lp_dev.backend == "device"
+    t = OP.Table(build_pda_tensors(CompiledGrammar.build(parse_gbnf(src)), VOCAB))
+    mirror = np.repeat(OP.init(t)[None], 2, axis=0)
     input_ids = torch.zeros(2, 1, dtype=torch.long)
     rng = random.Random(1)
-    for _ in range(8):
+    for step in range(8):
         s_cpu = torch.zeros(2, VOCAB.size)
         s_dev = torch.zeros(2, VOCAB.size, dtype=torch.bfloat16)
         lp_cpu(input_ids, s_cpu)
         lp_dev(input_ids, s_dev)
+        want = np.zeros((2, VOCAB.size), np.float32)
+        OP.apply_mask(t, mirror, want)
+        assert torch.equal(torch.isneginf(s_cpu), torch.from_numpy(np.isneginf(want)))
         assert torch.equal(torch.isneginf(s_cpu), torch.isneginf(s_dev))
         assert lp_cpu.is_complete(0) == lp_dev.is_complete(0)
         toks = [rng.choice((~torch.isneginf(s_cpu[r])).nonzero().flatten().tolist()) for r in range(2)]
+        assert OP.advance(t, mirror, toks).all()
         input_ids = torch.cat([input_ids, torch.tensor(toks).unsqueeze(1)], dim=1)
 
 
