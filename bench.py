@@ -254,6 +254,30 @@ class DenseRun:
             self.next_id += 1
 
 
+def _line_bytes_per_state(fsa, e: int):
+    """Per state (index S: a negative state), the bytes the memory side
+    moves for one row's mask at 128-byte line granularity: a line whose
+    elements are all rejected is written (128 B), a line mixing kept and
+    rejected elements is read and written back (256 B: the partial write is
+    merged below the caches), a line of kept elements is not touched."""
+    import numpy as np
+
+    bits = fsa.allow_bits.cpu().numpy().view(np.uint32)
+    S, W = bits.shape
+    V = fsa.vocab_size
+    per = 128 // e  # elements per line
+    allowed = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little")[:, :V].astype(np.int32)
+    pad = (-V) % per
+    if pad:
+        allowed = np.concatenate([allowed, np.ones((S, pad), np.int32)], axis=1)
+    counts = allowed.reshape(S, -1, per).sum(axis=2)
+    full_rej = (counts == 0).sum(axis=1)
+    mixed = ((counts > 0) & (counts < per)).sum(axis=1)
+    out = full_rej * 128 + mixed * 256
+    lines = -(-V // per)
+    return np.concatenate([out, [lines * 128]]).astype(np.float64)
+
+
 def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup, record_cpu=0):
     """The three passes of the dense step over one trajectory.  Returns the
     timings (ms lists over the timed steps), the distinct live states per
@@ -267,7 +291,8 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
     if not args.no_flush:
         flush64 = torch.zeros(512 << 20, dtype=torch.uint8, device=fsa.device).view(torch.int64)
     sh = torch.cuda.current_stream(fsa.device).cuda_stream
-    tokens, distinct, recorded, nxt_ref = [], [], [], []
+    tokens, distinct, recorded, nxt_ref, line_bytes = [], [], [], [], []
+    per_state = _line_bytes_per_state(fsa, torch.tensor([], dtype=dtype).element_size())
 
     # record pass: two brackets, sampling between them
     run = DenseRun(fsa, B, V, dtype, churn, starts, seed)
@@ -280,6 +305,7 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
         st = run.states_now(ids)
         live = st[st >= 0]
         distinct.append(int(np.unique(live).size))
+        line_bytes.append(float(per_state[np.where(st >= 0, st, len(per_state) - 1)].sum()))
         keep = k >= warmup and len(recorded) < record_cpu
         if keep:
             raw = run.logits.cpu()
@@ -334,6 +360,7 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
         ev.destroy()
         parity &= bool(agree.item()) and torch.equal(run.batch._state.cpu(), pool_ref)
     res["distinct"] = distinct[warmup:]
+    res["line_bytes"] = line_bytes[warmup:]
     res["passes_agree"] = parity
     res["recorded"] = recorded
     return res
@@ -411,10 +438,24 @@ def bench_dense(args) -> dict:
                                   duration_us=round(t_mask * 1e3, 3)),
             two_bracket_frac=round(statistics.fmean(d_step) / (statistics.fmean(two) * 1e-3) / 1e9
                                    / PEAK_HBM_GBS, 4),
+            memory_side=_memory_side(r, U, B, V, t_step),
         ),
     }
     if r["recorded"]:
         out["cpu_baseline"], out["parity_vs_oracle"] = _dense_cpu_baseline(args, fsa, r["recorded"], B, V)
+    return out
+
+
+def _memory_side(r, U, B, V, t_step_ms) -> dict:
+    """The bytes the memory system moves for the step at 128-byte line
+    granularity (see _line_bytes_per_state), plus the allow-bit rows read
+    (V/8 per distinct state) and the commit's 16 B per row."""
+    b = [lb + u * V / 8 + 16 * B for lb, u in zip(r["line_bytes"], U)]
+    out = _roofline(statistics.fmean(b), t_step_ms * 1e-3)
+    out["bytes_per_step_mean"] = round(statistics.fmean(b), 1)
+    out["basis"] = ("per 128-byte line of logits: all rejected = one write, kept and rejected mixed "
+                    "= read + write (merged below the caches), all kept = nothing; plus the allow-bit "
+                    "rows and the commit")
     return out
 
 
@@ -550,7 +591,12 @@ def bench_schema(args) -> dict:
         "roofline": _roofline(statistics.fmean(d_step), t_step * 1e-3, traffic=None,
                               scope="apply_mask + commit step (one event bracket)",
                               algorithmic_bytes_per_step_mean=round(statistics.fmean(d_step), 1),
-                              kernel="dense_fill_kernel<2, true>"),
+                              kernel="dense_fill_kernel<2, true>",
+                              memory_side=_memory_side(r, U, B, V, t_step),
+                              note=("D charges a read and a write of every logit; the kernel writes "
+                                    "only rejected logits and reads none, and rows inside the name "
+                                    "string keep most of the vocabulary, so D/t can exceed the peak; "
+                                    "memory_side counts the bytes the memory system moves")),
         "passes_agree": r["passes_agree"],
         "parity_dense_vs_walking_kernel_every_step": agree,
     }
