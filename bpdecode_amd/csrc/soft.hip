@@ -1009,6 +1009,7 @@ __global__ __launch_bounds__(kPriorOutThreads) void prior_out_kernel(
   }
 }
 
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool force_pieces() {

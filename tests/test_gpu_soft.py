@@ -10,6 +10,7 @@ import torch
 from bpdecode_amd import ops, synth
 from bpdecode_amd.batch import ConstraintBatch
 from bpdecode_amd.ops import FsaTensors
+from bpdecode_amd.tokenizer import Vocabulary
 from oracle import soft as OS
 from tests._util import TOY_PATTERNS, TOY_VOCAB
 
@@ -69,11 +70,18 @@ def test_apply_soft(dev, dtype, alpha):
 
 
 # ------------------------------------------------------- prior-weighted --
+# The toy vocabulary with three more tokens: V = 20, a multiple of 4, so the
+# vectorised kernels apply (V = 17 takes the scalar ones).
+TOY_VOCAB20 = Vocabulary.from_tokens(list(TOY_VOCAB.token_bytes) + [b"d", b"e0", b"bb"],
+                                     eos_id=TOY_VOCAB.eos_id)
+
+
 @pytest.mark.parametrize("pattern", TOY_PATTERNS)
 @pytest.mark.parametrize("k", [1, 2, 4])
 @pytest.mark.parametrize("alpha", [0.0, 1.0, -0.5])
-def test_prior_toy(dev, pattern, k, alpha):
-    fsa = FsaTensors.build(pattern, TOY_VOCAB).densify()
+@pytest.mark.parametrize("vocab", ["v17", "v20"])
+def test_prior_toy(dev, pattern, k, alpha, vocab):
+    fsa = FsaTensors.build(pattern, TOY_VOCAB if vocab == "v17" else TOY_VOCAB20).densify()
     S, V = fsa.tok_next.shape
     st = torch.tensor(list(range(S)) + [-1, 0], dtype=torch.int32)
     g = torch.Generator().manual_seed(k * 13 + len(pattern))
@@ -85,8 +93,9 @@ def test_prior_toy(dev, pattern, k, alpha):
     assert close(got.cpu().double().numpy(), want)
 
 
-def test_prior_batch_slots_and_errors(dev):
-    fsa = FsaTensors.build("a[012]+|b0", TOY_VOCAB).densify().to(dev)
+@pytest.mark.parametrize("vocab", ["v17", "v20"])
+def test_prior_batch_slots_and_errors(dev, vocab):
+    fsa = FsaTensors.build("a[012]+|b0", TOY_VOCAB if vocab == "v17" else TOY_VOCAB20).densify().to(dev)
     S, V = fsa.tok_next.shape
     batch = ConstraintBatch(fsa, capacity=8, device=dev)
     for i in range(6):
@@ -185,12 +194,13 @@ def test_prior_pieces_path_email(dev, monkeypatch):
     assert close(b, a)
 
 
-def test_prior_wide_class_map_and_extreme_logits(dev, monkeypatch):
+@pytest.mark.parametrize("vocab", ["v17", "v20"])
+def test_prior_wide_class_map_and_extreme_logits(dev, monkeypatch, vocab):
     """The statistics read the chunk member lists, else the uint16 class map
     when it is present, else the int32 one: same results.  Rows mixing -inf,
     very negative and large logits keep every class sum exact (checked
     against the oracle)."""
-    fsa = FsaTensors.build("-?[0-9]+(\\.[0-9]+)?", TOY_VOCAB).densify()
+    fsa = FsaTensors.build("-?[0-9]+(\\.[0-9]+)?", TOY_VOCAB if vocab == "v17" else TOY_VOCAB20).densify()
     S, V = fsa.tok_next.shape
     st = torch.tensor(list(range(S)) * 2, dtype=torch.int32)
     g = torch.Generator().manual_seed(3)
@@ -217,12 +227,13 @@ def test_prior_wide_class_map_and_extreme_logits(dev, monkeypatch):
 
 
 @pytest.mark.parametrize("pattern", ["[a-c]*", "a[012]+|b0"])
-def test_prior_error_stays_near_float32_rounding(dev, pattern):
+@pytest.mark.parametrize("vocab", ["v17", "v20"])
+def test_prior_error_stays_near_float32_rounding(dev, pattern, vocab):
     """Across seeded draws the device result stays at float32 rounding level
     of the float64 oracle at k = 4: within 2e-6 + 2e-7 * max|x| per row (the
     exponentials take x - max before scaling, so a large row maximum costs
     no precision beyond the rounding of the inputs themselves)."""
-    fsa = FsaTensors.build(pattern, TOY_VOCAB).densify()
+    fsa = FsaTensors.build(pattern, TOY_VOCAB if vocab == "v17" else TOY_VOCAB20).densify()
     S, V = fsa.tok_next.shape
     fd = fsa.to(dev)
     g = torch.Generator().manual_seed(23)
