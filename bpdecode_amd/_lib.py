@@ -74,6 +74,8 @@ _SIGNATURES = {
                                          vp, vp]),
     "bpd_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, i64, vp, cint, i64, vp, cint, vp, vp]),
     "bpd_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp, vp, vp]),
+    "bpd_build_reachability": (cint, [vp, i32, i32, vp, vp, vp]),
+    "bpd_host_build_reachability": (cint, [vp, i32, i32, vp, vp]),
     "bpd_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp, vp]),
     "bpd_fsa_apply_mask": (cint, [C.POINTER(FsaTableC), vp, cint, i64, i64, vp, vp, f64, vp, vp]),
     "bpd_fsa_compute_mask": (cint, [C.POINTER(FsaTableC), vp, vp, i64, vp, vp, vp]),

@@ -18,7 +18,7 @@ import torch
 
 from . import _lib, ops
 from ._lib import check, lib
-from .ops import DENSE_AUTO_LIMIT, FsaTensors, advance_state, apply_mask_, apply_soft_
+from .ops import FsaTensors, advance_state, apply_mask_, apply_soft_
 from .tokenizer import Vocabulary
 
 FREE = -2  # slot holds no sequence
@@ -81,12 +81,9 @@ class MaskCache:
 def build_bundle(pattern, vocab: Vocabulary, device: torch.device) -> FsaTensors:
     """Grammar bundle of a regex (or DFA) on ``device`` by the reference's
     density rule (ops.py:137-139): dense when states * vocab <= 32e6, the
-    symbol-class walk above it.  The table is built where the bundle lives
-    (the table-builder kernel on the device)."""
-    fsa = FsaTensors.build(pattern, vocab, dense=False).to(device)
-    if fsa.num_states * fsa.vocab_size <= DENSE_AUTO_LIMIT:
-        fsa = fsa.densify()
-    return fsa
+    symbol-class walk above it.  The live set and the table are built where
+    the bundle lives (the device kernels on a device)."""
+    return FsaTensors.build(pattern, vocab, device=device)
 
 
 class GrammarCache:

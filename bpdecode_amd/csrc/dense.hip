@@ -288,6 +288,44 @@ __global__ __launch_bounds__(256) void build_tok_next_kernel(
   out[int64_t(r) * vocab + t] = res;
 }
 
+// Reachability (the live set of a DFA): live[s] = 1 iff an accepting state
+// is reachable from s.  One workgroup sweeps the states in place over LDS
+// flags until a sweep changes nothing (monotone, so at most num_states + 1
+// sweeps); the flag is read by every thread between two barriers, so every
+// wave takes the same exit.
+constexpr int kReachThreads = 1024;
+constexpr int kReachMaxStates = 65536;  // LDS flags
+
+__global__ __launch_bounds__(kReachThreads) void reachability_kernel(
+    const int32_t* __restrict__ trans, int32_t num_states, int32_t num_symbols,
+    const uint8_t* __restrict__ accept, uint8_t* __restrict__ live_out) {
+  __shared__ uint8_t live[kReachMaxStates];
+  __shared__ int changed;
+  const int tid = threadIdx.x;
+  for (int32_t s = tid; s < num_states; s += kReachThreads) live[s] = accept[s] ? 1 : 0;
+  for (int32_t sweep = 0; sweep <= num_states; ++sweep) {
+    if (tid == 0) changed = 0;
+    __syncthreads();
+    for (int32_t s = tid; s < num_states; s += kReachThreads) {
+      if (live[s]) continue;
+      const int32_t* row = trans + int64_t(s) * num_symbols;
+      for (int32_t k = 0; k < num_symbols; ++k) {
+        const int32_t t = row[k];
+        if (t >= 0 && t < num_states && live[t]) {
+          live[s] = 1;
+          changed = 1;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    const int more = changed;
+    __syncthreads();  // every thread has read the flag before it is reset
+    if (!more) break;
+  }
+  for (int32_t s = tid; s < num_states; s += kReachThreads) live_out[s] = live[s];
+}
+
 }  // namespace
 }  // namespace bpd
 
@@ -431,6 +469,18 @@ extern "C" int bpd_build_tok_next(const int32_t* trans, int32_t num_states, int3
   build_tok_next_kernel<<<grid, 256, 0, as_stream(stream)>>>(
       trans, num_states, num_symbols, dead, accept, live, tok_offsets, tok_symbols, vocab,
       eos_id, row_states, num_rows, out);
+  BPD_LAUNCHED();
+  return BPD_OK;
+}
+
+extern "C" int bpd_build_reachability(const int32_t* trans, int32_t num_states, int32_t num_symbols,
+                                      const uint8_t* accept, uint8_t* live, void* stream) {
+  BPD_REQUIRE(num_states >= 0 && num_symbols > 0, "bad table shape");
+  BPD_REQUIRE(num_states <= kReachMaxStates, "at most %d states on the device", kReachMaxStates);
+  if (num_states == 0) return BPD_OK;
+  BPD_REQUIRE(trans && accept && live, "null pointer argument");
+  reachability_kernel<<<1, kReachThreads, 0, as_stream(stream)>>>(trans, num_states, num_symbols,
+                                                                   accept, live);
   BPD_LAUNCHED();
   return BPD_OK;
 }

@@ -165,3 +165,41 @@ extern "C" int bpd_host_build_tok_next(const int32_t* trans, int32_t num_states,
   }
   return BPD_OK;
 }
+
+extern "C" int bpd_host_build_reachability(const int32_t* trans, int32_t num_states,
+                                           int32_t num_symbols, const uint8_t* accept,
+                                           uint8_t* live) {
+  BPD_REQUIRE(num_states >= 0 && num_symbols > 0, "bad table shape");
+  if (num_states == 0) return BPD_OK;
+  BPD_REQUIRE(trans && accept && live, "null pointer argument");
+  // reverse edges (CSR), then a breadth-first search back from the accepting states
+  std::vector<int32_t> cnt(size_t(num_states) + 1, 0);
+  const int64_t nt = int64_t(num_states) * num_symbols;
+  for (int64_t i = 0; i < nt; ++i) {
+    const int32_t t = trans[i];
+    if (t >= 0 && t < num_states) ++cnt[size_t(t) + 1];
+  }
+  for (int32_t s = 0; s < num_states; ++s) cnt[size_t(s) + 1] += cnt[size_t(s)];
+  std::vector<int32_t> pred(static_cast<size_t>(cnt[static_cast<size_t>(num_states)]));
+  std::vector<int32_t> fill(cnt.begin(), cnt.end() - 1);
+  for (int64_t i = 0; i < nt; ++i) {
+    const int32_t t = trans[i];
+    if (t >= 0 && t < num_states) pred[size_t(fill[size_t(t)]++)] = int32_t(i / num_symbols);
+  }
+  std::vector<int32_t> todo;
+  for (int32_t s = 0; s < num_states; ++s) {
+    live[s] = accept[s] ? 1 : 0;
+    if (live[s]) todo.push_back(s);
+  }
+  for (size_t h = 0; h < todo.size(); ++h) {
+    const int32_t t = todo[h];
+    for (int32_t j = cnt[size_t(t)]; j < cnt[size_t(t) + 1]; ++j) {
+      const int32_t p = pred[size_t(j)];
+      if (!live[p]) {
+        live[p] = 1;
+        todo.push_back(p);
+      }
+    }
+  }
+  return BPD_OK;
+}

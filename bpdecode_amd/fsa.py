@@ -61,7 +61,9 @@ def build_reachability(num_states, num_symbols, trans, accept) -> list[int]:
     return live
 
 
-def fsa_from_dfa(dfa: DFA) -> FsaTable:
+def fsa_from_dfa(dfa: DFA, with_live: bool = True) -> FsaTable:
+    """The DFA as flat tables; ``with_live=False`` leaves ``live`` empty for
+    a builder that computes it elsewhere (the device)."""
     n = len(dfa.trans)
     m = len(dfa.symbols)
     flat = tuple(t for row in dfa.trans for t in row)
@@ -73,7 +75,7 @@ def fsa_from_dfa(dfa: DFA) -> FsaTable:
         dead=dfa.dead,
         trans=flat,
         accept=accept,
-        live=tuple(build_reachability(n, m, flat, accept)),
+        live=tuple(build_reachability(n, m, flat, accept)) if with_live else (),
         symbols=tuple(dfa.symbols),
     )
 

@@ -253,9 +253,20 @@ class FsaTensors:
         )
 
     @classmethod
-    def build(cls, pattern: str | DFA, vocab: Vocabulary, *, dense: bool | str = "auto") -> FsaTensors:
+    def build(cls, pattern: str | DFA, vocab: Vocabulary, *, dense: bool | str = "auto",
+              device=None) -> FsaTensors:
+        """Compile ``pattern`` for ``vocab`` (ops.py:127-140).  With a device,
+        the tables go there first and the live set and the dense table are
+        built by the device kernels."""
         dfa = pattern if isinstance(pattern, DFA) else compile_regex(pattern)
-        fsa = cls.from_tables(fsa_from_dfa(dfa), token_symbols(dfa, vocab))
+        dev = torch.device(device) if device is not None else torch.device("cpu")
+        on_dev = dev.type == "cuda"
+        fsa = cls.from_tables(fsa_from_dfa(dfa, with_live=not on_dev), token_symbols(dfa, vocab))
+        if on_dev:
+            fsa = fsa.to(dev)
+            fsa = replace(fsa, live=build_reachability(fsa.trans, fsa.accept, fsa.num_symbols))
+        elif dev.type != "cpu":
+            fsa = fsa.to(dev)
         want = dense is True or (dense == "auto" and fsa.num_states * fsa.vocab_size <= DENSE_AUTO_LIMIT)
         return fsa.densify() if want else fsa
 
@@ -287,6 +298,26 @@ def _symbols_u8(fsa: FsaTensors) -> torch.Tensor:
     if sym.numel() and (int(sym.min()) < 0 or int(sym.max()) > 255):
         raise RuntimeError("symbol-class ids must lie in [0, 255]")
     return sym.to(torch.uint8).contiguous() if sym.numel() else torch.zeros(1, dtype=torch.uint8, device=sym.device)
+
+
+def build_reachability(trans: torch.Tensor, accept: torch.Tensor, num_symbols: int) -> torch.Tensor:
+    """``live`` (uint8, on the tables' device): 1 where an accepting state is
+    reachable (fsa.py:70-104); the reachability kernel on the device, the
+    library's reverse search on the host."""
+    tr = _i32(trans)
+    ac = accept.to(torch.uint8).contiguous()
+    S = int(ac.numel())
+    if S and tr.numel() != S * int(num_symbols):
+        raise RuntimeError("trans must hold num_states * num_symbols entries")
+    live = torch.empty(S, dtype=torch.uint8, device=tr.device)
+    if S == 0:
+        return live
+    if tr.device.type == "cuda":
+        check(lib().bpd_build_reachability(ptr(tr), S, int(num_symbols), ptr(ac), ptr(live),
+                                           _lib.stream_of(tr.device)))
+    else:
+        check(lib().bpd_host_build_reachability(ptr(tr), S, int(num_symbols), ptr(ac), ptr(live)))
+    return live
 
 
 def build_token_transitions(fsa: FsaTensors, rows=None) -> torch.Tensor:

@@ -17,7 +17,6 @@ import torch
 
 from . import ops
 from ._lib import PDA_CONFIG_WORDS
-from .fsa import build_reachability as _reachability
 from .grammar import device as _gdev
 
 _SCHEMAS = (
@@ -115,10 +114,9 @@ def _pda_check_configs(configs: torch.Tensor) -> None:
 
 # --- FSA ops (torch_ops.cpp:95-229) --------------------------------------------
 def build_reachability(trans, accept, num_symbols):
-    tr = trans.to("cpu", torch.int32).contiguous()
-    ac = accept.to("cpu", torch.uint8).contiguous()
-    live = _reachability(int(ac.numel()), int(num_symbols), tr.tolist(), ac.tolist())
-    return torch.tensor(live, dtype=torch.uint8)
+    """torch_ops.cpp:95-107 (host only there); device tensors run the
+    reachability kernel."""
+    return ops.build_reachability(trans, accept, int(num_symbols))
 
 
 def apply_mask_(logits, trans, accept, live, num_symbols, dead, offsets, symbols, eos_id, states,

@@ -133,6 +133,17 @@ int bpd_build_tok_next(const int32_t* trans, int32_t num_states, int32_t num_sym
                        int64_t vocab, int32_t eos_id, const int32_t* row_states,
                        int32_t num_rows, int32_t* out, void* stream);
 
+/* bpd_build_reachability: live[s] = 1 iff an accepting state is reachable
+ * from s through trans ([num_states * num_symbols], targets outside
+ * [0, num_states) ignored); device pointers, at most 65536 states.  The
+ * reference's build_reachability (fsa.py:70-104, the torch op of
+ * torch_ops.cpp:95-107) and its sweep kernel (mask_cuda.cu:84-103, which its
+ * op never reaches); bpd_host_build_reachability is the host form. */
+int bpd_build_reachability(const int32_t* trans, int32_t num_states, int32_t num_symbols,
+                           const uint8_t* accept, uint8_t* live, void* stream);
+int bpd_host_build_reachability(const int32_t* trans, int32_t num_states, int32_t num_symbols,
+                                const uint8_t* accept, uint8_t* live);
+
 /* Symbol-class FSA walked per token on the device, without a tok_next table
  * (grammars too large to densify).  The reference's FsaTable + TokenSymbols
  * (mask.hpp:18-38) with the symbol classes narrowed to uint8.  The verdict

@@ -381,3 +381,36 @@ def test_toy_patterns_all_states(dev, pattern):
     got2 = lg.to(dev)
     ops.apply_mask_(got2, fsa.to(dev).densify(), st.to(dev))
     assert torch.equal(got2.cpu(), want)
+
+
+@pytest.mark.parametrize("S,M,seed", [(1, 1, 0), (5, 2, 1), (300, 7, 3), (5000, 5, 4), (20000, 3, 5)])
+def test_device_reachability_matches_host(dev, S, M, seed):
+    """The reachability kernel against the library's host reverse search on
+    random tables with sinks and unreachable accepting states."""
+    rng = np.random.default_rng(seed)
+    trans = rng.integers(0, S, size=(S, M)).astype(np.int32)
+    accept = (rng.random(S) < 0.05).astype(np.uint8)
+    for s in rng.choice(S, size=max(1, S // 4), replace=False):
+        trans[s] = s
+    host = ops.build_reachability(torch.from_numpy(trans.reshape(-1)), torch.from_numpy(accept), M)
+    got = ops.build_reachability(torch.from_numpy(trans.reshape(-1)).to(dev), torch.from_numpy(accept).to(dev), M)
+    assert torch.equal(got.cpu(), host)
+    assert 0 < int(host.sum()) < S or S == 1
+
+
+def test_device_built_bundles_equal_host_built(dev, serving_vocab):
+    """FsaTensors.build(..., device=cuda) builds the live set and the dense
+    table with the device kernels: the same tables as the host build, for
+    the email regex (dense) and the flat JSON-Schema DFA (above the auto
+    limit: live set only)."""
+    _log("case device-built bundles")
+    host = FsaTensors.build(synth.EMAIL, serving_vocab)
+    devb = FsaTensors.build(synth.EMAIL, serving_vocab, device=dev)
+    assert devb.device.type == "cuda" and devb.tok_next is not None
+    assert torch.equal(devb.live.cpu(), host.live) and torch.equal(devb.tok_next.cpu(), host.tok_next)
+    comp = CompiledGrammar.build(json_schema_to_grammar(synth.FLAT_SCHEMA))
+    dfa = residual_dfa(comp, comp.root, comp.rules[comp.root].start)
+    h2 = FsaTensors.build(dfa, serving_vocab)
+    d2 = FsaTensors.build(dfa, serving_vocab, device=dev)
+    assert h2.tok_next is None and d2.tok_next is None
+    assert torch.equal(d2.live.cpu(), h2.live) and torch.equal(d2.trans.cpu(), h2.trans)

@@ -284,3 +284,29 @@ def test_dense_oracle_matches_aten_sequence(dtype, neg_inf):
     nxt = torch.from_numpy(tn)[s.clamp(min=0), torch.from_numpy(toks_).long()]
     want_adv = torch.where(s < 0, torch.full_like(nxt, -1), nxt).to(torch.int32)
     assert OD.advance(tn, states, toks_).tolist() == want_adv.tolist()
+
+
+def _random_dfa_table(rng, S, M):
+    """Random transition table with absorbing sinks and an unreachable
+    accepting cycle, so both live and dead states occur."""
+    trans = rng.integers(0, S, size=(S, M)).astype(np.int32)
+    accept = (rng.random(S) < 0.15).astype(np.uint8)
+    for s in rng.choice(S, size=max(1, S // 5), replace=False):
+        trans[s] = s  # absorbing
+    return trans.reshape(-1), accept
+
+
+@need_ref
+@pytest.mark.parametrize("S,M,seed", [(1, 1, 0), (4, 2, 1), (37, 3, 2), (300, 7, 3), (2500, 4, 4)])
+def test_host_reachability_matches_reference(S, M, seed):
+    """The library's host reachability (reverse search) against the
+    reference's own build_reachability compiled from mask_cpu.cpp, and the
+    Python front-end's, on random tables."""
+    from bpdecode_amd import ops
+    from bpdecode_amd.fsa import build_reachability
+
+    trans, accept = _random_dfa_table(np.random.default_rng(seed), S, M)
+    want = R.fsa_build_reachability(trans, accept, M)
+    got = ops.build_reachability(torch.from_numpy(trans), torch.from_numpy(accept), M)
+    assert got.numpy().tolist() == want.tolist()
+    assert build_reachability(S, M, trans.tolist(), accept.tolist()) == want.tolist()
