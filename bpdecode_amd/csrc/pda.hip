@@ -48,6 +48,8 @@ struct MaskArgs {
   int32_t* err;
   const int32_t* only_rows;  // non-null: process only rows b with only_rows[b] != 0
   const int32_t* order;      // memo walk order (null: id order)
+  const int32_t* runs;       // first-byte runs of order (null: none)
+  BpdPdaFrames frames;       // num_lists 0: no frame lists
 };
 
 // Structural check of a row's config-set before any table lookup with its
@@ -605,6 +607,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail, loop_n;
   __shared__ uint32_t h0_sh;
   __shared__ uint8_t loop0[256];  // T[0][c] == 0: byte c keeps set 0 (row-wide walk)
+  // first pass of the row-wide walk: pass index i -> walk position
+  __shared__ int32_t grp_pre[258];    // runs: exclusive prefix of the live runs' lengths
+  __shared__ int32_t grp_start[257];  // runs: first walk position of each run
+  __shared__ int pass_mode, pass_list, pass_total, pass_base;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
   const int tid = threadIdx.x;
@@ -957,36 +963,135 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       qcount = 0;
       row_fail = 0;
       loop_n = 0;
+      pass_mode = 0;
+      pass_list = -1;
+      pass_total = dead_row ? 0 : int(V);  // a dead row rejects every token: nothing to walk
+      pass_base = 0;
     }
     __syncthreads();
     if (tid < 256) {
       loop0[tid] = T[tid] == 0 ? 1 : 0;
       if (T[tid] == 0) atomicAdd(&loop_n, 1);
     }
+    // Frame lists: a row whose configs share one stack below their tops
+    // (depth >= 2) and whose ordered tops are a list's key takes the tokens
+    // that stay inside the tops' call-free rule from the list's bitmap and
+    // walks only the list's seeds (the tokens that reach the rule's accept
+    // state, EOS and the empty tokens).
+    if (tid < kWave && !dead_row && !overflowed && a.frames.num_lists > 0) {
+      const int n = row_cfg[0];
+      const int d0 = n >= 1 ? row_cfg[2] : 0;
+      bool same = n >= 1 && d0 >= 2;
+      if (same) {
+        bool bad = tid < n && row_cfg[2 + tid] != d0;
+        for (int f = tid; f < n * kMaxDepth; f += kWave) {
+          const int i = f / kMaxDepth, k = f % kMaxDepth;
+          if (k < d0 - 1 && row_cfg[kF + i * kMaxDepth + k] != row_cfg[kF + k]) bad = true;
+        }
+        same = __ballot(bad) == 0;
+      }
+      if (same) {
+        bool hit = false;
+        if (tid < a.frames.num_lists) {
+          const int32_t* key = a.frames.keys + tid * BPD_PDA_FRAME_KEY_WORDS;
+          hit = key[0] == n;
+          for (int i = 0; i < n && hit; ++i) hit = key[1 + i] == row_cfg[kF + i * kMaxDepth + d0 - 1];
+        }
+        const uint64_t m = __ballot(hit);
+        if (m != 0u && tid == 0) {
+          const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
+          const int32_t s0 = a.frames.seed_off[l], s1 = a.frames.seed_off[l + 1];
+          pass_list = l;
+          pass_mode = 2;
+          pass_base = s0;
+          pass_total = s1 > s0 ? s1 - s0 : 0;
+        }
+      }
+    }
+    __syncthreads();
+    if (pass_list >= 0) {  // (pass_mode is written below; pass_list is not)
+      const uint32_t* al = a.frames.allowed + int64_t(pass_list) * a.frames.words;
+      for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = al[i];
+    } else if (a.runs && !dead_row && !overflowed && tid < kWave) {
+      // first-byte runs: the run of byte c is walked unless the byte
+      // empties set 0 (T[0][c] dead); lane l owns runs 4l..4l+3, lane 63
+      // also the run of EOS and the empty tokens
+      int cnt[4], st[4], sum = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = 4 * tid + q;
+        const int64_t b0 = a.runs[c], b1 = c < 255 ? a.runs[c + 1] : a.runs[256];
+        const int64_t lo = b0 < 0 ? 0 : (b0 > V ? V : b0);
+        const int64_t hi = b1 < lo ? lo : (b1 > V ? V : b1);
+        st[q] = int(lo);
+        cnt[q] = T[c] == kTDead ? 0 : int(hi - lo);
+        sum += cnt[q];
+      }
+      int incl = sum;
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (tid >= o) incl += y;
+      }
+      int ex = incl - sum;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        grp_pre[4 * tid + q] = ex;
+        grp_start[4 * tid + q] = st[q];
+        ex += cnt[q];
+      }
+      if (tid == kWave - 1) {
+        const int64_t b0 = a.runs[256];
+        const int64_t lo = b0 < 0 ? 0 : (b0 > V ? V : b0);
+        grp_pre[256] = incl;
+        grp_start[256] = int(lo);
+        grp_pre[257] = incl + int(V - lo);
+        pass_total = incl + int(V - lo);
+        pass_mode = 1;
+      }
+    }
     __syncthreads();
     // only a set that keeps itself on many bytes (a string or comment loop)
     // is worth the prefix check below
     const bool scan = loop_n >= 32;
+    const int mode = pass_mode;
+    const int64_t P = pass_total;
+    // walk position of pass index i (< P); -1 for a seed out of range
+    auto pass_pos = [&](int64_t i) -> int32_t {
+      if (mode == 0) return int32_t(i);
+      if (mode == 2) {
+        const int32_t k = a.frames.seeds[pass_base + i];
+        return k >= 0 && k < V ? k : -1;
+      }
+      int lo = 0, hi = 256;  // the last run whose prefix is <= i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (grp_pre[mid] <= i) lo = mid; else hi = mid - 1;
+      }
+      return grp_start[lo] + int32_t(i - grp_pre[lo]);
+    };
     if (!overflowed) {
       // the records of the next tile are loaded while this one is walked;
       // queue entries are stored after all four walks of a tile
       constexpr int64_t kTile = int64_t(kMemoThreads) * kMemoTok;
       int2 nm[kMemoTok];
       uint4 npk[kMemoTok];
+      int32_t nk[kMemoTok];
 #pragma unroll
       for (int j = 0; j < kMemoTok; ++j) {
-        const int64_t k = int64_t(j) * kMemoThreads + tid;
-        nm[j] = k < V ? ws.tmeta[k] : make_int2(-1, 0);
-        npk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+        const int64_t i = int64_t(j) * kMemoThreads + tid;
+        nk[j] = i < P ? pass_pos(i) : -1;
+        nm[j] = nk[j] >= 0 ? ws.tmeta[nk[j]] : make_int2(-1, 0);
+        npk[j] = nk[j] >= 0 ? ws.recs[nk[j]] : make_uint4(0u, 0u, 0u, 0u);
       }
-      for (int64_t tile = 0; tile < V; tile += kTile) {
-        int32_t tt[kMemoTok], pos[kMemoTok], len[kMemoTok];
+      for (int64_t tile = 0; tile < P; tile += kTile) {
+        int32_t tt[kMemoTok], pos[kMemoTok], len[kMemoTok], kk[kMemoTok];
         int cur[kMemoTok];
         uint4 pk[kMemoTok];
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
           const int2 m = nm[j];
           pk[j] = npk[j];
+          kk[j] = nk[j];
           const int32_t t = m.x;
           tt[j] = t;
           pos[j] = len[j] = 0;
@@ -1003,9 +1108,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
-          const int64_t k = tile + kTile + int64_t(j) * kMemoThreads + tid;
-          nm[j] = k < V ? ws.tmeta[k] : make_int2(-1, 0);
-          npk[j] = k < V ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+          const int64_t i = tile + kTile + int64_t(j) * kMemoThreads + tid;
+          nk[j] = i < P ? pass_pos(i) : -1;
+          nm[j] = nk[j] >= 0 ? ws.tmeta[nk[j]] : make_int2(-1, 0);
+          npk[j] = nk[j] >= 0 ? ws.recs[nk[j]] : make_uint4(0u, 0u, 0u, 0u);
         }
         // the leading bytes that keep set 0 (a string loop's body) are
         // checked together, with independent table reads, and the walk
@@ -1025,8 +1131,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) paused[j] = walk(cur[j], pos[j], len[j], pk[j], tt[j]);
 #pragma unroll
-        for (int j = 0; j < kMemoTok; ++j)
-          settle(paused[j], cur[j], pos[j], len[j], int32_t(tile + int64_t(j) * kMemoThreads + tid), tt[j], qin);
+        for (int j = 0; j < kMemoTok; ++j) settle(paused[j], cur[j], pos[j], len[j], kk[j], tt[j], qin);
       }
     }
     __syncthreads();
@@ -1305,42 +1410,36 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
     const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
     ok = true;
     if (s < e) {
-      // set reached after all bytes but the last, via the mask's table
-      int cur = -1;  // -1: use the direct walk
+      // walk the mask's table over the bytes but the last while it has the
+      // entries; then step the rest (at least the last byte) with
+      // advance_byte from the interned set reached, so the written
+      // config-set has the raw words of the direct walk
+      int cur = -1;  // -1: no usable table, step every byte from the row's set
+      int32_t i = s;
       const int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
       if (ws.pool && ws.meta[b * 4] == 1 && ws.meta[b * 4 + 1] == int32_t(uint32_t(tag)) &&
           ws.meta[b * 4 + 2] == int32_t(uint32_t(tag >> 32)) &&
           uint32_t(ws.meta[b * 4 + 3]) == ws.header[0] && coop_same(x, pool, lane)) {
         const uint8_t* T = reinterpret_cast<const uint8_t*>(ws.table + b * (kMemoSets * 64));
         cur = 0;
-        for (int32_t i = s; i + 1 < e; ++i) {
+        for (; i + 1 < e; ++i) {
           const uint8_t nx = T[cur * 256 + a.tok_bytes[i]];
           if (nx == kTDead) {
             cur = -2;
             break;
           }
-          if (nx >= kTOverflow) {
-            cur = -1;
-            break;
-          }
+          if (nx >= kTOverflow) break;  // not resolved by the mask: step from here
           cur = nx;
         }
       }
       if (cur == -2) {
         ok = false;
-      } else if (cur >= 0) {
-        const int32_t* src = cur == 0 ? x : pool + cur * kConfigWords;
-        if (cur != 0) {
-          for (int k = lane; k < kConfigWords; k += kWave) y[k] = src[k];
-          wave_sync();
-          for (int k = lane; k < kConfigWords; k += kWave) x[k] = y[k];
+      } else {
+        if (cur > 0) {
+          for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[cur * kConfigWords + k];
           wave_sync();
         }
-        ok = coop_advance_byte(a.g, x, y, a.tok_bytes[e - 1], lane);
-        if (ok)
-          for (int k = lane; k < kConfigWords; k += kWave) cfg[k] = y[k];
-      } else {
-        for (int32_t i = s; i < e && ok; ++i) {
+        for (; i < e && ok; ++i) {
           ok = coop_advance_byte(a.g, x, y, a.tok_bytes[i], lane);
           int32_t* tmp = x;
           x = y;
@@ -1482,6 +1581,18 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
   a.err = nullptr;
   a.only_rows = nullptr;
   a.order = toks->order;
+  a.runs = toks->order ? toks->runs : nullptr;
+  a.frames = BpdPdaFrames{};
+  if (const BpdPdaFrames* f = toks->frames) {
+    BPD_REQUIRE(f->num_lists >= 0 && f->num_lists <= BPD_PDA_MAX_FRAME_LISTS,
+                "frame lists: num_lists %d outside [0, %d]", f->num_lists, BPD_PDA_MAX_FRAME_LISTS);
+    if (f->num_lists > 0) {
+      BPD_REQUIRE(f->words == (toks->vocab_size + 31) / 32, "frame lists: words %d for vocab %d",
+                  f->words, toks->vocab_size);
+      BPD_REQUIRE(f->keys && f->allowed && f->seed_off && f->seeds, "frame lists: null array");
+      a.frames = *f;
+    }
+  }
   if (workspace && toks->vocab_size <= kMemoMaxVocab) {
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);

@@ -18,37 +18,50 @@ nested JSON under the 8-configuration cap.
 
 from __future__ import annotations
 
+import ctypes as C
 from collections.abc import Hashable, Sequence
 from dataclasses import dataclass, field, replace
 
+import numpy as np
 import torch
 
 from .. import _lib
 from .._lib import PDA_CONFIG_WORDS, PDA_MAX_CONFIGS, PDA_MAX_DEPTH, check, lib, ptr
 from ..tokenizer import Vocabulary
 from .nfa import RuleNFA
+from .frames import frame_lists
 from .pda import CompiledGrammar, coreachable_sets, rule_nonempty
 
 PDA_CONFIG_FLAT = PDA_CONFIG_WORDS
 _EPS, _BYTE, _CALL = 0, 1, 2
 
 
-def _walk_order(off: torch.Tensor, tb: torch.Tensor, vocab: int) -> torch.Tensor:
-    """Walk order of the memoised device mask: token ids by byte length, then
-    by their first 16 bytes.  Consecutive lanes of a wave take consecutive
-    positions, so they walk equally long tokens that share prefixes: they
-    reach the same table entries and leave the walk together."""
-    import numpy as np
+def _walk_order(off: torch.Tensor, tb: torch.Tensor, vocab: int, eos_id: int):
+    """Walk order of the memoised device mask and its first-byte runs.
 
+    Tokens are ordered by first byte, then byte length, then their next 15
+    bytes; EOS and empty tokens come last (group 256).  Consecutive lanes of
+    a wave take consecutive positions, so they walk equally long tokens that
+    share prefixes: they reach the same table entries and leave the walk
+    together.  ``runs[c]`` is the first position of group ``c`` (257
+    entries; group 256 ends at ``vocab``), so a row skips at once every
+    group whose first byte empties its config-set."""
     o = off.cpu().numpy().astype(np.int64)
     b = tb.cpu().numpy()
     start, length = o[:vocab], o[1 : vocab + 1] - o[:vocab]
+    lead = b[np.minimum(start, max(b.size - 1, 0))].astype(np.int64) if b.size else np.zeros(vocab, np.int64)
+    group = np.where(length > 0, lead, 256).astype(np.int64)
+    if 0 <= eos_id < vocab:
+        group[eos_id] = 256
     keys = []
-    for i in range(15, -1, -1):
+    for i in range(15, 0, -1):
         idx = np.minimum(start + i, max(b.size - 1, 0))
         keys.append(np.where(i < length, b[idx] if b.size else 0, 0).astype(np.int16))
-    keys.append(length)  # primary key last
-    return torch.from_numpy(np.lexsort(keys).astype(np.int32))
+    keys.append(length)
+    keys.append(group)  # primary key last
+    order = np.lexsort(keys).astype(np.int32)
+    runs = np.searchsorted(group[order], np.arange(257), side="left").astype(np.int32)
+    return torch.from_numpy(order), torch.from_numpy(runs)
 
 
 @dataclass
@@ -68,6 +81,9 @@ class PdaTensors:
     tok_bytes: torch.Tensor  # uint8 [tok_offsets[-1]]
     vocab_size: int
     eos_id: int
+    # per rule in flattening order: (first state, states, start, accept,
+    # has call edges, is the root rule); host metadata of the frame lists
+    rules: tuple = ()
     _c: dict = field(default_factory=dict, repr=False, compare=False)
 
     _TENSORS = ("accept", "live", "edge_offsets", "edge_kind", "edge_lo", "edge_hi",
@@ -137,16 +153,31 @@ class PdaTensors:
         return ws, need
 
     def c_tokens(self) -> _lib.TokenBytesC:
+        """Token tables of the device mask: bytes, the walk order, its
+        first-byte runs and the frame lists of the call-free rules."""
         t = self._c.get("tokens")
         if t is None:
             off = self.tok_offsets.contiguous()
             tb = self.tok_bytes.contiguous()
             if tb.numel() == 0:
                 tb = torch.zeros(1, dtype=torch.uint8, device=self.device)
-            order = _walk_order(off, tb, self.vocab_size).to(off.device)
-            t = _lib.TokenBytesC(self.vocab_size, self.eos_id, ptr(off), ptr(tb), ptr(order))
+            order, runs = _walk_order(off, tb, self.vocab_size, self.eos_id)
+            keep = [off, tb, order.to(off.device), runs.to(off.device)]
+            frames = None
+            fl = frame_lists(self, order.numpy())
+            if fl is not None and fl.num_lists > 0:
+                dev = off.device
+                arrs = [torch.from_numpy(fl.keys).to(dev), torch.from_numpy(fl.allowed.view("<i4")).to(dev),
+                        torch.from_numpy(fl.seed_off).to(dev),
+                        torch.from_numpy(fl.seeds if fl.seeds.size else np.zeros(1, np.int32)).to(dev)]
+                keep += arrs
+                frames = _lib.PdaFramesC(fl.num_lists, fl.allowed.shape[1], *(ptr(a) for a in arrs))
+                self._c["frames"] = frames
+                self._c["frame_lists"] = fl
+            t = _lib.TokenBytesC(self.vocab_size, self.eos_id, ptr(off), ptr(tb), ptr(keep[2]), ptr(keep[3]),
+                                 C.pointer(frames) if frames is not None else None)
             self._c["tokens"] = t
-            self._c["tokens_keep"] = (off, tb, order)
+            self._c["tokens_keep"] = keep
         return t
 
     def init_config(self) -> torch.Tensor:
@@ -250,6 +281,11 @@ def build_pda_tensors(compiled: CompiledGrammar, vocab: Vocabulary, device="cpu"
                 callee_l.append(row[4])
     offsets[total] = len(kind)
     root = compiled.rules[compiled.root]
+    rules = tuple(
+        (base[n], compiled.rules[n].num_states, compiled.rules[n].start, compiled.rules[n].accept,
+         any(lbl is not None and lbl[0] == "call" for s in range(compiled.rules[n].num_states)
+             for lbl, _ in compiled.rules[n].out(s)), n == compiled.root)
+        for n in names)
     raw, tok_offsets = vocab.packed
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32)  # noqa: E731
     g = PdaTensors(
@@ -268,6 +304,7 @@ def build_pda_tensors(compiled: CompiledGrammar, vocab: Vocabulary, device="cpu"
         tok_bytes=torch.frombuffer(bytearray(raw or b"\0"), dtype=torch.uint8)[: len(raw)].clone(),
         vocab_size=vocab.size,
         eos_id=vocab.eos_id if vocab.eos_id is not None else -1,
+        rules=rules,
     )
     g._validate()
     return g.to(device)

@@ -221,6 +221,28 @@ typedef struct BpdPdaTable {
   const int32_t* edge_callee;  /* [num_edges] */
 } BpdPdaTable;
 
+/* Frame lists of the device mask's fast path (no counterpart in the
+ * reference: an acceleration of pda_try_token, pda.hpp:248-258).  A row
+ * whose configs all share one stack below their top frames, at depth >= 2,
+ * with the ordered top states equal to keys[l][1..n] (n = keys[l][0]), takes
+ * its verdicts from allowed[l] (bit t of word t / 32: the token stays inside
+ * the tops' call-free rule without reaching its accept state and keeps the
+ * set non-empty) and walks only the tokens at walk positions
+ * seeds[seed_off[l] .. seed_off[l + 1]) (every other token not in allowed[l]
+ * is rejected).  Built by grammar/frames.py for the default walk order: the
+ * device trusts the contents (seed_off non-decreasing within the seeds
+ * array; wrong lists give wrong verdicts). */
+#define BPD_PDA_MAX_FRAME_LISTS 64
+#define BPD_PDA_FRAME_KEY_WORDS 9
+typedef struct BpdPdaFrames {
+  int32_t num_lists;       /* 0 .. BPD_PDA_MAX_FRAME_LISTS */
+  int32_t words;           /* (vocab_size + 31) / 32 */
+  const int32_t* keys;     /* [num_lists, BPD_PDA_FRAME_KEY_WORDS]; unused tops -1 */
+  const uint32_t* allowed; /* [num_lists, words] */
+  const int32_t* seed_off; /* [num_lists + 1] */
+  const int32_t* seeds;    /* [seed_off[num_lists]] walk positions */
+} BpdPdaFrames;
+
 typedef struct BpdTokenBytes {
   int32_t vocab_size;
   int32_t eos_id;
@@ -229,8 +251,17 @@ typedef struct BpdTokenBytes {
   /* optional (NULL = id order): a permutation of the token ids; the
    * memoised device mask walks tokens in this order, consecutive lanes of a
    * wave at consecutive positions (any permutation gives the same verdicts;
-   * by length, then bytes, lanes walk similar tokens) */
+   * by first byte, length, then bytes, lanes walk similar tokens) */
   const int32_t* order;
+  /* optional (NULL = none; ignored without `order`): [257] first-byte runs
+   * of `order`: walk positions [runs[c], runs[c + 1]) hold exactly the
+   * tokens of first byte c (c < 256; the run of c = 255 ends at runs[256]),
+   * [runs[256], vocab_size) the EOS token and the empty tokens.  The device
+   * mask skips the run of every byte that empties a row's config-set. */
+  const int32_t* runs;
+  /* optional (NULL = none): frame lists for `order` (device pointers inside
+   * a host struct) */
+  const BpdPdaFrames* frames;
 } BpdTokenBytes;
 
 /* bpd_pda_init: the closed initial config-set (pda.hpp:200-207), host only,

@@ -243,7 +243,7 @@ def test_json_walk_orders_give_the_same_masks(dev, json_case, which):
     default = gd.c_tokens()  # builds the default order
     from bpdecode_amd.grammar.device import _walk_order
 
-    base = _walk_order(gd.tok_offsets, gd.tok_bytes, gd.vocab_size)
+    base, _ = _walk_order(gd.tok_offsets, gd.tok_bytes, gd.vocab_size, gd.eos_id)
     perm = torch.from_numpy(np.random.default_rng(9).permutation(gd.vocab_size))
     assert default is not None
     assert np.array_equal(pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32), want)

@@ -264,20 +264,111 @@ def test_logits_processor_device_backend_matches_cpu_backend():
         input_ids = torch.cat([input_ids, torch.tensor(toks).unsqueeze(1)], dim=1)
 
 
-def test_memo_walk_order_is_a_permutation_by_length_then_bytes():
-    # tokens of every length class, duplicates, an empty token and tokens
-    # longer than the 16 bytes the order looks at
+def test_memo_walk_order_is_a_permutation_by_first_byte_length_then_bytes():
+    # tokens of every length class, duplicates, empty tokens, an EOS token
+    # with bytes, and tokens longer than the 16 bytes the order looks at
     rng = random.Random(3)
-    toks = [b"", b"b", b"a", b"ab", b"ab", b"aa", b"x" * 20 + b"b", b"x" * 20 + b"a"]
+    toks = [b"", b"b", b"a", b"ab", b"ab", b"aa", b"x" * 20 + b"b", b"x" * 20 + b"a", b"</s>", b""]
     toks += [bytes(rng.choice(b"ab\"[]{}") for _ in range(rng.randint(1, 24))) for _ in range(300)]
+    eos = 8
     off = torch.tensor([0] + list(itertools.accumulate(len(t) for t in toks)), dtype=torch.int32)
     tb = torch.tensor(list(b"".join(toks)), dtype=torch.uint8)
-    order = _walk_order(off, tb, len(toks))
-    assert order.dtype == torch.int32
+    order, runs = _walk_order(off, tb, len(toks), eos)
+    assert order.dtype == torch.int32 and runs.dtype == torch.int32 and runs.numel() == 257
     o = order.tolist()
     assert sorted(o) == list(range(len(toks)))
-    keys = [(len(toks[t]), toks[t][:16]) for t in o]
+
+    def group(t):
+        return 256 if (t == eos or not toks[t]) else toks[t][0]
+
+    keys = [(group(t), len(toks[t]), toks[t][1:16]) for t in o]
     assert keys == sorted(keys)
+    # the runs: positions [runs[c], runs[c + 1]) hold exactly the tokens of
+    # first byte c, [runs[256], V) the EOS token and the empty ones
+    r = runs.tolist() + [len(toks)]
+    for c in range(257):
+        assert all(group(o[k]) == c for k in range(r[c], r[c + 1]))
+    assert r == sorted(r)
+    assert {o[k] for k in range(r[256], len(toks))} == {0, 8, 9}
     # an empty byte table (every token empty) still orders every id
-    z = _walk_order(torch.zeros(4, dtype=torch.int32), torch.zeros(1, dtype=torch.uint8), 3)
+    z, zr = _walk_order(torch.zeros(4, dtype=torch.int32), torch.zeros(1, dtype=torch.uint8), 3, -1)
     assert sorted(z.tolist()) == [0, 1, 2]
+    assert zr.tolist() == [0] * 257
+
+
+def _frame_key_row(cfg: np.ndarray, keys: np.ndarray) -> int:
+    """The frame list a config-set takes on the device (-1: none): every
+    config at one depth >= 2 over the same frames below the top, and the
+    ordered tops equal to a key."""
+    n = int(cfg[0])
+    if n < 1:
+        return -1
+    depth = cfg[2:2 + n]
+    frames = cfg[2 + 8:].reshape(8, 32)
+    d0 = int(depth[0])
+    if d0 < 2 or (depth != d0).any() or (frames[:n, :d0 - 1] != frames[0, :d0 - 1]).any():
+        return -1
+    tops = [int(frames[i, d0 - 1]) for i in range(n)]
+    for l in range(keys.shape[0]):
+        if keys[l, 0] == n and list(keys[l, 1:1 + n]) == tops:
+            return l
+    return -1
+
+
+def test_frame_lists_against_the_oracle():
+    """Rows of the recursive JSON grammar whose set sits inside a string or a
+    number: every token outside the list's seeds gets the oracle's verdict
+    from the list's bitmap (inside the rule: allowed; dead before its accept
+    state: rejected).  Prefixes end in string bodies, after an escape
+    backslash, inside UTF-8 sequences and after a minus sign."""
+    from bpdecode_amd.grammar.frames import frame_lists
+    from bpdecode_amd.tokenizer import Vocabulary
+
+    base = synth.serving_vocab(6000, seed=4)
+    extra = [b"\"", b"\\", b"\\n", b"\\\"", b"\xc3", b"\xa9", b"\xe2\x82", b"\xac\"", b"\xe9", b"ab\"",
+             b"\" :", b"\\u", b"\x01", b"\x7f", b"", b"-1", b"12", b"\"}", b"\xc3\xa9x"]
+    vocab = Vocabulary.from_tokens(list(base.token_bytes[:-1]) + extra + [b"</s>"],
+                                   eos_id=len(base.token_bytes) - 1 + len(extra))
+    small = r"""
+root   ::= string | "[" number "]"
+string ::= "\"" ( [^"\\\x00-\x1F] | "\\" ["\\/bfnrt] )* "\""
+number ::= "-"? [0-9]+ ( "." [0-9]+ )?
+"""
+    rng = np.random.default_rng(17)
+    json_prefixes = [b"[\"ab", b"{\"k", b"[\"x\\", b"[\"\xc3", b"[\"\xe2\x82", b"{\"a\":[\"", b"[-",
+                     b"{\"a\":-", b"[\"a\\u00", b"[[[\"deep", b"\"", b"[\"\\\\", b"{\"a\":\"b\",\"c"]
+    json_prefixes += [synth.json_prefix(rng, int(rng.integers(0, 6))) for _ in range(60)]
+    small_prefixes = [b"\"", b"\"ab", b"\"a\\", b"\"\xc3", b"\"\xe2\x82", b"\"x\\\\y", b"[-", b"[",
+                      b"\"\xf0\x9f", b"\"\xf0\x9f\x98", b"\"a b c", b"\"\\n", b"\"\xed\x9f"]
+    # the recursive JSON grammar saturates the 8 configs without the
+    # epsilon reduction, so unreduced tables are covered by a small grammar
+    for src, reduce, prefixes, need in ((synth.JSON_GBNF, True, json_prefixes, 12),
+                                        (small, False, small_prefixes, 8),
+                                        (small, True, small_prefixes, 8)):
+        g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(src)), vocab, eps_reduce=reduce)
+        t = OP.Table(g)
+        order, _ = _walk_order(g.tok_offsets, g.tok_bytes, g.vocab_size, g.eos_id)
+        fl = frame_lists(g, order.numpy())
+        assert fl is not None and 0 < fl.num_lists <= 64
+        hits = 0
+        pos = np.empty(vocab.size, dtype=np.int64)
+        pos[order.numpy()] = np.arange(vocab.size)
+        for p in prefixes:
+            c = g.init_config()
+            if not g.feed(c, p):
+                continue
+            cfg = c.numpy()
+            l = _frame_key_row(cfg, fl.keys)
+            if l < 0:
+                continue
+            hits += 1
+            want = np.unpackbits(OP.compute_mask(t, cfg[None].copy())[0].view(np.uint8), bitorder="little")
+            have = np.unpackbits(fl.allowed[l].view(np.uint8), bitorder="little")
+            seeded = np.zeros(want.size, dtype=bool)
+            seeded[order.numpy()[fl.seeds[fl.seed_off[l]:fl.seed_off[l + 1]]]] = True
+            V = vocab.size
+            assert not (have[:V].astype(bool) & seeded[:V]).any(), p
+            off = ~seeded[:V]
+            assert np.array_equal(have[:V][off], want[:V][off]), p
+            assert not have[V:].any()
+        assert hits >= need, (src[:20], reduce, hits)
