@@ -46,8 +46,8 @@ class PdaTableC(C.Structure):
 
 
 class PdaFramesC(C.Structure):
-    _fields_ = [("num_lists", i32), ("words", i32), ("keys", vp), ("allowed", vp), ("seed_off", vp),
-                ("seeds", vp)]
+    _fields_ = [("num_lists", i32), ("words", i32), ("keys", vp), ("trans", vp), ("allowed", vp),
+                ("seed_off", vp), ("seeds", vp)]
 
 
 class TokenBytesC(C.Structure):

@@ -578,6 +578,46 @@ __device__ __forceinline__ int long_byte(const MaskArgs& a, int64_t k, int32_t p
   return a.tok_bytes[a.tok_off[t] + p];
 }
 
+// The frame list of a set held in LDS (-1: none): every config at one depth
+// >= 2 over the same frames below its top, and the ordered tops equal to a
+// list's key.  Called by the 64 lanes of a wave; every lane gets the answer.
+__device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, int lane) {
+  if (f.num_lists <= 0) return -1;
+  const int n = c[0];
+  const int d0 = n >= 1 ? c[2] : 0;
+  if (n < 1 || n > kMaxConfigs || d0 < 2 || d0 > kMaxDepth) return -1;
+  bool bad = lane < n && c[2 + lane] != d0;
+  for (int x = lane; x < n * kMaxDepth; x += kWave) {
+    const int i = x / kMaxDepth, k = x % kMaxDepth;
+    if (k < d0 - 1 && c[kF + i * kMaxDepth + k] != c[kF + k]) bad = true;
+  }
+  if (__ballot(bad) != 0) return -1;
+  bool hit = false;
+  if (lane < f.num_lists) {
+    const int32_t* key = f.keys + lane * BPD_PDA_FRAME_KEY_WORDS;
+    hit = key[0] == n;
+    for (int i = 0; i < n && hit; ++i) hit = key[1 + i] == c[kF + i * kMaxDepth + d0 - 1];
+  }
+  const uint64_t m = __ballot(hit);
+  return m != 0u ? __ffsll(static_cast<unsigned long long>(m)) - 1 : -1;
+}
+
+// Transition-table row of set `id`, a set in frame list l: a byte whose step
+// keeps the list (and, unless the set is already saturated, drops nothing)
+// leads back to the set, a byte whose step empties it is dead; the other
+// entries stay unknown until a walk requests them.  One wave.
+__device__ void frame_fill_row(const BpdPdaFrames& f, int l, bool sat, int id, uint8_t* trow, int lane) {
+  const int32_t* tr = f.trans + l * 256;
+  for (int c = lane; c < 256; c += kWave) {
+    const int32_t code = tr[c];
+    if (code == -1) {
+      trow[c] = kTDead;
+    } else if (code >= 0 && (code & (BPD_PDA_FRAME_SAT - 1)) == l && (sat || (code & BPD_PDA_FRAME_SAT) == 0)) {
+      trow[c] = uint8_t(id);
+    }
+  }
+}
+
 // verdicts of a token in the memoised walk, past every set id
 constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 
@@ -599,12 +639,13 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ uint32_t cand_hash[kMemoReq];
   __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new, -4 duplicate, -5 no edge
   __shared__ int32_t cand_lead[kMemoReq];
+  __shared__ int32_t cand_list[kMemoReq];  // frame list of a new set (| BPD_PDA_FRAME_SAT), -1 none
   __shared__ int32_t cand_id[kMemoReq];
   __shared__ int16_t cand_lo[kMemoReq];
   __shared__ int16_t cand_hi[kMemoReq];
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
-  __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail, loop_n;
+  __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail, loop_n, row_list;
   __shared__ uint32_t h0_sh;
   __shared__ uint8_t loop0[256];  // T[0][c] == 0: byte c keeps set 0 (row-wide walk)
   // first pass of the row-wide walk: pass index i -> walk position
@@ -682,6 +723,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     wave_sync();
     coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
+    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, tid);
+    if (tid == 0) row_list = l0;
+    if (l0 >= 0) {
+      wave_sync();
+      frame_fill_row(a.frames, l0, row_cfg[1] != 0, 0, T, tid);
+    }
   }
   for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
   __syncthreads();
@@ -742,8 +789,6 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
         wave_sync();
         const bool ok = coop_advance_byte(g, wsrc, wdst, byte, lane);
-        int32_t* out = cand + r * kConfigWords;
-        for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
         if (!ok) {
           if (lane == 0) cand_res[r] = -1;
         } else {
@@ -765,6 +810,15 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             const int d = lane < nn ? wdst[2 + lane] : 0;
             cand_tops[r][lane] = d > 0 ? wdst[kF + lane * kMaxDepth + d - 1] : -1;
             if (lane == 0) cand_n[r] = nn;
+          }
+          // a new set is kept in the candidate buffer (its words are needed
+          // after this wave's buffer is reused); stored after the pool
+          // lookup's loads, which would otherwise wait for these stores
+          const int lst = found == -2 ? frame_list_of(wdst, a.frames, lane) : -1;
+          if (lane == 0) cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0)) : -1;
+          if (found == -2) {
+            int32_t* out = cand + r * kConfigWords;
+            for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
           }
           if (lane == 0) {
             cand_hash[r] = h;
@@ -839,6 +893,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         for (int k = lane; k < kConfigWords; k += kWave) dst[k] = src[k];
         coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]],
                            T + cand_id[r] * 256, lane);
+        const int cl = cand_list[r];
+        if (cl >= 0) {
+          wave_sync();
+          frame_fill_row(a.frames, cl & (BPD_PDA_FRAME_SAT - 1), (cl & BPD_PDA_FRAME_SAT) != 0, cand_id[r],
+                         T + cand_id[r] * 256, lane);
+        }
       }
     }
     __syncthreads();
@@ -855,7 +915,13 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (tid == 0) set_n[0] = n0;
     }
     __syncthreads();
-    if (tid < kWave) coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
+    if (tid < kWave) {
+      coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
+      if (row_list >= 0) {
+        wave_sync();
+        frame_fill_row(a.frames, row_list, row_cfg[1] != 0, 0, T, tid);
+      }
+    }
     if (tid == 0) {
       pool_count = 1;
       pool_hash[0] = h0_sh;
@@ -956,7 +1022,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 
     if (!dead_row) {
       // every interval of set 0 first, so the first pass already steps past byte 0
-      if (tid < 8) req[tid] = (set_bnd[0][tid] | (tid == 0 ? 1u : 0u)) & set_hit[0][tid];
+      if (tid < 8) {
+        uint32_t m = (set_bnd[0][tid] | (tid == 0 ? 1u : 0u)) & set_hit[0][tid];
+        for (uint32_t x = m; x != 0u; x &= x - 1u) {
+          const int bit = __ffs(x) - 1;
+          if (T[tid * 32 + bit] != kTUnknown) m &= ~(1u << bit);  // filled from the frame list
+        }
+        req[tid] = m;
+      }
       resolve();
     }
     if (tid == 0) {
@@ -978,35 +1051,13 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     // that stay inside the tops' call-free rule from the list's bitmap and
     // walks only the list's seeds (the tokens that reach the rule's accept
     // state, EOS and the empty tokens).
-    if (tid < kWave && !dead_row && !overflowed && a.frames.num_lists > 0) {
-      const int n = row_cfg[0];
-      const int d0 = n >= 1 ? row_cfg[2] : 0;
-      bool same = n >= 1 && d0 >= 2;
-      if (same) {
-        bool bad = tid < n && row_cfg[2 + tid] != d0;
-        for (int f = tid; f < n * kMaxDepth; f += kWave) {
-          const int i = f / kMaxDepth, k = f % kMaxDepth;
-          if (k < d0 - 1 && row_cfg[kF + i * kMaxDepth + k] != row_cfg[kF + k]) bad = true;
-        }
-        same = __ballot(bad) == 0;
-      }
-      if (same) {
-        bool hit = false;
-        if (tid < a.frames.num_lists) {
-          const int32_t* key = a.frames.keys + tid * BPD_PDA_FRAME_KEY_WORDS;
-          hit = key[0] == n;
-          for (int i = 0; i < n && hit; ++i) hit = key[1 + i] == row_cfg[kF + i * kMaxDepth + d0 - 1];
-        }
-        const uint64_t m = __ballot(hit);
-        if (m != 0u && tid == 0) {
-          const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
-          const int32_t s0 = a.frames.seed_off[l], s1 = a.frames.seed_off[l + 1];
-          pass_list = l;
-          pass_mode = 2;
-          pass_base = s0;
-          pass_total = s1 > s0 ? s1 - s0 : 0;
-        }
-      }
+    if (tid == 0 && !dead_row && !overflowed && row_list >= 0) {
+      const int l = row_list;
+      const int32_t s0 = a.frames.seed_off[l], s1 = a.frames.seed_off[l + 1];
+      pass_list = l;
+      pass_mode = 2;
+      pass_base = s0;
+      pass_total = s1 > s0 ? s1 - s0 : 0;
     }
     __syncthreads();
     if (pass_list >= 0) {  // (pass_mode is written below; pass_list is not)

@@ -167,7 +167,8 @@ class PdaTensors:
             fl = frame_lists(self, order.numpy())
             if fl is not None and fl.num_lists > 0:
                 dev = off.device
-                arrs = [torch.from_numpy(fl.keys).to(dev), torch.from_numpy(fl.allowed.view("<i4")).to(dev),
+                arrs = [torch.from_numpy(fl.keys).to(dev), torch.from_numpy(fl.trans).to(dev),
+                        torch.from_numpy(fl.allowed.view("<i4")).to(dev),
                         torch.from_numpy(fl.seed_off).to(dev),
                         torch.from_numpy(fl.seeds if fl.seeds.size else np.zeros(1, np.int32)).to(dev)]
                 keep += arrs

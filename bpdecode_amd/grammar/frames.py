@@ -29,6 +29,7 @@ import numpy as np
 
 MAX_LISTS = 64  # the kernel matches a row against all keys with one wave
 KEY_WORDS = 9  # n, then up to 8 top states
+SAT = 0x10000  # transition flag: the step dropped a state at the 8-config cap
 _EPS, _BYTE, _CALL = 0, 1, 2
 _DEAD, _BOUNDARY = -1, -2
 _CAP = 8  # configs per set
@@ -37,6 +38,7 @@ _CAP = 8  # configs per set
 @dataclass
 class FrameLists:
     keys: np.ndarray  # int32 [L, 9]
+    trans: np.ndarray  # int32 [L, 256]: list reached (| SAT), -1 empty, -2 reaches the accept state
     allowed: np.ndarray  # uint32 [L, ceil(V/32)]
     seed_off: np.ndarray  # int32 [L + 1]
     seeds: np.ndarray  # int32 walk positions
@@ -61,42 +63,50 @@ class _Tables:
         return range(int(self.off[s]), int(self.off[s + 1]))
 
 
-def _close(t: _Tables, nxt: list[int]):
-    """Closure and compaction of a list inside a call-free rule; BOUNDARY
-    when some state accepts (its config pops into the caller)."""
+def _add(nxt: list[int], x: int) -> bool:
+    """Append x unless present; False when the list is full (x dropped)."""
+    if x in nxt:
+        return True
+    if len(nxt) >= _CAP:
+        return False
+    nxt.append(x)
+    return True
+
+
+def _close(t: _Tables, nxt: list[int], sat: bool):
+    """Closure and compaction of a list inside a call-free rule, and whether
+    some state was dropped at the cap; BOUNDARY when some state accepts (its
+    config pops into the caller)."""
     i = 0
     while i < len(nxt):
         s = nxt[i]
         if t.accept[s]:
-            return _BOUNDARY
+            return _BOUNDARY, sat
         for e in t.edges(s):
             k = int(t.kind[e])
             if k == _CALL:
-                return _BOUNDARY  # not call-free after all: leave it to the real walk
+                return _BOUNDARY, sat  # not call-free after all: leave it to the real walk
             if k == _EPS:
-                x = int(t.dst[e])
-                if x not in nxt and len(nxt) < _CAP:
-                    nxt.append(x)
+                sat = not _add(nxt, int(t.dst[e])) or sat
         i += 1
     out = tuple(s for s in nxt if t.live[s])
-    return out if out else _DEAD
+    return (out if out else _DEAD), sat
 
 
 def _step(t: _Tables, lst: tuple, byte: int):
     nxt: list[int] = []
+    sat = False
     for s in lst:
         for e in t.edges(s):
             if int(t.kind[e]) == _BYTE and int(t.lo[e]) <= byte <= int(t.hi[e]):
-                x = int(t.dst[e])
-                if x not in nxt and len(nxt) < _CAP:
-                    nxt.append(x)
-    return _close(t, nxt)
+                sat = not _add(nxt, int(t.dst[e])) or sat
+    return _close(t, nxt, sat)
 
 
 def _rule_lists(t: _Tables, start: int, limit: int) -> tuple[list[tuple], dict]:
     """Lists reachable from the rule's entry by steps that stay inside, in
     breadth-first order (at most ``limit``), and their byte transitions."""
-    entry = _close(t, [start])
+    entry, _ = _close(t, [start], False)
     if not isinstance(entry, tuple):
         return [], {}
     lists = [entry]
@@ -106,7 +116,7 @@ def _rule_lists(t: _Tables, start: int, limit: int) -> tuple[list[tuple], dict]:
     while head < len(lists):
         row = []
         for byte in range(256):
-            nx = _step(t, lists[head], byte)
+            nx, sat = _step(t, lists[head], byte)
             if isinstance(nx, tuple):
                 if nx not in index:
                     if len(lists) >= limit:
@@ -114,7 +124,12 @@ def _rule_lists(t: _Tables, start: int, limit: int) -> tuple[list[tuple], dict]:
                     else:
                         index[nx] = len(lists)
                         lists.append(nx)
-            row.append(_BOUNDARY if nx is None else (index[nx] if isinstance(nx, tuple) else nx))
+            if nx is None:
+                row.append(_BOUNDARY)
+            elif isinstance(nx, tuple):
+                row.append(index[nx] | (SAT if sat else 0))
+            else:
+                row.append(nx)
         trans[head] = row
         head += 1
     return lists, trans
@@ -136,11 +151,12 @@ def frame_lists(g, order: np.ndarray, limit: int = MAX_LISTS) -> FrameLists | No
         shift = len(keys)
         for i, lst in enumerate(lists):
             keys.append(lst)
-            trans_rows.append([x + shift if x >= 0 else x for x in trans[i]])
+            trans_rows.append([x + shift if x >= 0 else x for x in trans[i]])  # (SAT is above the ids)
     if not keys:
         return None
     L, V = len(keys), g.vocab_size
-    table = np.array(trans_rows, dtype=np.int32)  # [L, 256]
+    codes = np.array(trans_rows, dtype=np.int32)  # [L, 256]
+    table = np.where(codes >= 0, codes & (SAT - 1), codes)
     off = g.tok_offsets.cpu().numpy().astype(np.int64)
     tb = g.tok_bytes.cpu().numpy()
     lens = off[1:] - off[:-1]
@@ -177,6 +193,7 @@ def frame_lists(g, order: np.ndarray, limit: int = MAX_LISTS) -> FrameLists | No
         key_arr[i, 1:1 + len(lst)] = lst
     return FrameLists(
         keys=key_arr,
+        trans=np.ascontiguousarray(codes),
         allowed=np.ascontiguousarray(allowed.astype(np.uint32)),
         seed_off=np.array(seed_off, dtype=np.int32),
         seeds=np.concatenate(seed_parts) if seed_parts else np.zeros(0, np.int32),

@@ -229,15 +229,22 @@ typedef struct BpdPdaTable {
  * the tops' call-free rule without reaching its accept state and keeps the
  * set non-empty) and walks only the tokens at walk positions
  * seeds[seed_off[l] .. seed_off[l + 1]) (every other token not in allowed[l]
- * is rejected).  Built by grammar/frames.py for the default walk order: the
- * device trusts the contents (seed_off non-decreasing within the seeds
- * array; wrong lists give wrong verdicts). */
+ * is rejected).  trans[l][c] is the list a byte c step reaches (or-ed with
+ * BPD_PDA_FRAME_SAT when the step drops a state at the 8-config cap), -1
+ * when it empties the set, -2 when it reaches the accept state: the device
+ * fills the transition-table row of every such set it meets (a byte that
+ * keeps the list and the saturation flag leads back to the set, a byte that
+ * empties it is dead) without stepping it.  Built by grammar/frames.py for
+ * the default walk order: the device trusts the contents (seed_off
+ * non-decreasing within the seeds array; wrong lists give wrong verdicts). */
 #define BPD_PDA_MAX_FRAME_LISTS 64
 #define BPD_PDA_FRAME_KEY_WORDS 9
+#define BPD_PDA_FRAME_SAT 0x10000
 typedef struct BpdPdaFrames {
   int32_t num_lists;       /* 0 .. BPD_PDA_MAX_FRAME_LISTS */
   int32_t words;           /* (vocab_size + 31) / 32 */
   const int32_t* keys;     /* [num_lists, BPD_PDA_FRAME_KEY_WORDS]; unused tops -1 */
+  const int32_t* trans;    /* [num_lists, 256] */
   const uint32_t* allowed; /* [num_lists, words] */
   const int32_t* seed_off; /* [num_lists + 1] */
   const int32_t* seeds;    /* [seed_off[num_lists]] walk positions */

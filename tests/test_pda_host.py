@@ -371,4 +371,23 @@ number ::= "-"? [0-9]+ ( "." [0-9]+ )?
             off = ~seeded[:V]
             assert np.array_equal(have[:V][off], want[:V][off]), p
             assert not have[V:].any()
+            # the byte table: the oracle's step from the row by each byte
+            # gives the coded list over the same stack (saturation flag
+            # included), or empties the set
+            d0 = int(cfg[2])
+            below = cfg[10:10 + d0 - 1].copy()
+            for byte in range(256):
+                code = int(fl.trans[l, byte])
+                nxt = cfg.copy()
+                ok = OP.advance_byte(t, nxt, byte)
+                if code == -1:
+                    assert not ok, (p, byte)
+                elif code >= 0:
+                    assert ok, (p, byte)
+                    l2 = code & 0xFFFF
+                    assert _frame_key_row(nxt, fl.keys) == l2, (p, byte)
+                    n2 = int(nxt[0])
+                    assert (nxt[2:2 + n2] == d0).all()
+                    assert all((nxt[10 + i * 32:10 + i * 32 + d0 - 1] == below).all() for i in range(n2))
+                    assert int(nxt[1]) == (int(cfg[1]) | (1 if code & 0x10000 else 0)), (p, byte)
         assert hits >= need, (src[:20], reduce, hits)
