@@ -580,8 +580,9 @@ __device__ __forceinline__ int long_byte(const MaskArgs& a, int64_t k, int32_t p
 
 // The frame list of a set held in LDS (-1: none): every config at one depth
 // >= 2 over the same frames below its top, and the ordered tops equal to a
-// list's key.  Called by the 64 lanes of a wave; every lane gets the answer.
-__device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, int lane) {
+// list's key (`keys`: the lists' keys, staged in LDS).  Called by the 64
+// lanes of a wave; every lane gets the answer.
+__device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const int32_t* keys, int lane) {
   if (f.num_lists <= 0) return -1;
   const int n = c[0];
   const int d0 = n >= 1 ? c[2] : 0;
@@ -594,7 +595,7 @@ __device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, int lane) 
   if (__ballot(bad) != 0) return -1;
   bool hit = false;
   if (lane < f.num_lists) {
-    const int32_t* key = f.keys + lane * BPD_PDA_FRAME_KEY_WORDS;
+    const int32_t* key = keys + lane * BPD_PDA_FRAME_KEY_WORDS;
     hit = key[0] == n;
     for (int i = 0; i < n && hit; ++i) hit = key[1 + i] == c[kF + i * kMaxDepth + d0 - 1];
   }
@@ -640,6 +641,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new, -4 duplicate, -5 no edge
   __shared__ int32_t cand_lead[kMemoReq];
   __shared__ int32_t cand_list[kMemoReq];  // frame list of a new set (| BPD_PDA_FRAME_SAT), -1 none
+  __shared__ int32_t fkeys[BPD_PDA_MAX_FRAME_LISTS * BPD_PDA_FRAME_KEY_WORDS];
   __shared__ int32_t cand_id[kMemoReq];
   __shared__ int16_t cand_lo[kMemoReq];
   __shared__ int16_t cand_hi[kMemoReq];
@@ -694,6 +696,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     g.live = lv;
   }
   for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
+  for (int i = tid; i < a.frames.num_lists * BPD_PDA_FRAME_KEY_WORDS; i += kMemoThreads) fkeys[i] = a.frames.keys[i];
   const int32_t vwords = (a.vocab + 31) / 32;
   for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
   for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0;
@@ -723,7 +726,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     wave_sync();
     coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
-    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, tid);
+    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fkeys, tid);
     if (tid == 0) row_list = l0;
     if (l0 >= 0) {
       wave_sync();
@@ -785,10 +788,13 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       for (int r = wave; r < n; r += kMemoThreads / kWave) {
         if (cand_res[r] < -3) continue;
         const int set = req_list[r] >> 8, byte = req_list[r] & 255;
+        // set 0 is the row's own set, already in LDS
         const int32_t* ps = pool + set * kConfigWords;
-        for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
-        wave_sync();
-        const bool ok = coop_advance_byte(g, wsrc, wdst, byte, lane);
+        if (set != 0) {
+          for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
+          wave_sync();
+        }
+        const bool ok = coop_advance_byte(g, set != 0 ? wsrc : row_cfg, wdst, byte, lane);
         if (!ok) {
           if (lane == 0) cand_res[r] = -1;
         } else {
@@ -814,7 +820,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           // a new set is kept in the candidate buffer (its words are needed
           // after this wave's buffer is reused); stored after the pool
           // lookup's loads, which would otherwise wait for these stores
-          const int lst = found == -2 ? frame_list_of(wdst, a.frames, lane) : -1;
+          const int lst = found == -2 ? frame_list_of(wdst, a.frames, fkeys, lane) : -1;
           if (lane == 0) cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0)) : -1;
           if (found == -2) {
             int32_t* out = cand + r * kConfigWords;
