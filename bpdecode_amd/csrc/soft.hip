@@ -415,17 +415,23 @@ __device__ inline Lse block_lse(Lse a) {
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Launch geometry of one call.
+constexpr int kWideLoads = 8;                                   // float4 groups per thread (wave-shift stats)
+constexpr int64_t kWideChunk = kPriorThreads * 4 * kWideLoads;  // 16384 tokens per block
+
 struct PriorPlan {
   bool class_stats;  // class-atomic stats (else pieces)
+  bool wide;         // wave-shift stats over 16384-token chunks (class_stats only)
   int G;             // chunk blocks per row
   int Gp;            // piece blocks per row (pieces path)
 };
 
-PriorPlan prior_plan(int64_t rows, int64_t vocab, int32_t C, int32_t P, bool force_pieces) {
+PriorPlan prior_plan(int64_t rows, int64_t vocab, int32_t C, int32_t P, bool force_pieces, bool wide) {
   PriorPlan pl;
   pl.class_stats = !force_pieces && C <= kLdsClasses;
+  pl.wide = pl.class_stats && wide;
   if (pl.class_stats) {
-    pl.G = int((vocab + kStatChunk - 1) / kStatChunk);
+    const int64_t chunk = pl.wide ? kWideChunk : kStatChunk;
+    pl.G = int((vocab + chunk - 1) / chunk);
     pl.Gp = 0;
   } else {
     const int64_t g = rows > 0 ? (1024 + rows - 1) / rows : 1;
@@ -465,7 +471,7 @@ size_t prior_ws_bytes(int64_t rows, const PriorPlan& pl, int32_t C, int32_t P) {
 }
 
 size_t prior_lds_bytes(int32_t S, int32_t C, int32_t P, int64_t pairs, bool pairs_in_lds, bool pieces) {
-  size_t n = size_t(C) * (pieces ? 4 : 8) + size_t(S) * 8 + size_t(S + 3) / 4 * 4 + size_t(S + 1) * 4;
+  size_t n = size_t(C) * 4 + size_t(S) * 8 + size_t(S + 3) / 4 * 4 + size_t(S + 1) * 4;
   if (pairs_in_lds) n += size_t(pairs) * 4;
   n = (n + 7) / 8 * 8;
   return pieces ? n + size_t(P) * 8 : n;
@@ -644,6 +650,144 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_members_kernel(
   }
 }
 
+// Wave-shift statistics, grid (G, rows): block g takes tokens
+// [16384 g, 16384 (g + 1)) of its row, 64 per thread (16 float4 groups in
+// flight, each group coalesced), and the uint16 class map of the same tokens
+// (shared by every row, so it stays in L2).  Each wave shifts by its own
+// maximum M_w: the chunk logsumexp and, per class, sum exp(x - M_w) over the
+// wave's classed tokens go to the wave's own LDS array, so the block needs
+// no class-maximum pass and a single barrier.  The class partials written
+// are (max_w M_w over waves with a non-zero sum, the sums rescaled to it),
+// the same (max, sum) form the rounds kernel merges.  A class member more
+// than 80 below its wave maximum could underflow there; a block that has one
+// takes the exact per-class maximum instead (class-max pass, then the sums).
+// Dynamic LDS: 4 * C wave sums, then C class maxima and C sums (exact path).
+__global__ __launch_bounds__(kPriorThreads) void prior_stats_wave_kernel(
+    const float* __restrict__ logits, int64_t ld, int64_t V, const uint16_t* __restrict__ token_class16,
+    int32_t C, PriorWs ws) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int kWaves = kPriorThreads / 64;
+  float* wsum = smem;                                               // [kWaves][C]
+  int32_t* cmax = reinterpret_cast<int32_t*>(smem + kWaves * C);    // [C] exact path
+  float* esum = smem + kWaves * C + C;                              // [C] exact path
+  __shared__ float wm[kWaves], wl[kWaves];
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x / 64;
+  const float* row = logits + b * ld;
+  const int64_t base = int64_t(g) * kWideChunk;
+  for (int32_t c = lane; c < C; c += 64) wsum[w * C + c] = 0.0f;
+  float4 x[kWideLoads];
+  uint2 k[kWideLoads];
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) {
+    const int64_t t = base + (int64_t(u) * kPriorThreads + threadIdx.x) * 4;
+    if (t < V) {
+      x[u] = *reinterpret_cast<const float4*>(row + t);
+      k[u] = *reinterpret_cast<const uint2*>(token_class16 + t);
+    } else {
+      x[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      k[u] = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  // the wave's own class sums: only this wave writes them, and LDS
+  // operations of one wave complete in order, so a wave fence orders the
+  // zeroing above before the atomics
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float sum = 0.0f;
+  bool under = false;
+  if (m != -INFINITY) {
+    auto one = [&](float v, uint32_t kc) {
+      const float e = exp_shift(v, m);
+      sum += e;
+      if (kc != 0xFFFFu && v != -INFINITY) {
+        under = under || v - m < -80.0f;
+        atomicAdd(&wsum[w * C + int32_t(kc)], e);
+      }
+    };
+#pragma unroll
+    for (int u = 0; u < kWideLoads; ++u) {
+      one(x[u].x, k[u].x & 0xFFFFu);
+      one(x[u].y, k[u].x >> 16);
+      one(x[u].z, k[u].y & 0xFFFFu);
+      one(x[u].w, k[u].y >> 16);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  if (lane == 0) {
+    wm[w] = m;
+    wl[w] = sum;
+  }
+  const bool exact = __syncthreads_or(under);
+  if (threadIdx.x == 0) {
+    Lse r{-INFINITY, 0.0f};
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) r = lse_merge_fast(r, Lse{wm[i], wl[i]});
+    ws.part[(b * G + g) * 2] = r.m;
+    ws.part[(b * G + g) * 2 + 1] = r.s;
+  }
+  float* out = ws.mid + (b * G + g) * int64_t(C) * 2;
+  if (!exact) {
+    for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+      float cm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i)
+        if (wsum[i * C + c] > 0.0f) cm = fmaxf(cm, wm[i]);
+      float cs = 0.0f;
+      if (cm != -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i)
+          if (wsum[i * C + c] > 0.0f) cs += wsum[i * C + c] * exp_shift(wm[i], cm);
+      }
+      out[2 * c] = cm;
+      out[2 * c + 1] = cs;
+    }
+    return;
+  }
+  // exact path: per-class maximum, then the sums, from the values in registers
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    cmax[c] = ord_of(-INFINITY);
+    esum[c] = 0.0f;
+  }
+  __syncthreads();
+  auto cls_max = [&](float v, uint32_t kc) {
+    if (kc != 0xFFFFu && v != -INFINITY) atomicMax(&cmax[int32_t(kc)], ord_of(v));
+  };
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) {
+    cls_max(x[u].x, k[u].x & 0xFFFFu);
+    cls_max(x[u].y, k[u].x >> 16);
+    cls_max(x[u].z, k[u].y & 0xFFFFu);
+    cls_max(x[u].w, k[u].y >> 16);
+  }
+  __syncthreads();
+  auto cls_sum = [&](float v, uint32_t kc) {
+    if (kc != 0xFFFFu && v != -INFINITY) {
+      const int32_t c = int32_t(kc);
+      atomicAdd(&esum[c], exp_shift(v, float_of_ord(cmax[c])));
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) {
+    cls_sum(x[u].x, k[u].x & 0xFFFFu);
+    cls_sum(x[u].y, k[u].x >> 16);
+    cls_sum(x[u].z, k[u].y & 0xFFFFu);
+    cls_sum(x[u].w, k[u].y >> 16);
+  }
+  __syncthreads();
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    out[2 * c] = float_of_ord(cmax[c]);
+    out[2 * c + 1] = esum[c];
+  }
+}
+
 // Pieces stats, grid (G + Gp, rows): block g < G takes vocab chunk g
 // (partial row logsumexp), blocks G.. the class pieces (one wave per piece,
 // unnormalised piece logsumexp).
@@ -724,9 +868,7 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_pieces_kernel(
 // state: each lane folds every fourth pair of the state into a running
 // (max, sum of exp(v - max)), and the quad merges the four by DPP exchanges.
 constexpr int kRoundThreads = 1024;
-constexpr int kQuadLoads = 16;   // pairs per lane in flight
 constexpr int kPairRegs = 8;     // pairs per thread held in registers while they load
-constexpr int kMergeRegs = 8;    // class partials per thread held in registers
 
 // DPP quad permutations: lane i reads lane i ^ 1, lane i ^ 2 of its quad
 constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
@@ -748,10 +890,31 @@ __device__ inline void quad_lse_step(float& m, float& s) {
   m = nm;
 }
 
+// max / sum over the eight lanes of an aligned group (quad DPP, then the
+// other quad); every lane of the group gets the result
+__device__ inline float group8_max(float x) {
+  x = fmaxf(x, quad_read<kDppQuadXor1>(x));
+  x = fmaxf(x, quad_read<kDppQuadXor2>(x));
+  return fmaxf(x, __shfl_xor(x, 4));
+}
+__device__ inline float group8_sum(float x) {
+  x += quad_read<kDppQuadXor1>(x);
+  x += quad_read<kDppQuadXor2>(x);
+  return x + __shfl_xor(x, 4);
+}
+
 template <bool PairsInLds>
 __device__ inline uint32_t prior_pair(const uint32_t* pr, const BpdSoftClasses& cls, int32_t i) {
   if (PairsInLds) return pr[i];
   return (uint32_t(cls.pair_class[i]) << 16) | uint32_t(cls.pair_next[i]);
+}
+
+__device__ inline float prior_value(float x, float lse, int64_t t, float z, bool acc_s, int32_t eos,
+                                    float alpha) {
+  const float lp = x - lse;
+  if (t == eos) return acc_s ? lp : -INFINITY;
+  if (z == -INFINITY) return -INFINITY;
+  return alpha != 0.0f ? fmaf(alpha, z, lp) : lp;
 }
 
 template <bool PairsInLds, bool ClassStats>
@@ -766,9 +929,7 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
   const int tid = threadIdx.x;
   const int32_t C = cls.num_classes, P = cls.num_pieces, NP = cls.num_pairs;
   float* lc = lds;                                        // [C] class logsumexp, later zcls
-  int32_t* lci = reinterpret_cast<int32_t*>(lc);          // [C] class max (ord) while merging
-  float* cs = lc + C;                                     // [C] class sums while merging (ClassStats)
-  float* z0 = ClassStats ? cs + C : cs;                   // [S]
+  float* z0 = lc + C;                                     // [S]
   float* z1 = z0 + S;                                     // [S]
   uint8_t* flag = reinterpret_cast<uint8_t*>(z1 + S);     // [S] bit 0 live, bit 1 accept
   int32_t* so = reinterpret_cast<int32_t*>(z1 + S + (S + 3) / 4);  // [S + 1]
@@ -785,16 +946,22 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
       pv[u] = j < NP ? (uint32_t(cls.pair_class[j]) << 16) | uint32_t(cls.pair_next[j]) : 0u;
     }
   }
-  const int CG = ClassStats ? C * G : 0;
   const float* mid = ws.mid + b * int64_t(G) * C * 2;  // [G][C] (max, sum)
+  // class partials: eight lanes per class, lane q takes chunks q, q + 8, ...;
+  // those of the first 128 classes and 32 chunks are loaded here
+  constexpr int kMergeLanes = 8, kMergeRegs = 4;
+  const int mc = tid / kMergeLanes, mq = tid % kMergeLanes;
   float2 mv[kMergeRegs];
   if (ClassStats) {
 #pragma unroll
     for (int u = 0; u < kMergeRegs; ++u) {
-      const int e = tid + u * kRoundThreads;
-      mv[u] = e < CG ? *reinterpret_cast<const float2*>(mid + 2 * int64_t(e)) : make_float2(-INFINITY, 0.0f);
+      const int g = mq + kMergeLanes * u;
+      mv[u] = mc < C && g < G ? *reinterpret_cast<const float2*>(mid + (int64_t(g) * C + mc) * 2)
+                              : make_float2(-INFINITY, 0.0f);
     }
   }
+  // the row's state, needed only at the end, loaded with the rest
+  const int32_t sb = states[slots ? slots[b] : b];
   Lse part{-INFINITY, 0.0f};
   if (tid < 64 && tid < G) part = Lse{ws.part[(b * G + tid) * 2], ws.part[(b * G + tid) * 2 + 1]};
   const uint8_t lv0 = tid < S ? live[tid] : 0;
@@ -805,12 +972,6 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
     for (int i = tid + 64; i < G; i += 64) part = lse_merge(part, Lse{ws.part[(b * G + i) * 2], ws.part[(b * G + i) * 2 + 1]});
     part = wave_lse(part);
     if (tid == 0) lse_sh = lse_value(part);
-  }
-  if (ClassStats) {
-    for (int32_t c = tid; c < C; c += kRoundThreads) {
-      lci[c] = ord_of(-INFINITY);
-      cs[c] = 0.0f;
-    }
   }
   for (int32_t s = tid; s < S; s += kRoundThreads) {
     const bool lv = (s == tid ? lv0 : live[s]) != 0;
@@ -830,31 +991,37 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
   }
   __syncthreads();
   if (ClassStats) {
-    // class c: max over the G chunk partials, then the rescaled sum
+    // class c: the maximum of its G chunk partials over the group's lanes,
+    // then the rescaled sum (every lane runs the same loop: the group
+    // exchanges need all of them)
+    for (int32_t c0 = 0; c0 < C; c0 += kRoundThreads / kMergeLanes) {
+      const int32_t c = c0 + mc;
+      float2 v[kMergeRegs];
 #pragma unroll
-    for (int u = 0; u < kMergeRegs; ++u) {
-      const int e = tid + u * kRoundThreads;
-      if (e < CG && mv[u].x != -INFINITY) atomicMax(&lci[e % C], ord_of(mv[u].x));
-    }
-    for (int e = tid + kMergeRegs * kRoundThreads; e < CG; e += kRoundThreads) {
-      const float m = mid[2 * int64_t(e)];
-      if (m != -INFINITY) atomicMax(&lci[e % C], ord_of(m));
-    }
-    __syncthreads();
+      for (int u = 0; u < kMergeRegs; ++u) {
+        const int g = mq + kMergeLanes * u;
+        v[u] = c0 == 0 ? mv[u]
+                       : (c < C && g < G ? *reinterpret_cast<const float2*>(mid + (int64_t(g) * C + c) * 2)
+                                         : make_float2(-INFINITY, 0.0f));
+      }
+      float cm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kMergeRegs; ++u) {
-      const int e = tid + u * kRoundThreads;
-      if (e < CG && mv[u].x != -INFINITY)
-        atomicAdd(&cs[e % C], mv[u].y * exp_shift(mv[u].x, float_of_ord(lci[e % C])));
-    }
-    for (int e = tid + kMergeRegs * kRoundThreads; e < CG; e += kRoundThreads) {
-      const float2 v = *reinterpret_cast<const float2*>(mid + 2 * int64_t(e));
-      if (v.x != -INFINITY) atomicAdd(&cs[e % C], v.y * exp_shift(v.x, float_of_ord(lci[e % C])));
-    }
-    __syncthreads();
-    for (int32_t c = tid; c < C; c += kRoundThreads) {
-      const float s = cs[c];
-      lc[c] = s > 0.0f ? float_of_ord(lci[c]) + logf(s) : -INFINITY;
+      for (int u = 0; u < kMergeRegs; ++u) cm = fmaxf(cm, v[u].x);
+      for (int g = mq + kMergeLanes * kMergeRegs; c < C && g < G; g += kMergeLanes)
+        cm = fmaxf(cm, mid[(int64_t(g) * C + c) * 2]);
+      cm = group8_max(cm);
+      float csum = 0.0f;
+      if (cm != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < kMergeRegs; ++u)
+          if (v[u].x != -INFINITY) csum += v[u].y * exp_shift(v[u].x, cm);
+        for (int g = mq + kMergeLanes * kMergeRegs; c < C && g < G; g += kMergeLanes) {
+          const float2 w = *reinterpret_cast<const float2*>(mid + (int64_t(g) * C + c) * 2);
+          if (w.x != -INFINITY) csum += w.y * exp_shift(w.x, cm);
+        }
+      }
+      csum = group8_sum(csum);
+      if (mq == 0 && c < C) lc[c] = csum > 0.0f ? cm + logf(csum) : -INFINITY;
     }
   } else {
     // [P] piece (max, sum) pairs, 8-byte aligned after the pairs
@@ -873,57 +1040,100 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
   const float lse = lse_sh;
   const float lp_eos = eos >= 0 ? x_eos - lse : -INFINITY;
 
-  const int quad = tid >> 2, ql = tid & 3;
-  constexpr int kQuads = kRoundThreads / 4;
+  // eight lanes per state: lane l folds pairs l, l + 8, ... of its state
+  constexpr int kLanes = 8;
+  constexpr int kGroups = kRoundThreads / kLanes;
+  constexpr int kRegPairs = 16;  // pairs per lane kept in registers across the rounds
+  const int grp = tid / kLanes, gl = tid % kLanes;
   float* zc = z0;
   float* zn = z1;
-  for (int32_t j = 0; j < rounds; ++j) {
-    for (int32_t s0 = 0; s0 < S; s0 += kQuads) {
-      const int32_t s = s0 + quad;
-      const bool on = s < S;
-      const int32_t i1 = on ? so[s + 1] : 0;
-      float m = -INFINITY, sm = 0.0f;
-      for (int32_t base = (on ? so[s] : 0) + ql; base < i1; base += 4 * kQuadLoads) {
-        // indices clamped into the state's pairs, so that every read of the
-        // batch is issued before the first wait; the clamped ones read -inf
-        uint32_t pp[kQuadLoads];
-#pragma unroll
-        for (int u = 0; u < kQuadLoads; ++u) pp[u] = prior_pair<PairsInLds>(pr, cls, min(base + 4 * u, i1 - 1));
-        float v[kQuadLoads];
-#pragma unroll
-        for (int u = 0; u < kQuadLoads; ++u) {
-          const float x = lc[pp[u] >> 16] + zc[pp[u] & 0xFFFFu];
-          v[u] = base + 4 * u < i1 ? x : -INFINITY;
-        }
-        float bm = v[0];
-#pragma unroll
-        for (int u = 1; u < kQuadLoads; ++u) bm = fmaxf(bm, v[u]);
-        if (bm != -INFINITY) {
-          const float nm = fmaxf(m, bm);
-          float acc = sm * exp_shift(m, nm);  // 0 while m is -inf
-#pragma unroll
-          for (int u = 0; u < kQuadLoads; ++u) acc += exp_shift(v[u], nm);
-          sm = acc;
-          m = nm;
-        }
-      }
-      quad_lse_step<kDppQuadXor1>(m, sm);
-      quad_lse_step<kDppQuadXor2>(m, sm);
-      if (on && ql == 0) {
-        const uint8_t f = flag[s];
-        float v = m == -INFINITY ? -INFINITY : m + logf(sm) - lse;
-        if (f & 2) v = log_add_exp(v, lp_eos);
-        zn[s] = (f & 1) ? v : -INFINITY;
-      }
+  // the fold of one (value, ...) into a running (max, sum of exp(v - max))
+  auto fold = [](float& m, float& sm, float x) {
+    if (x == -INFINITY) return;
+    if (x > m) {
+      sm = (m == -INFINITY ? 0.0f : sm * exp_shift(m, x)) + 1.0f;
+      m = x;
+    } else {
+      sm += exp_shift(x, m);
     }
-    __syncthreads();
-    float* t = zc;
-    zc = zn;
-    zn = t;
+  };
+  // the group's (max, sum) into zn[s]
+  auto finish = [&](int32_t s, bool on, float m, float sm) {
+    quad_lse_step<kDppQuadXor1>(m, sm);
+    quad_lse_step<kDppQuadXor2>(m, sm);
+    {
+      // the two quads of the state
+      const float mo = __shfl_xor(m, 4), so4 = __shfl_xor(sm, 4);
+      const float nm = fmaxf(m, mo);
+      if (nm != -INFINITY) sm = sm * exp_shift(m, nm) + so4 * exp_shift(mo, nm);
+      m = nm;
+    }
+    if (on && gl == 0) {
+      const uint8_t f = flag[s];
+      float v = m == -INFINITY ? -INFINITY : m + logf(sm) - lse;
+      if (f & 2) v = log_add_exp(v, lp_eos);
+      zn[s] = (f & 1) ? v : -INFINITY;
+    }
+  };
+  if (S <= kGroups) {
+    // one state per group; a lane's first kRegPairs pairs are gathered once
+    // as (class logsumexp, next state), so a round reads only zc for them
+    const int32_t s = grp;
+    const bool on = s < S;
+    const int32_t i0 = on ? so[s] : 0, i1 = on ? so[s + 1] : 0;
+    float w[kRegPairs];
+    int32_t nx[kRegPairs];
+#pragma unroll
+    for (int u = 0; u < kRegPairs; ++u) {
+      const int32_t i = i0 + gl + kLanes * u;
+      const uint32_t p = i < i1 ? prior_pair<PairsInLds>(pr, cls, i) : 0u;
+      w[u] = i < i1 ? lc[p >> 16] : -INFINITY;
+      nx[u] = i < i1 ? int32_t(p & 0xFFFFu) : 0;
+    }
+    const int32_t i_rest = i0 + kLanes * kRegPairs;
+    for (int32_t j = 0; j < rounds; ++j) {
+      float v[kRegPairs];
+#pragma unroll
+      for (int u = 0; u < kRegPairs; ++u) v[u] = w[u] + zc[nx[u]];  // zc is never +inf
+      float m = v[0];
+#pragma unroll
+      for (int u = 1; u < kRegPairs; ++u) m = fmaxf(m, v[u]);
+      float sm = 0.0f;
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < kRegPairs; ++u) sm += exp_shift(v[u], m);
+      }
+      for (int32_t i = i_rest + gl; i < i1; i += kLanes) {
+        const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
+        fold(m, sm, lc[p >> 16] + zc[p & 0xFFFFu]);
+      }
+      finish(s, on, m, sm);
+      __syncthreads();
+      float* t = zc;
+      zc = zn;
+      zn = t;
+    }
+  } else {
+    for (int32_t j = 0; j < rounds; ++j) {
+      for (int32_t s0 = 0; s0 < S; s0 += kGroups) {
+        const int32_t s = s0 + grp;
+        const bool on = s < S;
+        const int32_t i1 = on ? so[s + 1] : 0;
+        float m = -INFINITY, sm = 0.0f;
+        for (int32_t i = (on ? so[s] : 0) + gl; i < i1; i += kLanes) {
+          const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
+          fold(m, sm, lc[p >> 16] + zc[p & 0xFFFFu]);
+        }
+        finish(s, on, m, sm);
+      }
+      __syncthreads();
+      float* t = zc;
+      zc = zn;
+      zn = t;
+    }
   }
 
   // zcls[b, c] = logZ(next state of class c from s_b), -inf when rejected
-  const int32_t sb = states[slots ? slots[b] : b];
   for (int32_t c = tid; c < C; c += kRoundThreads) lc[c] = -INFINITY;
   __syncthreads();
   if (sb >= 0 && sb < S) {
@@ -937,23 +1147,16 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
   if (tid == 0) ws.lse[b] = lse;
 }
 
-__device__ inline float prior_value(float x, float lse, int64_t t, float z, bool acc_s, int32_t eos,
-                                    float alpha) {
-  const float lp = x - lse;
-  if (t == eos) return acc_s ? lp : -INFINITY;
-  if (z == -INFINITY) return -INFINITY;
-  return alpha != 0.0f ? fmaf(alpha, z, lp) : lp;
-}
-
-constexpr int kOutLoads = 4;          // float4 loads in flight per thread
+constexpr int kOutLoads = 4;          // float4 loads in flight per thread (prior_out_kernel)
 constexpr int kOutLdsClasses = 4096;  // zcls rows up to this size are staged in LDS
 
 // grid (ceil(V / (16 * 256)), rows); each thread rewrites 16 tokens, four
-// float4 groups 256 * 4 tokens apart (coalesced per group).
-template <bool Vec, bool ZInLds>
+// float4 groups 256 * 4 tokens apart (coalesced per group).  Narrow: the
+// class ids come from the uint16 map (half the bytes; 0xFFFF: no class).
+template <bool Vec, bool ZInLds, bool Narrow>
 __global__ __launch_bounds__(kPriorOutThreads) void prior_out_kernel(
     float* __restrict__ logits, int64_t ld, int64_t V, const int32_t* __restrict__ token_class,
-    int32_t C, const float* __restrict__ lse_in, const float* __restrict__ zcls, int32_t S,
+    const uint16_t* __restrict__ token_class16, int32_t C, const float* __restrict__ lse_in, const float* __restrict__ zcls, int32_t S,
     const uint8_t* __restrict__ accept, int32_t eos, const int32_t* __restrict__ states,
     const int64_t* __restrict__ slots, float alpha, int32_t* __restrict__ err) {
   __shared__ float zs[ZInLds ? kOutLdsClasses : 1];
@@ -979,25 +1182,42 @@ __global__ __launch_bounds__(kPriorOutThreads) void prior_out_kernel(
   const bool acc_s = accept[s] != 0;
   auto zof = [&](int32_t c) { return c >= 0 ? z[c] : -INFINITY; };
   if (Vec) {
-    float4 x[kOutLoads];
+    // class ids first (the map is shared by every row and stays in L2),
+    // then the logits only of the groups of four that hold a token with a
+    // finite lookahead value or EOS: every other output is -inf whatever the
+    // logit, so those reads are skipped (a line of rejected tokens is only
+    // written)
     int4 c[kOutLoads];
 #pragma unroll
     for (int u = 0; u < kOutLoads; ++u) {
       const int64_t t = base + (int64_t(u) * kPriorOutThreads + threadIdx.x) * 4;
-      if (t < V) {
-        x[u] = *reinterpret_cast<const float4*>(row + t);
-        c[u] = *reinterpret_cast<const int4*>(token_class + t);
+      if (Narrow) {
+        const uint2 n = t < V ? *reinterpret_cast<const uint2*>(token_class16 + t) : make_uint2(~0u, ~0u);
+        c[u] = make_int4(narrow_class(n.x & 0xFFFFu), narrow_class(n.x >> 16), narrow_class(n.y & 0xFFFFu),
+                         narrow_class(n.y >> 16));
+      } else {
+        c[u] = t < V ? *reinterpret_cast<const int4*>(token_class + t) : make_int4(-1, -1, -1, -1);
       }
+    }
+    float4 zv[kOutLoads];
+    float4 x[kOutLoads];
+#pragma unroll
+    for (int u = 0; u < kOutLoads; ++u) {
+      const int64_t t = base + (int64_t(u) * kPriorOutThreads + threadIdx.x) * 4;
+      zv[u] = make_float4(zof(c[u].x), zof(c[u].y), zof(c[u].z), zof(c[u].w));
+      const bool need = t < V && (zv[u].x != -INFINITY || zv[u].y != -INFINITY || zv[u].z != -INFINITY ||
+                                  zv[u].w != -INFINITY || (eos >= t && eos < t + 4));
+      x[u] = need ? *reinterpret_cast<const float4*>(row + t) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
     for (int u = 0; u < kOutLoads; ++u) {
       const int64_t t = base + (int64_t(u) * kPriorOutThreads + threadIdx.x) * 4;
       if (t < V) {
         float4 o;
-        o.x = prior_value(x[u].x, lse, t, zof(c[u].x), acc_s, eos, alpha);
-        o.y = prior_value(x[u].y, lse, t + 1, zof(c[u].y), acc_s, eos, alpha);
-        o.z = prior_value(x[u].z, lse, t + 2, zof(c[u].z), acc_s, eos, alpha);
-        o.w = prior_value(x[u].w, lse, t + 3, zof(c[u].w), acc_s, eos, alpha);
+        o.x = prior_value(x[u].x, lse, t, zv[u].x, acc_s, eos, alpha);
+        o.y = prior_value(x[u].y, lse, t + 1, zv[u].y, acc_s, eos, alpha);
+        o.z = prior_value(x[u].z, lse, t + 2, zv[u].z, acc_s, eos, alpha);
+        o.w = prior_value(x[u].w, lse, t + 3, zv[u].w, acc_s, eos, alpha);
         *reinterpret_cast<float4*>(row + t) = o;
       }
     }
@@ -1017,6 +1237,17 @@ bool force_pieces() {
   return e && *e && std::strcmp(e, "0") != 0;
 }
 
+// BPD_SOFT_STATS=members / classes selects the 4096-token class statistics
+// (the member lists / the class map) instead of the wave-shift kernel (tests
+// of those paths); BPD_SOFT_MEMBERS=0 selects the class map too
+const char* stats_choice() {
+  const char* e = std::getenv("BPD_SOFT_STATS");
+  if (e && *e) return e;
+  const char* me = std::getenv("BPD_SOFT_MEMBERS");
+  if (me && std::strcmp(me, "0") == 0) return "classes";
+  return "wave";
+}
+
 }  // namespace
 }  // namespace bpd
 
@@ -1026,10 +1257,12 @@ extern "C" size_t bpd_soft_prior_workspace_bytes(int64_t rows, int64_t vocab, in
                                                  int32_t num_pieces) {
   if (rows <= 0 || vocab <= 0) return 0;
   const int32_t C = num_classes > 0 ? num_classes : 0, P = num_pieces > 0 ? num_pieces : 0;
-  // room for either stats path
-  const size_t a = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, false), C, P);
-  const size_t b = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, true), C, P);
-  return a > b ? a : b;
+  // room for every stats path
+  const size_t a = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, false, false), C, P);
+  const size_t b = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, true, false), C, P);
+  const size_t w = prior_ws_bytes(rows, prior_plan(rows, vocab, C, P, false, true), C, P);
+  const size_t m = a > b ? a : b;
+  return m > w ? m : w;
 }
 
 namespace {
@@ -1054,7 +1287,11 @@ int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int3
   BPD_REQUIRE(logits && accept && live && states && workspace && cls.class_off && cls.class_piece &&
                   cls.piece_off && cls.state_off && cls.token_class,
               "null pointer argument");
-  const PriorPlan pl = prior_plan(rows, vocab, cls.num_classes, cls.num_pieces, force_pieces());
+  const char* choice = stats_choice();
+  const bool wide_ok = std::strcmp(choice, "wave") == 0 && cls.token_class16 != nullptr &&
+                       cls.num_classes < 65535 && vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) &&
+                       (reinterpret_cast<uintptr_t>(cls.token_class16) & 7u) == 0;
+  const PriorPlan pl = prior_plan(rows, vocab, cls.num_classes, cls.num_pieces, force_pieces(), wide_ok);
   const bool pieces = !pl.class_stats;
   const bool pairs_in_lds =
       cls.num_classes < 65536 &&
@@ -1075,13 +1312,14 @@ int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int3
                                                                          cls.token_class,       \
                                                                          cls.token_class16,     \
                                                                          cls.num_classes, ws)
-    // BPD_SOFT_MEMBERS=0 keeps the class-map kernel (tests of that path)
-    const char* me = std::getenv("BPD_SOFT_MEMBERS");
     const bool members = vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) && cls.chunk_members != nullptr &&
-                         cls.num_classes < 65535 && !(me && std::strcmp(me, "0") == 0) &&
+                         cls.num_classes < 65535 && std::strcmp(choice, "classes") != 0 &&
                          (cls.chunk_cap == 256 || cls.chunk_cap == 512 || cls.chunk_cap == 1024);
     const size_t mlds = size_t(kStatChunk) * sizeof(float) + size_t(cls.num_classes) * 8;
-    if (members && cls.chunk_cap == 256)
+    if (pl.wide)
+      prior_stats_wave_kernel<<<grid, kPriorThreads, size_t(cls.num_classes) * (kPriorThreads / 64 + 2) * 4, st>>>(
+          logits, ld, vocab, cls.token_class16, cls.num_classes, ws);
+    else if (members && cls.chunk_cap == 256)
       prior_stats_members_kernel<256><<<grid, kPriorThreads, mlds, st>>>(logits, ld, vocab, cls.chunk_members, cls.num_classes, ws);
     else if (members && cls.chunk_cap == 512)
       prior_stats_members_kernel<512><<<grid, kPriorThreads, mlds, st>>>(logits, ld, vocab, cls.chunk_members, cls.num_classes, ws);
@@ -1116,14 +1354,18 @@ int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int3
                                    (4 * kOutLoads * kPriorOutThreads)),
                           unsigned(rows));
   const bool z_lds = cls.num_classes <= kOutLdsClasses;
-#define BPD_PRIOR_OUT(VEC, ZL)                                                                   \
-  prior_out_kernel<VEC, ZL><<<ogrid, kPriorOutThreads, 0, st>>>(                               \
-      logits, ld, vocab, cls.token_class, cls.num_classes, ws.lse, ws.zcls, num_states, accept, \
-      eos_id, states, slots, alpha, err)
-  if (vec && z_lds) BPD_PRIOR_OUT(true, true);
-  else if (vec) BPD_PRIOR_OUT(true, false);
-  else if (z_lds) BPD_PRIOR_OUT(false, true);
-  else BPD_PRIOR_OUT(false, false);
+  const bool onarrow = vec && cls.token_class16 != nullptr && cls.num_classes < 65535 &&
+                       (reinterpret_cast<uintptr_t>(cls.token_class16) & 7u) == 0;
+#define BPD_PRIOR_OUT(VEC, ZL, NW)                                                                \
+  prior_out_kernel<VEC, ZL, NW><<<ogrid, kPriorOutThreads, 0, st>>>(                            \
+      logits, ld, vocab, cls.token_class, cls.token_class16, cls.num_classes, ws.lse, ws.zcls,   \
+      num_states, accept, eos_id, states, slots, alpha, err)
+  if (onarrow && z_lds) BPD_PRIOR_OUT(true, true, true);
+  else if (onarrow) BPD_PRIOR_OUT(true, false, true);
+  else if (vec && z_lds) BPD_PRIOR_OUT(true, true, false);
+  else if (vec) BPD_PRIOR_OUT(true, false, false);
+  else if (z_lds) BPD_PRIOR_OUT(false, true, false);
+  else BPD_PRIOR_OUT(false, false, false);
 #undef BPD_PRIOR_OUT
   BPD_LAUNCHED();
   return BPD_OK;
