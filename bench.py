@@ -346,14 +346,19 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
                 run.batch.prepare(ids)
             if flush64 is not None:
                 flush64.sum()
-            h0 = time.perf_counter()
             ev.record(2 * k, sh)
+            h0 = time.perf_counter()
             run.batch.apply_mask(ids, run.logits)
             nxt = run.batch.commit(ids, tokens[k])
+            host_s.append(time.perf_counter() - h0)  # the two calls only, not the event records
             ev.record(2 * k + 1, sh)
-            host_s.append(time.perf_counter() - h0)
             agree &= (nxt == nxt_ref[k]).all()
             run.churn_step()
+            if mode == "api":
+                # a serving loop waits for each step's tokens; without this the
+                # host runs ~100 steps ahead, the hardware queue fills and the
+                # launches inside the calls wait for the device
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         res[f"{mode}_ms"] = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in timed]
         res[f"{mode}_host_s"] = host_s[warmup:]

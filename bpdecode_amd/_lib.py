@@ -90,6 +90,7 @@ _SIGNATURES = {
     "bpd_host_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, cint, i64, vp, cint]),
     "bpd_host_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp]),
     "bpd_host_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp]),
+    "bpd_stage_int64": (cint, [vp, vp, i64, vp]),
     "bpd_pda_init": (cint, [C.POINTER(PdaTableC), vp]),
     "bpd_pda_feed": (cint, [C.POINTER(PdaTableC), vp, C.c_char_p, i64]),
     "bpd_pda_workspace_bytes": (sz, [i64, i32]),

@@ -11,6 +11,8 @@ applies them itself, so per-request churn costs no launch of its own.
 
 from __future__ import annotations
 
+import array
+import operator
 from collections import OrderedDict, defaultdict
 from collections.abc import Hashable, Sequence
 
@@ -110,13 +112,21 @@ class GrammarCache:
         return len(self._cache)
 
 
+def _stage(values: array.array, device: torch.device) -> torch.Tensor:
+    """int64 device tensor holding ``values`` (one native staged copy on the
+    current stream; ``values`` may change once this returns)."""
+    out = torch.empty(len(values), dtype=torch.int64, device=device)
+    if len(values):
+        addr, n = values.buffer_info()
+        check(lib().bpd_stage_int64(out.data_ptr(), addr, n, _lib.stream_of(device)))
+    return out
+
+
 def index_tensor(values: Sequence[int], device: torch.device) -> torch.Tensor:
-    """int64 tensor of ``values`` on ``device`` (pinned staging for a device)."""
+    """int64 tensor of ``values`` on ``device``."""
     if device.type != "cuda":
         return torch.tensor(values, dtype=torch.long)
-    host = torch.empty(len(values), dtype=torch.long, pin_memory=True)
-    host.numpy()[:] = values
-    return host.to(device, non_blocking=True)
+    return _stage(array.array("q", values), device)
 
 
 _DENSE_CODES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16,
@@ -164,6 +174,8 @@ class ConstraintBatch:
             self._W = int(bits.shape[1])
             self._tn_ptr, self._bits_ptr = tn.data_ptr(), bits.data_ptr()
             self._pool_ptr, self._err_ptr = self._pool.data_ptr(), self._err.data_ptr()
+            self._f_mask = lib().bpd_dense_apply_mask_bits
+            self._f_advance = lib().bpd_dense_advance
 
     # --- pool -----------------------------------------------------------
     def _unstage(self) -> None:
@@ -241,10 +253,16 @@ class ConstraintBatch:
         """int64 slot per row on the device (uploaded when the ids or the
         slot map changed)."""
         if not self._same_ids(seq_ids):
-            slot_of = self._slot_of
-            vals = [slot_of[s] for s in seq_ids]
+            vals = self._lookup(seq_ids)
             self._remember(seq_ids, vals, index_tensor(vals, self.device))
         return self._slot_tensor
+
+    def _lookup(self, seq_ids: Sequence[Hashable]) -> list | tuple:
+        """Slot of each id (one C-level pass over the ids)."""
+        n = len(seq_ids)
+        if n > 1:
+            return operator.itemgetter(*seq_ids)(self._slot_of)
+        return [self._slot_of[s] for s in seq_ids]
 
     def _slots_fused(self, seq_ids: Sequence[Hashable], fuse: bool):
         """(slots, pending tensor or None, count) for a device launch.  With
@@ -267,15 +285,13 @@ class ConstraintBatch:
         if self._same_ids(seq_ids):
             vals = self._slot_vals
         else:
-            slot_of = self._slot_of
-            vals = [slot_of[s] for s in seq_ids]
+            vals = self._lookup(seq_ids)
         B = len(vals)
-        host = torch.empty(B + 2 * n, dtype=torch.int64, pin_memory=True)
-        arr = host.numpy()
-        arr[:B] = vals
-        arr[B:B + n] = list(self._pending.keys())
-        arr[B + n:] = list(self._pending.values())
-        dev = host.to(self.device, non_blocking=True)
+        # one upload of [slots | queued slots | queued values]
+        arr = array.array("q", vals)
+        arr.extend(self._pending.keys())
+        arr.extend(self._pending.values())
+        dev = _stage(arr, self.device)
         self._remember(seq_ids, vals, dev[:B])
         self._staged = (dev[:B], dev[B:], n)
         self._staged_pending = self._pending
@@ -309,7 +325,7 @@ class ConstraintBatch:
             B = len(seq_ids)
             slots, pend, n = self._slots_fused(seq_ids, True)
             ld = logits.stride(0) if B > 1 else self._V
-            check(lib().bpd_dense_apply_mask_bits(
+            check(self._f_mask(
                 logits.data_ptr(), code, B, self._V, ld, self._bits_ptr, self._W, self._S,
                 self._pool_ptr, slots.data_ptr(), None if pend is None else pend.data_ptr(), n,
                 float(neg_inf), self._err_ptr, _lib.stream_of(self.device)))
@@ -369,7 +385,7 @@ class ConstraintBatch:
             if code is not None:
                 slots, pend, n = self._slots_fused(seq_ids, B <= _COMMIT_FUSED_ROWS)
                 out = torch.empty(B, dtype=torch.int32, device=self.device)
-                check(lib().bpd_dense_advance(
+                check(self._f_advance(
                     self._tn_ptr, self._S, self._V, self._pool_ptr, slots.data_ptr(),
                     None if pend is None else pend.data_ptr(), n, tokens.data_ptr(), code, B,
                     out.data_ptr(), 1, self._err_ptr, _lib.stream_of(self.device)))

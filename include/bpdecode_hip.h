@@ -200,6 +200,15 @@ int bpd_host_build_tok_next(const int32_t* trans, int32_t num_states, int32_t nu
                             int64_t vocab, int32_t eos_id, const int32_t* row_states,
                             int32_t num_rows, int32_t* out);
 
+/* bpd_stage_int64: enqueue a copy of n int64 values from host memory `src`
+ * (any memory; free to change once the call returns) to device memory `dst`
+ * on `stream`, through a per-stream ring of pinned buffers (a buffer is
+ * reused once the copy that last read it has completed).  The per-step
+ * upload of slot lists and queued pool writes; no counterpart in the
+ * reference, whose batch classes build a device tensor per call
+ * (batch.py:176-190, 206-215). */
+int bpd_stage_int64(int64_t* dst, const int64_t* src, int64_t n, void* stream);
+
 /* ------------------------------------------------------------------ PDA --
  * Flattened grammar (grammar/device.py:79-158, pda.hpp:46-69): every rule's
  * NFA in one global state space plus a CSR edge list.  The same struct
