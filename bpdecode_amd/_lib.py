@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
@@ -52,7 +52,7 @@ class PdaFramesC(C.Structure):
 
 class TokenBytesC(C.Structure):
     _fields_ = [("vocab_size", i32), ("eos_id", i32), ("offsets", vp), ("bytes", vp), ("order", vp),
-                ("runs", vp), ("frames", C.POINTER(PdaFramesC))]
+                ("runs", vp), ("frames", C.POINTER(PdaFramesC)), ("pack_tag", C.c_uint64)]
 
 
 class FsaTableC(C.Structure):

@@ -50,7 +50,7 @@ using namespace bpd;
 
 extern "C" const char* bpd_last_error(void) { return g_error; }
 
-extern "C" int bpd_abi_version(void) { return 6; }
+extern "C" int bpd_abi_version(void) { return 7; }
 
 extern "C" int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab,
                                          int64_t ld, const int32_t* tok_next,

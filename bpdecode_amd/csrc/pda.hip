@@ -41,6 +41,7 @@ struct MaskArgs {
   uint8_t* logits;  // null when writing bits
   int64_t ld_bytes;
   int32_t elem;
+  int32_t vec_store;  // logits and ld_bytes aligned to 4 columns
   uint32_t fill;
   uint32_t* bits;  // null when writing logits
   int64_t words;
@@ -180,14 +181,21 @@ constexpr int kMemoMaxVocab = 262144;  // verdict bitmap of a row in LDS
 constexpr uint8_t kTUnknown = 0xFE;
 constexpr uint8_t kTDead = 0xFF;
 constexpr uint8_t kTOverflow = 0xFD;
+// In the table kept for the commit, an entry with kTExact set is an id whose
+// interned set has the raw words the step itself gives; ids stay below
+// kMemoIds so that no flagged id reaches the special entries.
+constexpr uint8_t kTExact = 0x80;
+constexpr int kMemoIds = 125;
 
 struct MemoWs {
-  uint32_t* header;   // [64]: word 0 = generation of the last mask launch on this workspace
+  uint32_t* header;   // [64]: word 0 = generation of the last mask launch on this workspace,
+                      // words 2-3 = pack key of the token records it walked (0: none)
   int32_t* pool;      // [rows, kMemoSets, kConfigWords]
   int32_t* cand;      // [rows, kMemoReq, kConfigWords]
   int32_t* overflow;  // [rows]
   int32_t* meta;      // [rows, 4]: valid, tag low, tag high, generation
   uint32_t* table;    // [rows, kMemoSets * 64]: the row's transition table after the mask
+                      // (ids flagged kTExact where the step's raw words are the set's)
   uint4* recs;        // [vocab] first 16 bytes of the token at walk position k, zero padded
   int2* tmeta;        // [vocab] (token id, length) of the token at walk position k
   uint2* queue;       // [rows, 2, vocab] paused tokens of the row-wide walk (two buffers)
@@ -252,14 +260,34 @@ uint64_t memo_tag(const BpdPdaTable* g, const BpdTokenBytes* toks, int64_t rows)
   return h;
 }
 
+// Key of the token records a launch packs: the caller's content tag of the
+// token tables, the row count (the records' place in the workspace depends
+// on it), the vocabulary and whether a walk order is given.  0 (never
+// skipped) when the caller gives no tag.
+uint64_t pack_key(const BpdTokenBytes* toks, int64_t rows) {
+  if (toks->pack_tag == 0) return 0;
+  uint64_t h = 1469598103934665603ull ^ toks->pack_tag;
+  auto mix = [&](uint64_t x) { h = (h ^ x) * 1099511628211ull; };
+  mix(uint64_t(rows));
+  mix(uint64_t(uint32_t(toks->vocab_size)));
+  mix(toks->order ? 1u : 0u);
+  return h ? h : 1;
+}
+
 // Token records in walk order (k -> t = order[k], or t = k): recs[k] = the
 // first 16 bytes of t (little-endian words, zero padded), meta[k] = (t,
-// length of t), so the walks read them coalesced.
+// length of t), so the walks read them coalesced.  Nothing to do when the
+// workspace header carries this launch's pack key: the last mask launch on
+// the workspace walked records of the same tables at the same place, and
+// nothing but a pack writes there.
 __global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restrict__ off,
                                                           const uint8_t* __restrict__ bytes,
                                                           const int32_t* __restrict__ order,
                                                           int32_t vocab, uint4* __restrict__ recs,
-                                                          int2* __restrict__ meta) {
+                                                          int2* __restrict__ meta,
+                                                          const uint32_t* __restrict__ header,
+                                                          uint64_t key) {
+  if (key != 0 && header[2] == uint32_t(key) && header[3] == uint32_t(key >> 32)) return;
   const int32_t k = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x);
   if (k >= vocab) return;
   const int32_t t = order ? order[k] : k;
@@ -322,6 +350,7 @@ __device__ inline void wave_sync() {
 }
 
 constexpr int kF = 2 + kMaxConfigs;  // first frame word
+constexpr int kSetLoads = (kConfigWords + kWave - 1) / kWave;  // words of a set per lane
 
 __device__ inline bool coop_holds(const int32_t* dst, const int32_t* src, int i, int keep, int x0,
                                   int x1, int nx, int lane) {
@@ -481,22 +510,30 @@ __device__ uint32_t coop_hash(const int32_t* c, int lane) {
   return h;
 }
 
-// Equal meaningful words (x in LDS, y anywhere); every lane gets the answer.
-__device__ bool coop_same(const int32_t* x, const int32_t* y, int lane) {
+// Equal meaningful words (x in LDS, y anywhere); every lane gets the answer,
+// and `raw` whether every word is equal.  One pass over the words: n and the
+// saturation flag are words 0 and 1, the depths words 2..9, so a frame is
+// compared where it is meaningful in x once those are equal.
+__device__ bool coop_same_raw(const int32_t* x, const int32_t* y, int lane, bool& raw) {
   const int n = x[0];
-  if (n != y[0] || x[1] != y[1]) return false;
-  bool diff = false;
+  bool diff = false, rdiff = false;
   for (int w = lane; w < kConfigWords; w += kWave) {
+    const bool ne = x[w] != y[w];
+    rdiff |= ne;
     if (w < kF) {
-      diff |= (w >= 2 && w - 2 < n && x[w] != y[w]);
+      diff |= ne && (w < 2 || w - 2 < n);
     } else {
       const int i = (w - kF) / kMaxDepth, k = (w - kF) % kMaxDepth;
-      // depths are compared by lanes 2..9 above; a frame is compared where
-      // it is meaningful in x
-      diff |= (i < n && k < x[2 + i] && x[w] != y[w]);
+      diff |= ne && i < n && k < x[2 + i];
     }
   }
+  raw = __ballot(rdiff) == 0;
   return __ballot(diff) == 0;
+}
+
+__device__ inline bool coop_same(const int32_t* x, const int32_t* y, int lane) {
+  bool raw;
+  return coop_same_raw(x, y, lane, raw);
 }
 
 // Elementary byte intervals of a set, from its top states: advance_byte
@@ -624,7 +661,8 @@ constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
                                                                      int table_in_lds, uint64_t tag,
-                                                                     uint32_t gen, int row_mode) {
+                                                                     uint32_t gen, int row_mode,
+                                                                     uint64_t pkey) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
@@ -635,11 +673,13 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ uint32_t T32[kMemoSets * 256 / 4];
   __shared__ uint32_t vbits[kMemoMaxVocab / 32];  // allowed tokens of the row
   __shared__ uint32_t req[kMemoSets * 8];
+  __shared__ uint32_t texact[kMemoSets * 8];  // entries whose step gives the set's raw words
   __shared__ uint32_t pool_hash[kMemoSets];
   __shared__ int32_t req_list[kMemoReq];
   __shared__ uint32_t cand_hash[kMemoReq];
   __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new, -4 duplicate, -5 no edge
   __shared__ int32_t cand_lead[kMemoReq];
+  __shared__ uint8_t cand_exact[kMemoReq];  // an existing set with every word of the step's
   __shared__ int32_t cand_list[kMemoReq];  // frame list of a new set (| BPD_PDA_FRAME_SAT), -1 none
   __shared__ int32_t fkeys[BPD_PDA_MAX_FRAME_LISTS * BPD_PDA_FRAME_KEY_WORDS];
   __shared__ int32_t cand_id[kMemoReq];
@@ -651,9 +691,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ uint32_t h0_sh;
   __shared__ uint8_t loop0[256];  // T[0][c] == 0: byte c keeps set 0 (row-wide walk)
   // first pass of the row-wide walk: pass index i -> walk position
-  __shared__ int32_t grp_pre[258];    // runs: exclusive prefix of the live runs' lengths
-  __shared__ int32_t grp_start[257];  // runs: first walk position of each run
-  __shared__ int pass_mode, pass_list, pass_total, pass_base;
+  __shared__ int32_t grp_pre[258];    // runs: exclusive prefix of the live runs' lengths, then the total
+  __shared__ int32_t grp_start[257];  // runs: first walk position of each live run
+  __shared__ int pass_mode, pass_list, pass_total, pass_base, run_n, run_top;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
   const int tid = threadIdx.x;
@@ -661,6 +701,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   const int64_t row = a.slots ? a.slots[b] : b;
   int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
   int32_t* cand = ws.cand + b * kMemoReq * kConfigWords;
+  if (b == 0 && tid == 0) {
+    // the records this launch walks (the pack before it has finished)
+    ws.header[2] = uint32_t(pkey);
+    ws.header[3] = uint32_t(pkey >> 32);
+  }
 
   for (int k = tid; k < kConfigWords; k += kMemoThreads) row_cfg[k] = a.configs[row * kConfigWords + k];
   PdaTableView g = a.g;
@@ -699,7 +744,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   for (int i = tid; i < a.frames.num_lists * BPD_PDA_FRAME_KEY_WORDS; i += kMemoThreads) fkeys[i] = a.frames.keys[i];
   const int32_t vwords = (a.vocab + 31) / 32;
   for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
-  for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0;
+  for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) {
+    req[i] = 0;
+    texact[i] = 0;
+  }
   if (tid == 0) {
     pool_count = 1;
     overflowed = 0;
@@ -785,15 +833,37 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       const int lane = tid & (kWave - 1), wave = tid / kWave;
       int32_t* wsrc = work[wave][0];
       int32_t* wdst = work[wave][1];
-      for (int r = wave; r < n; r += kMemoThreads / kWave) {
-        if (cand_res[r] < -3) continue;
-        const int set = req_list[r] >> 8, byte = req_list[r] & 255;
-        // set 0 is the row's own set, already in LDS
+      // the wave's requests r = wave, wave + 16, ... that compute; the
+      // source set of the next one is loaded into registers while the
+      // current one is computed (set 0, the row's own set, is in LDS)
+      auto next_req = [&](int r) {
+        while (r < n && cand_res[r] < -3) r += kMemoThreads / kWave;
+        return r;
+      };
+      int32_t words[kSetLoads];
+      auto load_src = [&](int r) {
+        const int set = r < n ? req_list[r] >> 8 : 0;
         const int32_t* ps = pool + set * kConfigWords;
+#pragma unroll
+        for (int q = 0; q < kSetLoads; ++q) {
+          const int k = lane + q * kWave;
+          words[q] = set != 0 && k < kConfigWords ? ps[k] : 0;
+        }
+      };
+      int r = next_req(wave);
+      load_src(r);
+      while (r < n) {
+        const int set = req_list[r] >> 8, byte = req_list[r] & 255;
         if (set != 0) {
-          for (int k = lane; k < kConfigWords; k += kWave) wsrc[k] = ps[k];
+#pragma unroll
+          for (int q = 0; q < kSetLoads; ++q) {
+            const int k = lane + q * kWave;
+            if (k < kConfigWords) wsrc[k] = words[q];
+          }
           wave_sync();
         }
+        const int r_next = next_req(r + kMemoThreads / kWave);
+        load_src(r_next);
         const bool ok = coop_advance_byte(g, set != 0 ? wsrc : row_cfg, wdst, byte, lane);
         if (!ok) {
           if (lane == 0) cand_res[r] = -1;
@@ -802,13 +872,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           // the first pool set with this hash and these meaningful words;
           // hashes compared 64 at a time
           int found = -2;
+          bool raw = false;
           const int pc = pool_count < max_sets ? pool_count : max_sets;
           for (int k0 = 0; k0 < pc && found < 0; k0 += kWave) {
             uint64_t m = __ballot(k0 + lane < pc && pool_hash[k0 + lane] == h);
             while (m != 0u && found < 0) {
               const int k = k0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
               m &= m - 1;
-              if (coop_same(wdst, pool + k * kConfigWords, lane)) found = k;
+              if (coop_same_raw(wdst, pool + k * kConfigWords, lane, raw)) found = k;
             }
           }
           if (lane < kMaxConfigs) {
@@ -829,9 +900,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           if (lane == 0) {
             cand_hash[r] = h;
             cand_res[r] = found;
+            cand_exact[r] = found >= 0 && raw ? 1 : 0;
           }
         }
         wave_sync();
+        r = r_next;
       }
     }
     __syncthreads();
@@ -890,13 +963,29 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
         const int lo = cand_lo[r], hi = cand_hi[r];
         for (int c = lo + lane; c <= hi; c += kWave) T[set * 256 + c] = e;
+        // the interval's step gives the set's raw words: a new set (its
+        // first computation) or an existing one equal in every word
+        const bool exact = (res >= 0 && cand_exact[r]) || (res == -2 && cand_lead[r] == r && id >= 0);
+        if (exact && lane >= (lo >> 5) && lane <= (hi >> 5)) {
+          const int b0 = (lo > lane * 32 ? lo : lane * 32) - lane * 32;
+          const int b1 = (hi < lane * 32 + 31 ? hi : lane * 32 + 31) - lane * 32;
+          const uint32_t upto = b1 == 31 ? 0xFFFFFFFFu : ((1u << (b1 + 1)) - 1u);
+          atomicOr(&texact[set * 8 + lane], upto & ~((1u << b0) - 1u));
+        }
         if (lane == 0 && res != -5) atomicAnd(&req[set * 8 + (lo >> 5)], ~(1u << (lo & 31)));
       }
       for (int r = wave; r < n; r += kMemoThreads / kWave) {
         if (cand_res[r] != -2 || cand_lead[r] != r || cand_id[r] < 0) continue;
+        // the set's words are loaded first and stored last, so the load
+        // waits behind the interval and frame-list work
         const int32_t* src = cand + r * kConfigWords;
         int32_t* dst = pool + cand_id[r] * kConfigWords;
-        for (int k = lane; k < kConfigWords; k += kWave) dst[k] = src[k];
+        int32_t words[kSetLoads];
+#pragma unroll
+        for (int q = 0; q < kSetLoads; ++q) {
+          const int k = lane + q * kWave;
+          words[q] = k < kConfigWords ? src[k] : 0;
+        }
         coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]],
                            T + cand_id[r] * 256, lane);
         const int cl = cand_list[r];
@@ -904,6 +993,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           wave_sync();
           frame_fill_row(a.frames, cl & (BPD_PDA_FRAME_SAT - 1), (cl & BPD_PDA_FRAME_SAT) != 0, cand_id[r],
                          T + cand_id[r] * 256, lane);
+        }
+#pragma unroll
+        for (int q = 0; q < kSetLoads; ++q) {
+          const int k = lane + q * kWave;
+          if (k < kConfigWords) dst[k] = words[q];
         }
       }
     }
@@ -913,6 +1007,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   // Empty the pool back to the row's own set (set 0) and T to "unknown".
   auto reset_pool = [&]() {
     for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
+    for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) texact[i] = 0u;
     for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
     if (tid < kMaxConfigs) {
       const int n0 = row_cfg[0];
@@ -1072,37 +1167,43 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     } else if (a.runs && !dead_row && !overflowed && tid < kWave) {
       // first-byte runs: the run of byte c is walked unless the byte
       // empties set 0 (T[0][c] dead); lane l owns runs 4l..4l+3, lane 63
-      // also the run of EOS and the empty tokens
-      int cnt[4], st[4], sum = 0;
+      // also the run of EOS and the empty tokens.  Only the live runs are
+      // listed (the pass searches them), in byte order, then the total.
+      int cnt[5], st[5], sum = 0, live = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = 4 * tid + q;
-        const int64_t b0 = a.runs[c], b1 = c < 255 ? a.runs[c + 1] : a.runs[256];
+      for (int q = 0; q < 5; ++q) {
+        const int c = q < 4 ? 4 * tid + q : 256;
+        const int64_t b0 = a.runs[c], b1 = c < 255 ? a.runs[c + 1] : (c == 255 ? a.runs[256] : V);
         const int64_t lo = b0 < 0 ? 0 : (b0 > V ? V : b0);
         const int64_t hi = b1 < lo ? lo : (b1 > V ? V : b1);
         st[q] = int(lo);
-        cnt[q] = T[c] == kTDead ? 0 : int(hi - lo);
+        cnt[q] = (q == 4 && tid != kWave - 1) || (c < 256 && T[c] == kTDead) ? 0 : int(hi - lo);
         sum += cnt[q];
+        live += cnt[q] > 0 ? 1 : 0;
       }
-      int incl = sum;
+      int incl = sum, incl_live = live;
       for (int o = 1; o < kWave; o <<= 1) {
-        const int y = __shfl_up(incl, o);
-        if (tid >= o) incl += y;
+        const int y = __shfl_up(incl, o), z = __shfl_up(incl_live, o);
+        if (tid >= o) {
+          incl += y;
+          incl_live += z;
+        }
       }
-      int ex = incl - sum;
+      int ex = incl - sum, li = incl_live - live;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        grp_pre[4 * tid + q] = ex;
-        grp_start[4 * tid + q] = st[q];
-        ex += cnt[q];
+      for (int q = 0; q < 5; ++q) {
+        if (cnt[q] > 0) {
+          grp_pre[li] = ex;
+          grp_start[li] = st[q];
+          ++li;
+          ex += cnt[q];
+        }
       }
       if (tid == kWave - 1) {
-        const int64_t b0 = a.runs[256];
-        const int64_t lo = b0 < 0 ? 0 : (b0 > V ? V : b0);
-        grp_pre[256] = incl;
-        grp_start[256] = int(lo);
-        grp_pre[257] = incl + int(V - lo);
-        pass_total = incl + int(V - lo);
+        grp_pre[li] = ex;
+        run_n = li;
+        run_top = li > 1 ? 1 << (31 - __clz(li - 1)) : 0;
+        pass_total = ex;
         pass_mode = 1;
       }
     }
@@ -1112,20 +1213,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     const bool scan = loop_n >= 32;
     const int mode = pass_mode;
     const int64_t P = pass_total;
-    // walk position of pass index i (< P); -1 for a seed out of range
-    auto pass_pos = [&](int64_t i) -> int32_t {
-      if (mode == 0) return int32_t(i);
-      if (mode == 2) {
-        const int32_t k = a.frames.seeds[pass_base + i];
-        return k >= 0 && k < V ? k : -1;
-      }
-      int lo = 0, hi = 256;  // the last run whose prefix is <= i
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (grp_pre[mid] <= i) lo = mid; else hi = mid - 1;
-      }
-      return grp_start[lo] + int32_t(i - grp_pre[lo]);
-    };
+    const int rn = run_n, rtop = run_top;
     if (!overflowed) {
       // the records of the next tile are loaded while this one is walked;
       // queue entries are stored after all four walks of a tile
@@ -1133,13 +1221,43 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       int2 nm[kMemoTok];
       uint4 npk[kMemoTok];
       int32_t nk[kMemoTok];
+      // walk positions of pass indices base + j * kMemoThreads + tid (-1
+      // past the pass or for a seed out of range) and their records.  Over
+      // the live runs, the last run whose prefix is <= i is found by binary
+      // lifting, the four searches of a thread interleaved (one LDS wait per
+      // step); the total after the last run stops every step at it.
+      auto prefetch = [&](int64_t base) {
+        int32_t ii[kMemoTok], lo[kMemoTok];
 #pragma unroll
-      for (int j = 0; j < kMemoTok; ++j) {
-        const int64_t i = int64_t(j) * kMemoThreads + tid;
-        nk[j] = i < P ? pass_pos(i) : -1;
-        nm[j] = nk[j] >= 0 ? ws.tmeta[nk[j]] : make_int2(-1, 0);
-        npk[j] = nk[j] >= 0 ? ws.recs[nk[j]] : make_uint4(0u, 0u, 0u, 0u);
-      }
+        for (int j = 0; j < kMemoTok; ++j) {
+          const int64_t i = base + int64_t(j) * kMemoThreads + tid;
+          ii[j] = i < P ? int32_t(i) : -1;
+          lo[j] = 0;
+        }
+        if (mode == 1) {
+          for (int stp = rtop; stp > 0; stp >>= 1) {
+#pragma unroll
+            for (int j = 0; j < kMemoTok; ++j) {
+              const int m = lo[j] + stp < rn ? lo[j] + stp : rn;
+              if (grp_pre[m] <= ii[j]) lo[j] = m;
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          int32_t k = ii[j];
+          if (k >= 0 && mode == 1) {
+            k = grp_start[lo[j]] + (k - grp_pre[lo[j]]);
+          } else if (k >= 0 && mode == 2) {
+            k = a.frames.seeds[pass_base + k];
+            k = k >= 0 && k < V ? k : -1;
+          }
+          nk[j] = k;
+          nm[j] = k >= 0 ? ws.tmeta[k] : make_int2(-1, 0);
+          npk[j] = k >= 0 ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
+        }
+      };
+      prefetch(0);
       for (int64_t tile = 0; tile < P; tile += kTile) {
         int32_t tt[kMemoTok], pos[kMemoTok], len[kMemoTok], kk[kMemoTok];
         int cur[kMemoTok];
@@ -1163,13 +1281,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             cur[j] = len[j] == 0 ? ((flags & 4) ? kAllowed : kRejected) : 0;
           }
         }
-#pragma unroll
-        for (int j = 0; j < kMemoTok; ++j) {
-          const int64_t i = tile + kTile + int64_t(j) * kMemoThreads + tid;
-          nk[j] = i < P ? pass_pos(i) : -1;
-          nm[j] = nk[j] >= 0 ? ws.tmeta[nk[j]] : make_int2(-1, 0);
-          npk[j] = nk[j] >= 0 ? ws.recs[nk[j]] : make_uint4(0u, 0u, 0u, 0u);
-        }
+        prefetch(tile + kTile);
         // the leading bytes that keep set 0 (a string loop's body) are
         // checked together, with independent table reads, and the walk
         // starts at the first other byte
@@ -1325,7 +1437,16 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __syncthreads();
   // keep the transition table for the commit of this step
   uint32_t* tout = ws.table + b * (kMemoSets * 64);
-  for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) tout[i] = T32[i];
+  for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) {
+    const uint32_t v = T32[i];
+    const int c = (i & 63) * 4;
+    const uint32_t nib = (texact[(i >> 6) * 8 + (c >> 5)] >> (c & 31)) & 0xFu;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (((nib >> j) & 1u) != 0u && ((v >> (8 * j)) & 0xFFu) < kTOverflow) m |= uint32_t(kTExact) << (8 * j);
+    tout[i] = v | m;
+  }
   if (tid == 0) {
     ws.overflow[b] = overflowed;
     ws.meta[b * 4 + 0] = dead_row ? 0 : 1;
@@ -1346,6 +1467,31 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   uint8_t* rowp = a.logits + b * a.ld_bytes;
   const int lane = tid & (kWave - 1);
   const uint16_t fill16 = uint16_t(a.fill & 0xFFFFu);
+  if (a.vec_store) {
+    // four consecutive columns per lane (256 per wave and step, one nibble
+    // of a verdict word): four rejected columns are one 16-byte (fp32) or
+    // 8-byte (16-bit) store, a mixed group stores its rejected columns
+    const uint32_t f2 = uint32_t(fill16) | (uint32_t(fill16) << 16);
+    for (int64_t c = int64_t(tid) * 4; c < V; c += int64_t(kMemoThreads) * 4) {
+      const uint32_t nib = (vbits[c >> 5] >> (c & 31)) & 0xFu;
+      if (nib == 0u && c + 4 <= V) {
+        if (a.elem == 2)
+          *reinterpret_cast<uint2*>(rowp + c * 2) = make_uint2(f2, f2);
+        else
+          *reinterpret_cast<uint4*>(rowp + c * 4) = make_uint4(a.fill, a.fill, a.fill, a.fill);
+      } else {
+        for (int j = 0; j < 4; ++j) {
+          if (c + j < V && ((nib >> j) & 1u) == 0u) {
+            if (a.elem == 2)
+              *reinterpret_cast<uint16_t*>(rowp + (c + j) * 2) = fill16;
+            else
+              *reinterpret_cast<uint32_t*>(rowp + (c + j) * 4) = a.fill;
+          }
+        }
+      }
+    }
+    return;
+  }
   for (int64_t c0 = int64_t(tid - lane); c0 < V; c0 += kMemoThreads) {
     const int64_t c = c0 + lane;
     const bool rejected = c < V && ((vbits[c >> 5] >> (c & 31)) & 1u) == 0u;
@@ -1467,11 +1613,18 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
     const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
     ok = true;
     if (s < e) {
-      // walk the mask's table over the bytes but the last while it has the
-      // entries; then step the rest (at least the last byte) with
-      // advance_byte from the interned set reached, so the written
-      // config-set has the raw words of the direct walk
-      int cur = -1;  // -1: no usable table, step every byte from the row's set
+      // the token's first 64 bytes, one per lane
+      const int32_t bl = s + lane < e ? int32_t(a.tok_bytes[s + lane]) : 0;
+      auto byte_at = [&](int32_t i) -> int {
+        return i - s < kWave ? __shfl(bl, int(i - s)) : int(a.tok_bytes[i]);
+      };
+      // walk the mask's table while it has the entries.  A step's raw words
+      // depend only on the meaningful words of the set it starts from, so
+      // when the last byte's entry is flagged exact the interned set is the
+      // written config-set; otherwise the rest (at least the last byte) is
+      // stepped with advance_byte from the interned set reached
+      int cur = -1, prev = -1;  // -1: no usable table, step every byte from the row's set
+      bool exact = false;
       int32_t i = s;
       const int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
       if (ws.pool && ws.meta[b * 4] == 1 && ws.meta[b * 4 + 1] == int32_t(uint32_t(tag)) &&
@@ -1479,25 +1632,33 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
           uint32_t(ws.meta[b * 4 + 3]) == ws.header[0] && coop_same(x, pool, lane)) {
         const uint8_t* T = reinterpret_cast<const uint8_t*>(ws.table + b * (kMemoSets * 64));
         cur = 0;
-        for (; i + 1 < e; ++i) {
-          const uint8_t nx = T[cur * 256 + a.tok_bytes[i]];
+        for (; i < e; ++i) {
+          const uint8_t nx = T[cur * 256 + byte_at(i)];
           if (nx == kTDead) {
             cur = -2;
             break;
           }
           if (nx >= kTOverflow) break;  // not resolved by the mask: step from here
-          cur = nx;
+          prev = cur;
+          cur = nx & (kTExact - 1);
+          exact = (nx & kTExact) != 0;
         }
       }
       if (cur == -2) {
         ok = false;
+      } else if (cur >= 0 && i == e && exact) {
+        for (int k = lane; k < kConfigWords; k += kWave) cfg[k] = pool[cur * kConfigWords + k];
       } else {
+        if (cur >= 0 && i == e) {
+          cur = prev;  // every byte had its entry: step the last one again
+          i = e - 1;
+        }
         if (cur > 0) {
           for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[cur * kConfigWords + k];
           wave_sync();
         }
         for (; i < e && ok; ++i) {
-          ok = coop_advance_byte(a.g, x, y, a.tok_bytes[i], lane);
+          ok = coop_advance_byte(a.g, x, y, byte_at(i), lane);
           int32_t* tmp = x;
           x = y;
           y = tmp;
@@ -1622,6 +1783,8 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     a.fill = fill;
     a.logits = static_cast<uint8_t*>(logits);
     a.ld_bytes = ld * a.elem;
+    const int64_t group = 4 * int64_t(a.elem);
+    a.vec_store = reinterpret_cast<uintptr_t>(logits) % group == 0 && a.ld_bytes % group == 0;
   } else {
     a.bits = bits;
     a.words = (int64_t(toks->vocab_size) + 31) / 32;
@@ -1654,14 +1817,15 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
     const MemoWs ws = memo_ws(workspace, rows, toks->vocab_size);
+    const uint64_t pkey = pack_key(toks, rows);
     pack_tokens_kernel<<<unsigned((toks->vocab_size + 255) / 256), 256, 0, as_stream(stream)>>>(
-        toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta);
+        toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta, ws.header, pkey);
     BPD_LAUNCHED();
     // BPD_PDA_MEMO_SETS lowers the interned-set limit (tests of the overflow path)
-    int max_sets = kMemoSets;
+    int max_sets = kMemoIds;
     if (const char* e = std::getenv("BPD_PDA_MEMO_SETS")) {
       const int v = std::atoi(e);
-      if (v >= 1 && v < kMemoSets) max_sets = v;
+      if (v >= 1 && v < kMemoIds) max_sets = v;
     }
     // BPD_PDA_MEMO_MODE=tile resolves per tile of tokens only (tests of that path)
     const char* mode = std::getenv("BPD_PDA_MEMO_MODE");
@@ -1676,9 +1840,17 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&pda_memo_mask_kernel)));
     const bool in_lds = fa.sharedSizeBytes + tab_bytes <= size_t(max_lds);
     pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
-        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), next_generation(), row_mode);
+        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), next_generation(), row_mode, pkey);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
+    // rows that overflow are rare: four waves per row keep short a launch
+    // whose blocks mostly read their flag and exit
+    if (chunks > 4) {
+      per = (int64_t(toks->vocab_size) + 3) / 4;
+      per = (per + kWave - 1) / kWave * kWave;
+      chunks = (int64_t(toks->vocab_size) + per - 1) / per;
+      a.chunk_tokens = int32_t(per);
+    }
   }
   pda_mask_kernel<<<dim3(unsigned(chunks), unsigned(rows)), dim3(kWave), 0, as_stream(stream)>>>(a);
   BPD_LAUNCHED();

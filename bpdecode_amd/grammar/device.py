@@ -19,6 +19,7 @@ nested JSON under the 8-configuration cap.
 from __future__ import annotations
 
 import ctypes as C
+import hashlib
 from collections.abc import Hashable, Sequence
 from dataclasses import dataclass, field, replace
 
@@ -149,6 +150,7 @@ class PdaTensors:
         ws = self._c.get(key)
         if ws is None or ws.numel() < need:
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+            ws[:256].zero_()  # header: no token records packed yet
             self._c[key] = ws
         return ws, need
 
@@ -176,7 +178,8 @@ class PdaTensors:
                 self._c["frames"] = frames
                 self._c["frame_lists"] = fl
             t = _lib.TokenBytesC(self.vocab_size, self.eos_id, ptr(off), ptr(tb), ptr(keep[2]), ptr(keep[3]),
-                                 C.pointer(frames) if frames is not None else None)
+                                 C.pointer(frames) if frames is not None else None,
+                                 _pack_tag(off, tb, order, self.vocab_size))
             self._c["tokens"] = t
             self._c["tokens_keep"] = keep
         return t
@@ -206,6 +209,17 @@ class PdaTensors:
 
     def init_batch(self, batch: int) -> torch.Tensor:
         return self.init_config().unsqueeze(0).expand(batch, -1).contiguous()
+
+
+def _pack_tag(off: torch.Tensor, tb: torch.Tensor, order: torch.Tensor, vocab: int) -> int:
+    """Content tag of the token tables (never 0): the device mask packs its
+    token records into a workspace once per tag instead of once per call."""
+    h = hashlib.blake2b(digest_size=8)
+    h.update(int(vocab).to_bytes(8, "little"))
+    for x in (off, tb, order):
+        h.update(x.detach().cpu().contiguous().numpy().tobytes())
+        h.update(b"|")
+    return int.from_bytes(h.digest(), "little") or 1
 
 
 # ------------------------------------------------------------ flattening --

@@ -278,6 +278,12 @@ typedef struct BpdTokenBytes {
   /* optional (NULL = none): frame lists for `order` (device pointers inside
    * a host struct) */
   const BpdPdaFrames* frames;
+  /* optional (0 = none): a tag that identifies the contents of offsets,
+   * bytes and order.  The device mask packs the token records into its
+   * workspace on every call unless the workspace header already carries
+   * this tag for the same row count (a workspace keeps them between calls;
+   * zero the first 256 bytes of a newly allocated workspace). */
+  uint64_t pack_tag;
 } BpdTokenBytes;
 
 /* bpd_pda_init: the closed initial config-set (pda.hpp:200-207), host only,

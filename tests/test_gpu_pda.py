@@ -513,3 +513,87 @@ def test_cfg_batch_commit_reads_int64_low_bits(dev, json_case):
     ok_o = OP.advance(t, mirror, np.array(toks, dtype=np.int32))
     assert ok_o.all() and status.cpu().tolist() == [1, 1, 1, 1]
     assert np.array_equal(batch._configs.cpu().numpy(), mirror)
+
+
+def _toy_rows(g, t, vocab, B, rng):
+    """B config-sets reached by 0-5 random allowed tokens from the start."""
+    rows = []
+    for _ in range(B):
+        c = g.init_config()
+        for _ in range(int(rng.integers(0, 6))):
+            bits = OP.compute_mask(t, c.numpy()[None])[0]
+            allowed = [k for k in range(vocab.size) if bits[k >> 5] >> (k & 31) & 1 and k != vocab.eos_id]
+            if not allowed or not g.feed(c, vocab.token_bytes[int(rng.choice(allowed))]):
+                break
+        rows.append(c)
+    return torch.stack(rows)
+
+
+@pytest.mark.parametrize("idx", range(len(GRAMMARS)))
+def test_logits_views_of_every_alignment(dev, idx):
+    """A 35-token vocabulary and logits rows inside wider buffers: aligned
+    rows of four-column groups (stored whole) with a ragged last group,
+    rows whose start or stride breaks the alignment (column by column), in
+    every dtype; the oracle's masks, and columns outside the view untouched."""
+    vocab = Vocabulary.from_tokens(list(VOCAB.token_bytes) + [b"xy", b"0,", b"}}"], eos_id=VOCAB.eos_id)
+    g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(GRAMMARS[idx])), vocab, eps_reduce=True)
+    t = OP.Table(g)
+    B, V = 6, vocab.size
+    cfgs = _toy_rows(g, t, vocab, B, np.random.default_rng(200 + idx))
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        for width, start in ((35, 0), (36, 0), (40, 1), (48, 4)):
+            _log(f"case toy grammar {idx} logits {dtype} width {width} start {start}")
+            base = torch.randn(B, width, generator=torch.Generator().manual_seed(width)).to(dtype)
+            ref = base.float().numpy().copy()
+            view = ref[:, start:start + V].copy()
+            OP.apply_mask(t, cfgs.numpy().copy(), view)
+            want = base.clone()
+            want[:, start:start + V][torch.from_numpy(np.isneginf(view))] = float("-inf")
+            got = base.to(dev)
+            pda_mask_(got[:, start:start + V], gd, pool)
+            assert torch.equal(got.cpu().view(torch.uint8), want.view(torch.uint8)), (dtype, width, start)
+
+
+def test_json_token_records_across_row_counts(dev, json_case):
+    """Masks at 16, 4, 16 and 16 rows on one workspace: the records packed
+    at one row count are not taken at another (their place moves), and the
+    last call reuses the records of the one before; each against the oracle."""
+    vocab, g, t = json_case
+    gd = g.to(dev)
+    cfgs = _json_configs(g, 16, seed=91)
+    for n in (16, 4, 16, 16):
+        _log(f"case json token records B={n}")
+        got = pda_compute_mask(gd, cfgs[:n].to(dev)).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, OP.compute_mask(t, cfgs[:n].numpy())), n
+
+
+def test_token_records_of_two_vocabularies_one_workspace(dev):
+    """Two vocabularies of the same size and different bytes, masked in turn
+    through the C ABI on one workspace (header zeroed once): the content tags
+    differ, so each call walks its own tables' records; against the oracle."""
+    from bpdecode_amd._lib import check, lib, ptr
+
+    comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
+    base = [bytes([i]) for i in range(256)]
+    cases = []
+    for extra in ([b"", b"\"a", b"</s>", b"", b"1, ", b"[{\"", b"true]"],
+                  [b"", b"{\"", b"</s>", b"", b"2]", b"\"k\":", b"null,"]):
+        vocab = Vocabulary.from_tokens(base + extra, eos_id=258)
+        g = build_pda_tensors(comp, vocab, eps_reduce=True)
+        cfgs = _json_configs(g, 8, seed=93)
+        cases.append((g.to(dev), cfgs.to(dev), OP.compute_mask(OP.Table(g), cfgs.numpy())))
+    assert cases[0][0].c_tokens().pack_tag != cases[1][0].c_tokens().pack_tag
+    V = cases[0][0].vocab_size
+    need = int(lib().bpd_pda_workspace_bytes(8, V))
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for i in (0, 1, 0, 0, 1):
+        _log(f"case two vocabularies, tables {i}")
+        gd, pool, want = cases[i]
+        out = torch.empty((8, (V + 31) // 32), dtype=torch.int32, device=dev)
+        check(lib().bpd_pda_compute_mask(gd.c_table(), gd.c_tokens(), ptr(pool), None, 8, ptr(out),
+                                         ptr(ws), need, stream))
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want), i
+

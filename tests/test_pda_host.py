@@ -296,6 +296,25 @@ def test_memo_walk_order_is_a_permutation_by_first_byte_length_then_bytes():
     assert zr.tolist() == [0] * 257
 
 
+def test_token_pack_tag_follows_the_table_contents():
+    """The tag under which the device mask keeps its packed token records:
+    equal for equal tables, different when a byte, a boundary or the walk
+    order changes, never 0."""
+    from bpdecode_amd.grammar.device import _pack_tag
+
+    off = torch.tensor([0, 1, 3, 3, 6], dtype=torch.int32)
+    tb = torch.tensor(list(b"abcdef"), dtype=torch.uint8)
+    order = torch.tensor([3, 0, 1, 2], dtype=torch.int32)
+    tag = _pack_tag(off, tb, order, 4)
+    assert tag != 0 and tag == _pack_tag(off.clone(), tb.clone(), order.clone(), 4)
+    others = [
+        _pack_tag(off, torch.tensor(list(b"abcdeg"), dtype=torch.uint8), order, 4),
+        _pack_tag(torch.tensor([0, 2, 3, 3, 6], dtype=torch.int32), tb, order, 4),
+        _pack_tag(off, tb, torch.tensor([3, 0, 2, 1], dtype=torch.int32), 4),
+    ]
+    assert len({tag, *others}) == 4
+
+
 def _frame_key_row(cfg: np.ndarray, keys: np.ndarray) -> int:
     """The frame list a config-set takes on the device (-1: none): every
     config at one depth >= 2 over the same frames below the top, and the
