@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
@@ -46,8 +46,8 @@ class PdaTableC(C.Structure):
 
 
 class PdaFramesC(C.Structure):
-    _fields_ = [("num_lists", i32), ("words", i32), ("keys", vp), ("trans", vp), ("allowed", vp),
-                ("seed_off", vp), ("seeds", vp)]
+    _fields_ = [("num_lists", i32), ("words", i32), ("keys", vp), ("slots", vp), ("trans", vp),
+                ("allowed", vp), ("seed_off", vp), ("seeds", vp)]
 
 
 class TokenBytesC(C.Structure):
@@ -93,6 +93,7 @@ _SIGNATURES = {
     "bpd_stage_int64": (cint, [vp, vp, i64, vp]),
     "bpd_pda_init": (cint, [C.POINTER(PdaTableC), vp]),
     "bpd_pda_feed": (cint, [C.POINTER(PdaTableC), vp, C.c_char_p, i64]),
+    "bpd_host_frame_classify": (cint, [vp, i32, vp, vp, i32, i32, vp, vp, vp, vp, vp, i32]),
     "bpd_pda_workspace_bytes": (sz, [i64, i32]),
     "bpd_pda_apply_mask": (cint, [C.POINTER(PdaTableC), C.POINTER(TokenBytesC), vp, vp, vp,
                                   i64, vp, cint, i64, f64, vp, sz, vp]),

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "bpd_common.hpp"
@@ -50,7 +51,7 @@ using namespace bpd;
 
 extern "C" const char* bpd_last_error(void) { return g_error; }
 
-extern "C" int bpd_abi_version(void) { return 7; }
+extern "C" int bpd_abi_version(void) { return 8; }
 
 extern "C" int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab,
                                          int64_t ld, const int32_t* tok_next,
@@ -201,5 +202,76 @@ extern "C" int bpd_host_build_reachability(const int32_t* trans, int32_t num_sta
       }
     }
   }
+  return BPD_OK;
+}
+
+// Every (frame list, token) walk of the PDA mask's frame lists, split over
+// `threads` host threads by list.  trans[l][c]: the list byte c leads to
+// (or-ed with the saturation flag), -1 when the step empties the set, -2 at
+// a boundary.  A token is inside list l when every byte leads to a list;
+// its bit in allowed[l] is set unless it is EOS or empty.  The seeds of l are
+// the walk positions whose token meets a boundary, or is EOS or empty.
+extern "C" int bpd_host_frame_classify(const int32_t* trans, int32_t num_lists, const int32_t* tok_offsets,
+                                       const uint8_t* tok_bytes, int32_t vocab_size, int32_t eos_id,
+                                       const int32_t* order, uint32_t* allowed, int32_t* seed_count,
+                                       const int32_t* seed_off, int32_t* seeds, int32_t threads) {
+  BPD_REQUIRE(num_lists >= 0 && vocab_size >= 0, "bad shape");
+  if (num_lists == 0) return BPD_OK;
+  BPD_REQUIRE(trans && tok_offsets && order && allowed && seed_count, "null pointer argument");
+  BPD_REQUIRE((seed_off != nullptr) == (seeds != nullptr), "seeds and seed_off go together");
+  for (int64_t i = 0; i < int64_t(num_lists) * 256; ++i) {
+    const int32_t c = trans[i];
+    BPD_REQUIRE(c == -1 || c == -2 || (c >= 0 && (c & (BPD_PDA_FRAME_SAT - 1)) < num_lists &&
+                                       (c & ~(BPD_PDA_FRAME_SAT | (BPD_PDA_FRAME_SAT - 1))) == 0),
+                "frame transition %d out of range", c);
+  }
+  BPD_REQUIRE(tok_offsets[0] == 0, "token offsets start at %d", tok_offsets[0]);
+  for (int32_t t = 0; t < vocab_size; ++t)
+    BPD_REQUIRE(tok_offsets[t + 1] >= tok_offsets[t], "token offsets decrease at %d", t);
+  BPD_REQUIRE(tok_offsets[vocab_size] == 0 || tok_bytes, "null token bytes");
+  for (int32_t k = 0; k < vocab_size; ++k)
+    BPD_REQUIRE(order[k] >= 0 && order[k] < vocab_size, "walk order entry %d out of range", order[k]);
+  if (seed_off) {
+    BPD_REQUIRE(seed_off[0] == 0, "seed offsets start at %d", seed_off[0]);
+    for (int32_t l = 0; l < num_lists; ++l)
+      BPD_REQUIRE(seed_off[l + 1] >= seed_off[l] && int64_t(seed_off[l + 1]) - seed_off[l] <= vocab_size,
+                  "seed offsets out of range at list %d", l);
+  }
+  const int64_t words = (int64_t(vocab_size) + 31) / 32;
+  auto work = [&](int32_t first, int32_t step) {
+    for (int32_t l = first; l < num_lists; l += step) {
+      uint32_t* al = allowed + int64_t(l) * words;
+      std::fill(al, al + words, 0u);
+      int32_t n = 0;
+      const int32_t cap = seed_off ? seed_off[l + 1] - seed_off[l] : 0;
+      int32_t* out = seeds ? seeds + seed_off[l] : nullptr;
+      for (int32_t k = 0; k < vocab_size; ++k) {
+        const int32_t t = order[k];
+        const int32_t s = tok_offsets[t], e = tok_offsets[t + 1];
+        int32_t cur = l;
+        for (int32_t i = s; i < e && cur >= 0; ++i) {
+          const int32_t c = trans[int64_t(cur) * 256 + tok_bytes[i]];
+          cur = c >= 0 ? (c & (BPD_PDA_FRAME_SAT - 1)) : c;
+        }
+        const bool special = e == s || t == eos_id;
+        if (special || cur == -2) {
+          if (out && n < cap) out[n] = k;
+          ++n;
+        } else if (cur >= 0) {
+          al[t >> 5] |= 1u << (t & 31);
+        }
+      }
+      seed_count[l] = n;
+    }
+  };
+  const int32_t nt = std::max<int32_t>(1, std::min<int32_t>(threads, std::min<int32_t>(num_lists, 64)));
+  std::vector<std::thread> pool;
+  for (int32_t i = 1; i < nt; ++i) pool.emplace_back(work, i, nt);
+  work(0, nt);
+  for (auto& th : pool) th.join();
+  if (seed_off)
+    for (int32_t l = 0; l < num_lists; ++l)
+      BPD_REQUIRE(seed_count[l] == seed_off[l + 1] - seed_off[l], "list %d has %d seeds, not %d", l,
+                  seed_count[l], seed_off[l + 1] - seed_off[l]);
   return BPD_OK;
 }

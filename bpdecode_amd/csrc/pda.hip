@@ -615,29 +615,90 @@ __device__ __forceinline__ int long_byte(const MaskArgs& a, int64_t k, int32_t p
   return a.tok_bytes[a.tok_off[t] + p];
 }
 
-// The frame list of a set held in LDS (-1: none): every config at one depth
-// >= 2 over the same frames below its top, and the ordered tops equal to a
-// list's key (`keys`: the lists' keys, staged in LDS).  Called by the 64
-// lanes of a wave; every lane gets the answer.
-__device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const int32_t* keys, int lane) {
+__device__ __forceinline__ uint32_t frame_mix(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7FEB352Du;
+  x ^= x >> 15;
+  x *= 0x846CA68Bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// The frame list of a set held in LDS (-1: none).  The common stack P is
+// tried at the configs' longest common prefix below every top and up to
+// BPD_PDA_FRAME_SUFFIX - 1 frames shorter, shortest first, each with every
+// suffix at most BPD_PDA_FRAME_SUFFIX frames and P plus that many frames
+// within the depth limit.  For each, lane w < BPD_PDA_FRAME_KEY_WORDS builds
+// word w of the key the suffixes would have and its term of the key's hash
+// (a sum of per-word mixes, grammar/frames.py list_hash); the probe reads the
+// slot table (`slots`, staged in LDS) 64 slots at a time up to the first
+// empty slot and compares the keys of fingerprint matches lane-parallel.
+// Called by the 64 lanes of a wave; every lane gets the answer (and, in
+// base_out, the depth of P).
+__device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const uint32_t* slots, int lane,
+                              int* base_out = nullptr) {
   if (f.num_lists <= 0) return -1;
   const int n = c[0];
-  const int d0 = n >= 1 ? c[2] : 0;
-  if (n < 1 || n > kMaxConfigs || d0 < 2 || d0 > kMaxDepth) return -1;
-  bool bad = lane < n && c[2 + lane] != d0;
-  for (int x = lane; x < n * kMaxDepth; x += kWave) {
-    const int i = x / kMaxDepth, k = x % kMaxDepth;
-    if (k < d0 - 1 && c[kF + i * kMaxDepth + k] != c[kF + k]) bad = true;
+  if (n < 1 || n > kMaxConfigs) return -1;
+  int mind = kMaxDepth + 1, maxd = 0;
+  for (int i = 0; i < n; ++i) {
+    const int d = c[2 + i];
+    mind = d < mind ? d : mind;
+    maxd = d > maxd ? d : maxd;
   }
-  if (__ballot(bad) != 0) return -1;
-  bool hit = false;
-  if (lane < f.num_lists) {
-    const int32_t* key = keys + lane * BPD_PDA_FRAME_KEY_WORDS;
-    hit = key[0] == n;
-    for (int i = 0; i < n && hit; ++i) hit = key[1 + i] == c[kF + i * kMaxDepth + d0 - 1];
+  if (mind < 1 || maxd > kMaxDepth) return -1;
+  // common prefix: lane k < mind - 1 compares frame k of every config
+  bool stop = lane >= mind - 1;
+  for (int i = 1; i < n && !stop; ++i) stop = c[kF + i * kMaxDepth + lane] != c[kF + lane];
+  const int p = __ffsll(static_cast<unsigned long long>(__ballot(stop))) - 1;
+  const int jmax = p < BPD_PDA_FRAME_SUFFIX - 1 ? p : BPD_PDA_FRAME_SUFFIX - 1;
+  for (int j = jmax; j >= 0; --j) {
+    const int base = p - j;
+    if (base + BPD_PDA_FRAME_SUFFIX > kMaxDepth || maxd - base > BPD_PDA_FRAME_SUFFIX) continue;
+    int32_t want = 0;
+    uint32_t term = 0;
+    if (lane == 0) {
+      want = n;
+      term = frame_mix(0xC2B2AE35u ^ uint32_t(n));
+    } else if (lane <= kMaxConfigs) {
+      const int i = lane - 1;
+      if (i < n) {
+        want = c[2 + i] - base;
+        term = frame_mix((uint32_t((i << 8) | 0xFF) * 0x85EBCA6Bu) ^ uint32_t(want));
+      }
+    } else if (lane < 1 + kMaxConfigs + kMaxConfigs * BPD_PDA_FRAME_SUFFIX) {
+      const int i = (lane - 1 - kMaxConfigs) / BPD_PDA_FRAME_SUFFIX;
+      const int k = (lane - 1 - kMaxConfigs) % BPD_PDA_FRAME_SUFFIX;
+      if (i < n && k < c[2 + i] - base) {
+        want = c[kF + i * kMaxDepth + base + k];
+        term = frame_mix((uint32_t((i << 8) | k) * 0x9E3779B1u) ^ uint32_t(want));
+      }
+    }
+    for (int o = 1; o < kWave; o <<= 1) term += __shfl_xor(term, o);
+    const uint32_t h = frame_mix(term);
+    const uint32_t fp = (h >> 10) & 0xFFFFFu;
+    uint32_t at = h;
+    for (int w = 0; w < BPD_PDA_FRAME_SLOTS / kWave; ++w, at += kWave) {
+      const uint32_t e = slots[(at + uint32_t(lane)) & (BPD_PDA_FRAME_SLOTS - 1)];
+      const uint64_t empty = __ballot(e == BPD_PDA_FRAME_EMPTY);
+      const int lim = empty != 0u ? __ffsll(static_cast<unsigned long long>(empty)) - 1 : kWave;
+      uint64_t m = __ballot(lane < lim && (e >> 12) == fp);
+      while (m != 0u) {
+        const int k = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        m &= m - 1;
+        const int id = int(__shfl(e, k) & 0xFFFu);
+        if (id < f.num_lists) {
+          const bool diff = lane < BPD_PDA_FRAME_KEY_WORDS && f.keys[id * BPD_PDA_FRAME_KEY_WORDS + lane] != want;
+          if (__ballot(diff) == 0u) {
+            if (base_out) *base_out = base;
+            return id;
+          }
+        }
+      }
+      if (empty != 0u) break;
+    }
   }
-  const uint64_t m = __ballot(hit);
-  return m != 0u ? __ffsll(static_cast<unsigned long long>(m)) - 1 : -1;
+  return -1;
 }
 
 // Transition-table row of set `id`, a set in frame list l: a byte whose step
@@ -654,6 +715,72 @@ __device__ void frame_fill_row(const BpdPdaFrames& f, int l, bool sat, int id, u
       trow[c] = uint8_t(id);
     }
   }
+}
+
+// LDS bytes a launch of `kernel` can add to its static arrays on the current
+// device (the device's per-workgroup limit less the kernel's own), queried
+// once per device and kernel slot.
+int lds_room(const void* kernel, int slot, size_t* room) {
+  constexpr int kDevices = 64;
+  static std::atomic<long long> cache[kDevices][1];  // room + 1; 0: not queried yet
+  int dev = 0;
+  BPD_HIP(hipGetDevice(&dev));
+  if (dev >= 0 && dev < kDevices) {
+    const long long c = cache[dev][slot].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *room = size_t(c - 1);
+      return BPD_OK;
+    }
+  }
+  int max_lds = 0;
+  BPD_HIP(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+  hipFuncAttributes fa{};
+  BPD_HIP(hipFuncGetAttributes(&fa, kernel));
+  *room = size_t(max_lds) > fa.sharedSizeBytes ? size_t(max_lds) - fa.sharedSizeBytes : 0;
+  if (dev >= 0 && dev < kDevices) cache[dev][slot].store((long long)(*room) + 1, std::memory_order_relaxed);
+  return BPD_OK;
+}
+
+// Bytes of the grammar tables staged in LDS by stage_tables.
+size_t staged_table_bytes(const BpdPdaTable* g) {
+  return (size_t(g->num_states) + 1) * 4 + size_t(g->num_edges) * 20 + (size_t(g->num_states) * 2 + 3) / 4 * 4;
+}
+
+// Copy of the grammar tables in LDS at `tab` (staged_table_bytes long) made
+// by the workgroup's `nthreads` threads, and a view of it; the caller
+// synchronises before the view is read.
+__device__ PdaTableView stage_tables(const PdaTableView& src, int32_t* tab, int tid, int nthreads) {
+  const int N = src.num_states, E = src.num_edges;
+  int32_t* eo = tab;
+  int32_t* ek = eo + N + 1;
+  int32_t* elo = ek + E;
+  int32_t* ehi = elo + E;
+  int32_t* ed = ehi + E;
+  int32_t* ec = ed + E;
+  uint8_t* acc = reinterpret_cast<uint8_t*>(ec + E);
+  uint8_t* lv = acc + N;
+  for (int i = tid; i <= N; i += nthreads) eo[i] = src.edge_offsets[i];
+  for (int i = tid; i < E; i += nthreads) {
+    ek[i] = src.edge_kind[i];
+    elo[i] = src.edge_lo[i];
+    ehi[i] = src.edge_hi[i];
+    ed[i] = src.edge_dst[i];
+    ec[i] = src.edge_callee[i];
+  }
+  for (int i = tid; i < N; i += nthreads) {
+    acc[i] = src.accept[i];
+    lv[i] = src.live[i];
+  }
+  PdaTableView g = src;
+  g.edge_offsets = eo;
+  g.edge_kind = ek;
+  g.edge_lo = elo;
+  g.edge_hi = ehi;
+  g.edge_dst = ed;
+  g.edge_callee = ec;
+  g.accept = acc;
+  g.live = lv;
+  return g;
 }
 
 // verdicts of a token in the memoised walk, past every set id
@@ -681,7 +808,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t cand_lead[kMemoReq];
   __shared__ uint8_t cand_exact[kMemoReq];  // an existing set with every word of the step's
   __shared__ int32_t cand_list[kMemoReq];  // frame list of a new set (| BPD_PDA_FRAME_SAT), -1 none
-  __shared__ int32_t fkeys[BPD_PDA_MAX_FRAME_LISTS * BPD_PDA_FRAME_KEY_WORDS];
+  __shared__ uint32_t fslots[BPD_PDA_FRAME_SLOTS];  // the frame lists' slot table
   __shared__ int32_t cand_id[kMemoReq];
   __shared__ int16_t cand_lo[kMemoReq];
   __shared__ int16_t cand_hi[kMemoReq];
@@ -708,40 +835,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   }
 
   for (int k = tid; k < kConfigWords; k += kMemoThreads) row_cfg[k] = a.configs[row * kConfigWords + k];
-  PdaTableView g = a.g;
-  if (table_in_lds) {
-    const int N = a.g.num_states, E = a.g.num_edges;
-    int32_t* eo = tab;
-    int32_t* ek = eo + N + 1;
-    int32_t* elo = ek + E;
-    int32_t* ehi = elo + E;
-    int32_t* ed = ehi + E;
-    int32_t* ec = ed + E;
-    uint8_t* acc = reinterpret_cast<uint8_t*>(ec + E);
-    uint8_t* lv = acc + N;
-    for (int i = tid; i <= N; i += kMemoThreads) eo[i] = a.g.edge_offsets[i];
-    for (int i = tid; i < E; i += kMemoThreads) {
-      ek[i] = a.g.edge_kind[i];
-      elo[i] = a.g.edge_lo[i];
-      ehi[i] = a.g.edge_hi[i];
-      ed[i] = a.g.edge_dst[i];
-      ec[i] = a.g.edge_callee[i];
-    }
-    for (int i = tid; i < N; i += kMemoThreads) {
-      acc[i] = a.g.accept[i];
-      lv[i] = a.g.live[i];
-    }
-    g.edge_offsets = eo;
-    g.edge_kind = ek;
-    g.edge_lo = elo;
-    g.edge_hi = ehi;
-    g.edge_dst = ed;
-    g.edge_callee = ec;
-    g.accept = acc;
-    g.live = lv;
-  }
+  const PdaTableView g = table_in_lds ? stage_tables(a.g, tab, tid, kMemoThreads) : a.g;
   for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
-  for (int i = tid; i < a.frames.num_lists * BPD_PDA_FRAME_KEY_WORDS; i += kMemoThreads) fkeys[i] = a.frames.keys[i];
+  for (int i = tid; i < BPD_PDA_FRAME_SLOTS; i += kMemoThreads)
+    fslots[i] = a.frames.num_lists > 0 ? a.frames.slots[i] : BPD_PDA_FRAME_EMPTY;
   const int32_t vwords = (a.vocab + 31) / 32;
   for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
   for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) {
@@ -774,7 +871,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     wave_sync();
     coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
-    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fkeys, tid);
+    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, tid);
     if (tid == 0) row_list = l0;
     if (l0 >= 0) {
       wave_sync();
@@ -891,7 +988,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           // a new set is kept in the candidate buffer (its words are needed
           // after this wave's buffer is reused); stored after the pool
           // lookup's loads, which would otherwise wait for these stores
-          const int lst = found == -2 ? frame_list_of(wdst, a.frames, fkeys, lane) : -1;
+          const int lst = found == -2 ? frame_list_of(wdst, a.frames, fslots, lane) : -1;
           if (lane == 0) cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0)) : -1;
           if (found == -2) {
             int32_t* out = cand + r * kConfigWords;
@@ -1519,6 +1616,7 @@ struct AdvanceArgs {
   uint8_t* broken;
   int32_t* status;
   int32_t* err;
+  BpdPdaFrames frames;  // num_lists 0: no frame lists
 };
 
 __device__ bool flat_config_ok(const int32_t* c, int32_t num_states) {
@@ -1585,20 +1683,65 @@ __global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a)
 // from the interned set reached, so the written config-set has the raw words
 // of the direct walk.  Otherwise (or when the table walk meets an entry the
 // mask left unresolved) every byte is stepped with advance_byte.
-constexpr int kCommitWaves = 4;
+// The meaningful words of the set of list `key` over the common stack that
+// config 0 of `x` holds in its first `base` frames, written over `x` (words
+// past each depth set to 0).  One wave.
+__device__ void compose_list_set(int32_t* x, const int32_t* key, int base, int sat, int lane) {
+  const int32_t pw = lane < base ? x[kF + lane] : 0;
+  const int n = key[0];
+  int32_t len[kMaxConfigs];
+#pragma unroll
+  for (int i = 0; i < kMaxConfigs; ++i) len[i] = i < n ? key[1 + i] : 0;
+  wave_sync();
+  for (int w = lane; w < kMaxConfigs * kMaxDepth; w += kWave) {
+    const int i = w / kMaxDepth, k = w % kMaxDepth;
+    const int32_t p = __shfl(pw, k < base ? k : 0);
+    int32_t v = 0;
+    if (i < n) {
+      if (k < base)
+        v = p;
+      else if (k < base + len[i])
+        v = key[1 + kMaxConfigs + i * BPD_PDA_FRAME_SUFFIX + (k - base)];
+    }
+    x[kF + w] = v;
+  }
+  if (lane < kMaxConfigs) x[2 + lane] = lane < n ? base + len[lane] : 0;
+  if (lane == 0) {
+    x[0] = n;
+    x[1] = sat;
+  }
+  wave_sync();
+}
 
-__global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(AdvanceArgs a, MemoWs ws,
-                                                                               uint64_t tag) {
-  __shared__ int32_t bufs[kCommitWaves][2][kConfigWords];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int64_t b = int64_t(blockIdx.x) * kCommitWaves + wave;
-  if (b >= a.rows) return;
+// The memoised commit: one row per workgroup.  All its threads stage the
+// row's transition table in LDS with one round of loads (the walk over the
+// token's bytes is then a chain of LDS reads, not of global ones); wave 0
+// commits the row.
+constexpr int kCommitThreads = 256;
+
+__global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(AdvanceArgs a, MemoWs ws,
+                                                                         uint64_t tag) {
+  __shared__ int32_t bufs[2][kConfigWords];
+  __shared__ uint4 trow[kMemoSets * 16];  // the row's table (256 bytes per set)
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t b = blockIdx.x;
   const int64_t row = a.slots ? a.slots[b] : b;
   int32_t* cfg = a.configs + row * kConfigWords;
-  int32_t* x = bufs[wave][0];
-  int32_t* y = bufs[wave][1];
-  for (int k = lane; k < kConfigWords; k += kWave) x[k] = cfg[k];
-  wave_sync();
+  int32_t* x = bufs[0];
+  int32_t* y = bufs[1];
+  if (threadIdx.x < kWave)
+    for (int k = lane; k < kConfigWords; k += kWave) x[k] = cfg[k];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(ws.table + b * (kMemoSets * 64));
+    uint4 v[kMemoSets * 16 / kCommitThreads];
+#pragma unroll
+    for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) v[q] = src[q * kCommitThreads + threadIdx.x];
+#pragma unroll
+    for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) trow[q * kCommitThreads + threadIdx.x] = v[q];
+  }
+  const PdaTableView& g = a.g;
+  __syncthreads();
+  if (threadIdx.x >= kWave) return;
   const int64_t t = read_token(a.tokens, a.tok_dtype, b);
   bool ok;
   if (t < 0 || t >= a.vocab) {
@@ -1608,7 +1751,7 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
     if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_STATE_RANGE);
     ok = false;
   } else if (t == a.eos) {
-    ok = is_complete(a.g, ConstFlatView{x});
+    ok = is_complete(g, ConstFlatView{x});
   } else {
     const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
     ok = true;
@@ -1630,7 +1773,7 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
       if (ws.pool && ws.meta[b * 4] == 1 && ws.meta[b * 4 + 1] == int32_t(uint32_t(tag)) &&
           ws.meta[b * 4 + 2] == int32_t(uint32_t(tag >> 32)) &&
           uint32_t(ws.meta[b * 4 + 3]) == ws.header[0] && coop_same(x, pool, lane)) {
-        const uint8_t* T = reinterpret_cast<const uint8_t*>(ws.table + b * (kMemoSets * 64));
+        const uint8_t* T = reinterpret_cast<const uint8_t*>(trow);
         cur = 0;
         for (; i < e; ++i) {
           const uint8_t nx = T[cur * 256 + byte_at(i)];
@@ -1657,8 +1800,33 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
           for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[cur * kConfigWords + k];
           wave_sync();
         }
+        // bytes before the last taken through the frame lists' byte table
+        // while the set is in a list: only the set before the last byte
+        // needs its words, and only its meaningful ones (the last step
+        // zeroes the set it writes), rebuilt from the common stack and the
+        // list's key
+        if (i < e - 1 && ok && a.frames.num_lists > 0) {
+          int base = 0;
+          const int l0 = frame_list_of(x, a.frames, a.frames.slots, lane, &base);
+          if (l0 >= 0) {
+            int l = l0, sat = x[1] != 0 ? 1 : 0, code = 0;
+            int32_t j = i;
+            for (; j < e - 1; ++j) {
+              code = a.frames.trans[l * 256 + byte_at(j)];
+              if (code < 0) break;
+              l = code & (BPD_PDA_FRAME_SAT - 1);
+              sat |= (code & BPD_PDA_FRAME_SAT) != 0 ? 1 : 0;
+            }
+            if (j < e - 1 && code == -1) {
+              ok = false;  // the list (and so the set) empties at byte j
+            } else if (j > i) {
+              compose_list_set(x, a.frames.keys + int64_t(l) * BPD_PDA_FRAME_KEY_WORDS, base, sat, lane);
+              i = j;
+            }
+          }
+        }
         for (; i < e && ok; ++i) {
-          ok = coop_advance_byte(a.g, x, y, byte_at(i), lane);
+          ok = coop_advance_byte(g, x, y, byte_at(i), lane);
           int32_t* tmp = x;
           x = y;
           y = tmp;
@@ -1677,6 +1845,23 @@ __global__ __launch_bounds__(kCommitWaves * kWave) void pda_memo_advance_kernel(
       a.status[b] = ok ? 1 : -1;
     }
   }
+}
+
+// The frame lists of `toks` as a kernel argument (num_lists 0: none).
+int frames_arg(const BpdTokenBytes* toks, BpdPdaFrames* out) {
+  *out = BpdPdaFrames{};
+  if (const BpdPdaFrames* f = toks->frames) {
+    BPD_REQUIRE(f->num_lists >= 0 && f->num_lists <= BPD_PDA_MAX_FRAME_LISTS,
+                "frame lists: num_lists %d outside [0, %d]", f->num_lists, BPD_PDA_MAX_FRAME_LISTS);
+    if (f->num_lists > 0) {
+      BPD_REQUIRE(f->words == (toks->vocab_size + 31) / 32, "frame lists: words %d for vocab %d",
+                  f->words, toks->vocab_size);
+      BPD_REQUIRE(f->keys && f->slots && f->trans && f->allowed && f->seed_off && f->seeds,
+                  "frame lists: null array");
+      *out = *f;
+    }
+  }
+  return BPD_OK;
 }
 
 int check_tables(const BpdPdaTable* g, const BpdTokenBytes* toks) {
@@ -1802,17 +1987,7 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
   a.only_rows = nullptr;
   a.order = toks->order;
   a.runs = toks->order ? toks->runs : nullptr;
-  a.frames = BpdPdaFrames{};
-  if (const BpdPdaFrames* f = toks->frames) {
-    BPD_REQUIRE(f->num_lists >= 0 && f->num_lists <= BPD_PDA_MAX_FRAME_LISTS,
-                "frame lists: num_lists %d outside [0, %d]", f->num_lists, BPD_PDA_MAX_FRAME_LISTS);
-    if (f->num_lists > 0) {
-      BPD_REQUIRE(f->words == (toks->vocab_size + 31) / 32, "frame lists: words %d for vocab %d",
-                  f->words, toks->vocab_size);
-      BPD_REQUIRE(f->keys && f->allowed && f->seed_off && f->seeds, "frame lists: null array");
-      a.frames = *f;
-    }
-  }
+  if (int rc = frames_arg(toks, &a.frames)) return rc;
   if (workspace && toks->vocab_size <= kMemoMaxVocab) {
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
@@ -1831,14 +2006,10 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     const char* mode = std::getenv("BPD_PDA_MEMO_MODE");
     const int row_mode = mode && std::strcmp(mode, "tile") == 0 ? 0 : 1;
     // stage the grammar tables in LDS when they fit beside the static arrays
-    const size_t tab_bytes = (size_t(g->num_states) + 1) * 4 + size_t(g->num_edges) * 20 +
-                             (size_t(g->num_states) * 2 + 3) / 4 * 4;
-    int dev = 0, max_lds = 0;
-    BPD_HIP(hipGetDevice(&dev));
-    BPD_HIP(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
-    hipFuncAttributes fa{};
-    BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&pda_memo_mask_kernel)));
-    const bool in_lds = fa.sharedSizeBytes + tab_bytes <= size_t(max_lds);
+    const size_t tab_bytes = staged_table_bytes(g);
+    size_t room = 0;
+    if (int rc = lds_room(reinterpret_cast<const void*>(&pda_memo_mask_kernel), 0, &room)) return rc;
+    const bool in_lds = tab_bytes <= room;
     pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
         a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), next_generation(), row_mode, pkey);
     BPD_LAUNCHED();
@@ -1900,13 +2071,13 @@ extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, 
   a.broken = broken;
   a.status = status;
   a.err = err;
+  if (int rc = frames_arg(toks, &a.frames)) return rc;
   if (workspace) {
     // the mask's workspace of the same batch: reuse its transition tables
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
     const MemoWs ws = memo_ws(workspace, rows, toks->vocab_size);
-    const unsigned blocks = unsigned((rows + kCommitWaves - 1) / kCommitWaves);
-    pda_memo_advance_kernel<<<blocks, kCommitWaves * kWave, 0, as_stream(stream)>>>(a, ws, memo_tag(g, toks, rows));
+    pda_memo_advance_kernel<<<unsigned(rows), kCommitThreads, 0, as_stream(stream)>>>(a, ws, memo_tag(g, toks, rows));
     BPD_LAUNCHED();
     return BPD_OK;
   }

@@ -156,7 +156,7 @@ class PdaTensors:
 
     def c_tokens(self) -> _lib.TokenBytesC:
         """Token tables of the device mask: bytes, the walk order, its
-        first-byte runs and the frame lists of the call-free rules."""
+        first-byte runs and the stack-relative frame lists."""
         t = self._c.get("tokens")
         if t is None:
             off = self.tok_offsets.contiguous()
@@ -169,7 +169,8 @@ class PdaTensors:
             fl = frame_lists(self, order.numpy())
             if fl is not None and fl.num_lists > 0:
                 dev = off.device
-                arrs = [torch.from_numpy(fl.keys).to(dev), torch.from_numpy(fl.trans).to(dev),
+                arrs = [torch.from_numpy(fl.keys).to(dev), torch.from_numpy(fl.slots.view("<i4")).to(dev),
+                        torch.from_numpy(fl.trans).to(dev),
                         torch.from_numpy(fl.allowed.view("<i4")).to(dev),
                         torch.from_numpy(fl.seed_off).to(dev),
                         torch.from_numpy(fl.seeds if fl.seeds.size else np.zeros(1, np.int32)).to(dev)]

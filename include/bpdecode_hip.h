@@ -231,28 +231,42 @@ typedef struct BpdPdaTable {
 } BpdPdaTable;
 
 /* Frame lists of the device mask's fast path (no counterpart in the
- * reference: an acceleration of pda_try_token, pda.hpp:248-258).  A row
- * whose configs all share one stack below their top frames, at depth >= 2,
- * with the ordered top states equal to keys[l][1..n] (n = keys[l][0]), takes
- * its verdicts from allowed[l] (bit t of word t / 32: the token stays inside
- * the tops' call-free rule without reaching its accept state and keeps the
- * set non-empty) and walks only the tokens at walk positions
- * seeds[seed_off[l] .. seed_off[l + 1]) (every other token not in allowed[l]
- * is rejected).  trans[l][c] is the list a byte c step reaches (or-ed with
- * BPD_PDA_FRAME_SAT when the step drops a state at the 8-config cap), -1
- * when it empties the set, -2 when it reaches the accept state: the device
- * fills the transition-table row of every such set it meets (a byte that
- * keeps the list and the saturation flag leads back to the set, a byte that
- * empties it is dead) without stepping it.  Built by grammar/frames.py for
- * the default walk order: the device trusts the contents (seed_off
+ * reference: an acceleration of pda_try_token, pda.hpp:248-258).  A list is
+ * an ordered list of n <= 8 config suffixes, each of 1..BPD_PDA_FRAME_SUFFIX
+ * frames: keys[l] = {n, the n suffix lengths (0 past n), then suffix i's
+ * frames at words 9 + BPD_PDA_FRAME_SUFFIX * i .., 0 elsewhere}.  A config-set
+ * whose configs are a common stack P followed by list l's suffixes (in
+ * config order, every depth within BPD_PDA_MAX_DEPTH after
+ * BPD_PDA_FRAME_SUFFIX more frames on P) steps exactly like the list while no
+ * config pops into P and no suffix grows past BPD_PDA_FRAME_SUFFIX frames.
+ * Such a row takes its verdicts from allowed[l] (bit t of word t / 32: every
+ * byte of token t leads to a list) and walks only the tokens at walk
+ * positions seeds[seed_off[l] .. seed_off[l + 1]) (the tokens that meet a
+ * boundary, EOS and the empty tokens; every other token not in allowed[l]
+ * is rejected).  trans[l][c] is the list byte c leads to (or-ed with
+ * BPD_PDA_FRAME_SAT when the step drops a config at the 8-config cap), -1
+ * when it empties the set, -2 at a boundary: the device fills the
+ * transition-table row of every such set it meets (a byte that keeps the
+ * list and the saturation flag leads back to the set, a byte that empties
+ * it is dead) without stepping it.  slots is an open-addressing table of the
+ * keys: the probe for a list starts at slot h & (BPD_PDA_FRAME_SLOTS - 1) of
+ * its hash h (grammar/frames.py list_hash) and ends at the first
+ * BPD_PDA_FRAME_EMPTY slot; a slot holds l | ((h >> 10) & 0xFFFFF) << 12.
+ * The device matches a set at its longest common stack below every top and
+ * up to BPD_PDA_FRAME_SUFFIX - 1 frames less.  Built by grammar/frames.py
+ * for the default walk order: the device trusts the contents (seed_off
  * non-decreasing within the seeds array; wrong lists give wrong verdicts). */
-#define BPD_PDA_MAX_FRAME_LISTS 64
-#define BPD_PDA_FRAME_KEY_WORDS 9
+#define BPD_PDA_MAX_FRAME_LISTS 700
+#define BPD_PDA_FRAME_SLOTS 1024
+#define BPD_PDA_FRAME_SUFFIX 4
+#define BPD_PDA_FRAME_KEY_WORDS 48
 #define BPD_PDA_FRAME_SAT 0x10000
+#define BPD_PDA_FRAME_EMPTY 0xFFFFFFFFu
 typedef struct BpdPdaFrames {
   int32_t num_lists;       /* 0 .. BPD_PDA_MAX_FRAME_LISTS */
   int32_t words;           /* (vocab_size + 31) / 32 */
-  const int32_t* keys;     /* [num_lists, BPD_PDA_FRAME_KEY_WORDS]; unused tops -1 */
+  const int32_t* keys;     /* [num_lists, BPD_PDA_FRAME_KEY_WORDS] */
+  const uint32_t* slots;   /* [BPD_PDA_FRAME_SLOTS] */
   const int32_t* trans;    /* [num_lists, 256] */
   const uint32_t* allowed; /* [num_lists, words] */
   const int32_t* seed_off; /* [num_lists + 1] */
@@ -297,6 +311,19 @@ int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out);
  * single reference entry point corresponds (the reference's tests feed bytes
  * through pda_advance_byte directly, test_pda.cpp:46-51). */
 int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data, int64_t n);
+
+/* bpd_host_frame_classify: host only (no counterpart in the reference: it
+ * builds the frame lists' bitmaps and seeds, BpdPdaFrames).  Walks every
+ * token from every list through trans [num_lists, 256] on up to `threads`
+ * host threads: allowed [num_lists, (vocab_size + 31) / 32] gets the inside
+ * tokens, seed_count [num_lists] the number of seeds of each list, and, when
+ * seed_off [num_lists + 1] (offsets matching those counts) and seeds are
+ * given, seeds the walk positions in `order` of each list's seeds,
+ * ascending. */
+int bpd_host_frame_classify(const int32_t* trans, int32_t num_lists, const int32_t* tok_offsets,
+                            const uint8_t* tok_bytes, int32_t vocab_size, int32_t eos_id,
+                            const int32_t* order, uint32_t* allowed, int32_t* seed_count,
+                            const int32_t* seed_off, int32_t* seeds, int32_t threads);
 
 /* bpd_pda_apply_mask: logits[b, t] = neg_inf unless token t is accepted from
  * config-set configs[row(b)] (pda_try_token, pda.hpp:248-258), or for every t

@@ -315,39 +315,71 @@ def test_token_pack_tag_follows_the_table_contents():
     assert len({tag, *others}) == 4
 
 
-def _frame_key_row(cfg: np.ndarray, keys: np.ndarray) -> int:
-    """The frame list a config-set takes on the device (-1: none): every
-    config at one depth >= 2 over the same frames below the top, and the
-    ordered tops equal to a key."""
+def _compose(key: np.ndarray, stack: np.ndarray, sat: int) -> np.ndarray:
+    """The flat config-set of a frame list's key over a common stack."""
+    from bpdecode_amd.grammar.frames import MAX_SUFFIX
+
+    cfg = np.zeros(266, dtype=np.int32)
+    n = int(key[0])
+    cfg[0], cfg[1] = n, sat
+    base = stack.size
+    for i in range(n):
+        ln = int(key[1 + i])
+        cfg[2 + i] = base + ln
+        row = cfg[10 + i * 32:10 + (i + 1) * 32]
+        row[:base] = stack
+        row[base:base + ln] = key[9 + i * MAX_SUFFIX:9 + i * MAX_SUFFIX + ln]
+    return cfg
+
+
+def _meaningful(cfg: np.ndarray) -> list:
     n = int(cfg[0])
-    if n < 1:
-        return -1
-    depth = cfg[2:2 + n]
-    frames = cfg[2 + 8:].reshape(8, 32)
-    d0 = int(depth[0])
-    if d0 < 2 or (depth != d0).any() or (frames[:n, :d0 - 1] != frames[0, :d0 - 1]).any():
-        return -1
-    tops = [int(frames[i, d0 - 1]) for i in range(n)]
-    for l in range(keys.shape[0]):
-        if keys[l, 0] == n and list(keys[l, 1:1 + n]) == tops:
-            return l
-    return -1
+    return [n, int(cfg[1])] + [tuple(cfg[10 + i * 32:10 + i * 32 + int(cfg[2 + i])]) for i in range(n)]
+
+
+def _check_list(t, fl, order_np, cfg, l, base, vsize, what):
+    """A set over list l at common-stack depth `base`: every token outside the
+    list's seeds gets the oracle's verdict from the bitmap, and the oracle's
+    step by each byte reaches the coded list over the same stack (saturation
+    flag included) or empties the set."""
+    want = np.unpackbits(OP.compute_mask(t, cfg[None].copy())[0].view(np.uint8), bitorder="little")
+    have = np.unpackbits(fl.allowed[l].view(np.uint8), bitorder="little")
+    seeded = np.zeros(want.size, dtype=bool)
+    seeded[order_np[fl.seeds[fl.seed_off[l]:fl.seed_off[l + 1]]]] = True
+    V = vsize
+    assert not (have[:V].astype(bool) & seeded[:V]).any(), what
+    off = ~seeded[:V]
+    assert np.array_equal(have[:V][off], want[:V][off]), what
+    assert not have[V:].any()
+    stack = cfg[10:10 + base].copy()
+    for byte in range(256):
+        code = int(fl.trans[l, byte])
+        nxt = cfg.copy()
+        ok = OP.advance_byte(t, nxt, byte)
+        if code == -1:
+            assert not ok, (what, byte)
+        elif code >= 0:
+            assert ok, (what, byte)
+            sat = int(cfg[1]) | (1 if code & 0x10000 else 0)
+            exp = _compose(fl.keys[code & 0xFFFF], stack, sat)
+            assert _meaningful(nxt) == _meaningful(exp), (what, byte)
 
 
 def test_frame_lists_against_the_oracle():
-    """Rows of the recursive JSON grammar whose set sits inside a string or a
-    number: every token outside the list's seeds gets the oracle's verdict
-    from the list's bitmap (inside the rule: allowed; dead before its accept
-    state: rejected).  Prefixes end in string bodies, after an escape
-    backslash, inside UTF-8 sequences and after a minus sign."""
-    from bpdecode_amd.grammar.frames import frame_lists
+    """Stack-relative frame lists against the C oracle: rows of real prefixes
+    (string bodies, escapes, UTF-8 sequences, numbers, nested values) that
+    the matcher finds, and every list composed over an empty and over a
+    3-frame common stack: the bitmap gives the oracle's verdict of every
+    token outside the seeds and the byte table the oracle's step."""
+    from bpdecode_amd.grammar.frames import MAX_LISTS, frame_match, frame_lists
     from bpdecode_amd.tokenizer import Vocabulary
 
-    base = synth.serving_vocab(6000, seed=4)
+    base_v = synth.serving_vocab(6000, seed=4)
     extra = [b"\"", b"\\", b"\\n", b"\\\"", b"\xc3", b"\xa9", b"\xe2\x82", b"\xac\"", b"\xe9", b"ab\"",
-             b"\" :", b"\\u", b"\x01", b"\x7f", b"", b"-1", b"12", b"\"}", b"\xc3\xa9x"]
-    vocab = Vocabulary.from_tokens(list(base.token_bytes[:-1]) + extra + [b"</s>"],
-                                   eos_id=len(base.token_bytes) - 1 + len(extra))
+             b"\" :", b"\\u", b"\x01", b"\x7f", b"", b"-1", b"12", b"\"}", b"\xc3\xa9x", b"[{", b"[[",
+             b"{\"", b"\":[", b"],", b"},{"]
+    vocab = Vocabulary.from_tokens(list(base_v.token_bytes[:-1]) + extra + [b"</s>"],
+                                   eos_id=len(base_v.token_bytes) - 1 + len(extra))
     small = r"""
 root   ::= string | "[" number "]"
 string ::= "\"" ( [^"\\\x00-\x1F] | "\\" ["\\/bfnrt] )* "\""
@@ -355,58 +387,36 @@ number ::= "-"? [0-9]+ ( "." [0-9]+ )?
 """
     rng = np.random.default_rng(17)
     json_prefixes = [b"[\"ab", b"{\"k", b"[\"x\\", b"[\"\xc3", b"[\"\xe2\x82", b"{\"a\":[\"", b"[-",
-                     b"{\"a\":-", b"[\"a\\u00", b"[[[\"deep", b"\"", b"[\"\\\\", b"{\"a\":\"b\",\"c"]
-    json_prefixes += [synth.json_prefix(rng, int(rng.integers(0, 6))) for _ in range(60)]
+                     b"{\"a\":-", b"[\"a\\u00", b"[[[\"deep", b"\"", b"[\"\\\\", b"{\"a\":\"b\",\"c", b"[",
+                     b"[[", b"{\"a\":", b"{\"a\":[", b"[1,", b"{\"a\":{\"b\":["]
+    json_prefixes += [synth.json_prefix(rng, int(rng.integers(0, 9))) for _ in range(80)]
     small_prefixes = [b"\"", b"\"ab", b"\"a\\", b"\"\xc3", b"\"\xe2\x82", b"\"x\\\\y", b"[-", b"[",
                       b"\"\xf0\x9f", b"\"\xf0\x9f\x98", b"\"a b c", b"\"\\n", b"\"\xed\x9f"]
     # the recursive JSON grammar saturates the 8 configs without the
     # epsilon reduction, so unreduced tables are covered by a small grammar
-    for src, reduce, prefixes, need in ((synth.JSON_GBNF, True, json_prefixes, 12),
+    for src, reduce, prefixes, need in ((synth.JSON_GBNF, True, json_prefixes, 60),
                                         (small, False, small_prefixes, 8),
                                         (small, True, small_prefixes, 8)):
         g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(src)), vocab, eps_reduce=reduce)
         t = OP.Table(g)
         order, _ = _walk_order(g.tok_offsets, g.tok_bytes, g.vocab_size, g.eos_id)
-        fl = frame_lists(g, order.numpy())
-        assert fl is not None and 0 < fl.num_lists <= 64
+        order_np = order.numpy()
+        fl = frame_lists(g, order_np)
+        assert fl is not None and 0 < fl.num_lists <= MAX_LISTS
         hits = 0
-        pos = np.empty(vocab.size, dtype=np.int64)
-        pos[order.numpy()] = np.arange(vocab.size)
         for p in prefixes:
             c = g.init_config()
             if not g.feed(c, p):
                 continue
             cfg = c.numpy()
-            l = _frame_key_row(cfg, fl.keys)
+            l, base = frame_match(cfg, fl)
             if l < 0:
                 continue
             hits += 1
-            want = np.unpackbits(OP.compute_mask(t, cfg[None].copy())[0].view(np.uint8), bitorder="little")
-            have = np.unpackbits(fl.allowed[l].view(np.uint8), bitorder="little")
-            seeded = np.zeros(want.size, dtype=bool)
-            seeded[order.numpy()[fl.seeds[fl.seed_off[l]:fl.seed_off[l + 1]]]] = True
-            V = vocab.size
-            assert not (have[:V].astype(bool) & seeded[:V]).any(), p
-            off = ~seeded[:V]
-            assert np.array_equal(have[:V][off], want[:V][off]), p
-            assert not have[V:].any()
-            # the byte table: the oracle's step from the row by each byte
-            # gives the coded list over the same stack (saturation flag
-            # included), or empties the set
-            d0 = int(cfg[2])
-            below = cfg[10:10 + d0 - 1].copy()
-            for byte in range(256):
-                code = int(fl.trans[l, byte])
-                nxt = cfg.copy()
-                ok = OP.advance_byte(t, nxt, byte)
-                if code == -1:
-                    assert not ok, (p, byte)
-                elif code >= 0:
-                    assert ok, (p, byte)
-                    l2 = code & 0xFFFF
-                    assert _frame_key_row(nxt, fl.keys) == l2, (p, byte)
-                    n2 = int(nxt[0])
-                    assert (nxt[2:2 + n2] == d0).all()
-                    assert all((nxt[10 + i * 32:10 + i * 32 + d0 - 1] == below).all() for i in range(n2))
-                    assert int(nxt[1]) == (int(cfg[1]) | (1 if code & 0x10000 else 0)), (p, byte)
+            _check_list(t, fl, order_np, cfg, l, base, vocab.size, p)
+        for l in range(fl.num_lists):
+            for stack in (np.zeros(0, np.int32), np.array([0, 1, 2], np.int32) % g.num_states):
+                cfg = _compose(fl.keys[l], stack, 0)
+                assert frame_match(cfg, fl)[0] >= 0, l
+                _check_list(t, fl, order_np, cfg, l, stack.size, vocab.size, (l, stack.size))
         assert hits >= need, (src[:20], reduce, hits)
