@@ -185,6 +185,9 @@ constexpr uint8_t kTOverflow = 0xFD;
 // interned set has the raw words the step itself gives; ids stay below
 // kMemoIds so that no flagged id reaches the special entries.
 constexpr uint8_t kTExact = 0x80;
+// bit of a frame-list word above the list id and the saturation flag where
+// the depth of the list's common stack starts
+constexpr int kListBase = 17;
 constexpr int kMemoIds = 125;
 
 struct MemoWs {
@@ -717,6 +720,37 @@ __device__ void frame_fill_row(const BpdPdaFrames& f, int l, bool sat, int id, u
   }
 }
 
+// The meaningful words of the set of list `key` over the common stack that
+// config 0 of `src` holds in its first `base` frames, written to `dst`
+// (words past each depth set to 0; dst may be src).  One wave.
+__device__ void compose_list_set(const int32_t* src, int32_t* dst, const int32_t* key, int base, int sat,
+                                 int lane) {
+  const int32_t pw = lane < base ? src[kF + lane] : 0;
+  const int n = key[0];
+  int32_t len[kMaxConfigs];
+#pragma unroll
+  for (int i = 0; i < kMaxConfigs; ++i) len[i] = i < n ? key[1 + i] : 0;
+  wave_sync();
+  for (int w = lane; w < kMaxConfigs * kMaxDepth; w += kWave) {
+    const int i = w / kMaxDepth, k = w % kMaxDepth;
+    const int32_t p = __shfl(pw, k < base ? k : 0);
+    int32_t v = 0;
+    if (i < n) {
+      if (k < base)
+        v = p;
+      else if (k < base + len[i])
+        v = key[1 + kMaxConfigs + i * BPD_PDA_FRAME_SUFFIX + (k - base)];
+    }
+    dst[kF + w] = v;
+  }
+  if (lane < kMaxConfigs) dst[2 + lane] = lane < n ? base + len[lane] : 0;
+  if (lane == 0) {
+    dst[0] = n;
+    dst[1] = sat;
+  }
+  wave_sync();
+}
+
 // LDS bytes a launch of `kernel` can add to its static arrays on the current
 // device (the device's per-workgroup limit less the kernel's own), queried
 // once per device and kernel slot.
@@ -807,7 +841,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t cand_res[kMemoReq];   // >= 0 pool id, -1 empty, -2 new, -4 duplicate, -5 no edge
   __shared__ int32_t cand_lead[kMemoReq];
   __shared__ uint8_t cand_exact[kMemoReq];  // an existing set with every word of the step's
-  __shared__ int32_t cand_list[kMemoReq];  // frame list of a new set (| BPD_PDA_FRAME_SAT), -1 none
+  // frame list of a new set: l | BPD_PDA_FRAME_SAT (the set's saturation
+  // flag) | base << kListBase (the depth of its common stack), -1 none
+  __shared__ int32_t cand_list[kMemoReq];
+  __shared__ int32_t set_list[kMemoSets];  // the same for the interned sets, without the flag
+  __shared__ uint8_t cand_comp[kMemoReq];  // composed from a list's key: raw words unknown
   __shared__ uint32_t fslots[BPD_PDA_FRAME_SLOTS];  // the frame lists' slot table
   __shared__ int32_t cand_id[kMemoReq];
   __shared__ int16_t cand_lo[kMemoReq];
@@ -871,8 +909,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     wave_sync();
     coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
-    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, tid);
-    if (tid == 0) row_list = l0;
+    int base0 = 0;
+    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, tid, &base0);
+    if (tid == 0) {
+      row_list = l0;
+      set_list[0] = l0 >= 0 ? (l0 | (base0 << kListBase)) : -1;
+    }
     if (l0 >= 0) {
       wave_sync();
       frame_fill_row(a.frames, l0, row_cfg[1] != 0, 0, T, tid);
@@ -961,7 +1003,24 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
         const int r_next = next_req(r + kMemoThreads / kWave);
         load_src(r_next);
-        const bool ok = coop_advance_byte(g, set != 0 ? wsrc : row_cfg, wdst, byte, lane);
+        // a set in a frame list whose list leads by this byte to a list
+        // (over the same common stack): the result is composed from the
+        // key instead of stepped
+        const int32_t* src = set != 0 ? wsrc : row_cfg;
+        const int sl = set_list[set];
+        const int code = sl >= 0 ? a.frames.trans[(sl & (BPD_PDA_FRAME_SAT - 1)) * 256 + byte] : -3;
+        bool ok;
+        if (code >= 0) {
+          const int sat = src[1] != 0 || (code & BPD_PDA_FRAME_SAT) != 0 ? 1 : 0;
+          compose_list_set(src, wdst,
+                           a.frames.keys + int64_t(code & (BPD_PDA_FRAME_SAT - 1)) * BPD_PDA_FRAME_KEY_WORDS,
+                           sl >> kListBase, sat, lane);
+          ok = true;
+        } else if (code == -1) {
+          ok = false;
+        } else {
+          ok = coop_advance_byte(g, src, wdst, byte, lane);
+        }
         if (!ok) {
           if (lane == 0) cand_res[r] = -1;
         } else {
@@ -988,8 +1047,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           // a new set is kept in the candidate buffer (its words are needed
           // after this wave's buffer is reused); stored after the pool
           // lookup's loads, which would otherwise wait for these stores
-          const int lst = found == -2 ? frame_list_of(wdst, a.frames, fslots, lane) : -1;
-          if (lane == 0) cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0)) : -1;
+          int lbase = code >= 0 ? (sl >> kListBase) : 0;
+          const int lst = found != -2 ? -1
+                          : code >= 0 ? (code & (BPD_PDA_FRAME_SAT - 1))
+                                      : frame_list_of(wdst, a.frames, fslots, lane, &lbase);
+          if (lane == 0) {
+            cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0) | (lbase << kListBase)) : -1;
+            cand_comp[r] = code >= 0 ? 1 : 0;
+          }
           if (found == -2) {
             int32_t* out = cand + r * kConfigWords;
             for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
@@ -997,7 +1062,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           if (lane == 0) {
             cand_hash[r] = h;
             cand_res[r] = found;
-            cand_exact[r] = found >= 0 && raw ? 1 : 0;
+            cand_exact[r] = found >= 0 && raw && code < 0 ? 1 : 0;
           }
         }
         wave_sync();
@@ -1033,6 +1098,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (id < max_sets) {
         pool_hash[id] = cand_hash[tid];
         set_n[id] = cand_n[tid];
+        set_list[id] = cand_list[tid] >= 0 ? (cand_list[tid] & ~BPD_PDA_FRAME_SAT) : -1;
         for (int i = 0; i < kMaxConfigs; ++i) set_tops[id][i] = cand_tops[tid][i];
         cand_id[tid] = id;
       } else {
@@ -1062,7 +1128,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         for (int c = lo + lane; c <= hi; c += kWave) T[set * 256 + c] = e;
         // the interval's step gives the set's raw words: a new set (its
         // first computation) or an existing one equal in every word
-        const bool exact = (res >= 0 && cand_exact[r]) || (res == -2 && cand_lead[r] == r && id >= 0);
+        const bool exact = (res >= 0 && cand_exact[r]) || (res == -2 && cand_lead[r] == r && id >= 0 && !cand_comp[r]);
         if (exact && lane >= (lo >> 5) && lane <= (hi >> 5)) {
           const int b0 = (lo > lane * 32 ? lo : lane * 32) - lane * 32;
           const int b1 = (hi < lane * 32 + 31 ? hi : lane * 32 + 31) - lane * 32;
@@ -1683,36 +1749,6 @@ __global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a)
 // from the interned set reached, so the written config-set has the raw words
 // of the direct walk.  Otherwise (or when the table walk meets an entry the
 // mask left unresolved) every byte is stepped with advance_byte.
-// The meaningful words of the set of list `key` over the common stack that
-// config 0 of `x` holds in its first `base` frames, written over `x` (words
-// past each depth set to 0).  One wave.
-__device__ void compose_list_set(int32_t* x, const int32_t* key, int base, int sat, int lane) {
-  const int32_t pw = lane < base ? x[kF + lane] : 0;
-  const int n = key[0];
-  int32_t len[kMaxConfigs];
-#pragma unroll
-  for (int i = 0; i < kMaxConfigs; ++i) len[i] = i < n ? key[1 + i] : 0;
-  wave_sync();
-  for (int w = lane; w < kMaxConfigs * kMaxDepth; w += kWave) {
-    const int i = w / kMaxDepth, k = w % kMaxDepth;
-    const int32_t p = __shfl(pw, k < base ? k : 0);
-    int32_t v = 0;
-    if (i < n) {
-      if (k < base)
-        v = p;
-      else if (k < base + len[i])
-        v = key[1 + kMaxConfigs + i * BPD_PDA_FRAME_SUFFIX + (k - base)];
-    }
-    x[kF + w] = v;
-  }
-  if (lane < kMaxConfigs) x[2 + lane] = lane < n ? base + len[lane] : 0;
-  if (lane == 0) {
-    x[0] = n;
-    x[1] = sat;
-  }
-  wave_sync();
-}
-
 // The memoised commit: one row per workgroup.  All its threads stage the
 // row's transition table in LDS with one round of loads (the walk over the
 // token's bytes is then a chain of LDS reads, not of global ones); wave 0
@@ -1820,7 +1856,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
             if (j < e - 1 && code == -1) {
               ok = false;  // the list (and so the set) empties at byte j
             } else if (j > i) {
-              compose_list_set(x, a.frames.keys + int64_t(l) * BPD_PDA_FRAME_KEY_WORDS, base, sat, lane);
+              compose_list_set(x, x, a.frames.keys + int64_t(l) * BPD_PDA_FRAME_KEY_WORDS, base, sat, lane);
               i = j;
             }
           }
