@@ -788,6 +788,137 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_wave_kernel(
   }
 }
 
+// Member-list statistics, grid (G, rows): block g takes tokens [8192 g,
+// 8192 (g + 1)) of its row, 32 per thread (eight float4 groups in flight),
+// and stages them in LDS.  Each wave shifts by its own maximum M_w: the
+// chunk logsumexp as in prior_stats_wave_kernel.  The class sums come from
+// the member lists of the block's two 4096-token chunks alone (no per-token
+// class test): member o of class c adds exp(x_o - M_w) to the class sum of
+// the wave w that loaded token o ((o >> 8) & 3 in this layout).  Partials,
+// the exact path for members more than 80 below their wave's maximum and
+// the outputs are those of prior_stats_wave_kernel.  Dynamic LDS: the 8192
+// logits, 4 * C wave sums, C class maxima and C sums (exact path).
+template <int Cap>
+__global__ __launch_bounds__(kPriorThreads) void prior_stats_list_kernel(
+    const float* __restrict__ logits, int64_t ld, int64_t V, const uint32_t* __restrict__ members,
+    int32_t C, PriorWs ws) {
+  static_assert(kWideChunk == 2 * BPD_SOFT_MEMBER_CHUNK, "a block covers two member chunks");
+  extern __shared__ __align__(16) float smem[];
+  constexpr int kWaves = kPriorThreads / 64;
+  constexpr int kHalf = Cap / kPriorThreads;  // member slots per thread and chunk
+  float4* xs = reinterpret_cast<float4*>(smem);                   // [kWideChunk / 4]
+  float* wsum = smem + kWideChunk;                                // [kWaves][C]
+  int32_t* cmax = reinterpret_cast<int32_t*>(wsum + kWaves * C);  // [C] exact path
+  float* esum = wsum + kWaves * C + C;                            // [C] exact path
+  __shared__ float wm[kWaves], wl[kWaves];
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x / 64;
+  const float* row = logits + b * ld;
+  const int64_t base = int64_t(g) * kWideChunk;
+  const int64_t nchunks = (V + BPD_SOFT_MEMBER_CHUNK - 1) / BPD_SOFT_MEMBER_CHUNK;
+  // the member entries first: loads complete in issue order, so waiting for
+  // them does not wait for the logits
+  uint32_t mm[2 * kHalf];
+#pragma unroll
+  for (int j = 0; j < 2 * kHalf; ++j) {
+    const int64_t ch = 2 * int64_t(g) + j / kHalf;
+    mm[j] = ch < nchunks ? members[ch * Cap + (j % kHalf) * kPriorThreads + threadIdx.x] : 0xFFFFFFFFu;
+  }
+  float4 x[kWideLoads];
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) {
+    const int64_t t = base + (int64_t(u) * kPriorThreads + threadIdx.x) * 4;
+    x[u] = t < V ? *reinterpret_cast<const float4*>(row + t)
+                 : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  }
+  for (int32_t c = threadIdx.x; c < kWaves * C; c += kPriorThreads) wsum[c] = 0.0f;
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  float sum = 0.0f;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int u = 0; u < kWideLoads; ++u)
+      sum += (exp_shift(x[u].x, m) + exp_shift(x[u].y, m)) + (exp_shift(x[u].z, m) + exp_shift(x[u].w, m));
+  }
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+#pragma unroll
+  for (int u = 0; u < kWideLoads; ++u) xs[u * kPriorThreads + threadIdx.x] = x[u];
+  if (lane == 0) {
+    wm[w] = m;
+    wl[w] = sum;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Lse r{-INFINITY, 0.0f};
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) r = lse_merge_fast(r, Lse{wm[i], wl[i]});
+    ws.part[(b * G + g) * 2] = r.m;
+    ws.part[(b * G + g) * 2 + 1] = r.s;
+  }
+  const float* xf = smem;
+  float v[2 * kHalf];
+  bool under = false;
+#pragma unroll
+  for (int j = 0; j < 2 * kHalf; ++j) {
+    v[j] = -INFINITY;
+    if (mm[j] != 0xFFFFFFFFu) {
+      const int o = int(mm[j] >> 16) + (j / kHalf) * BPD_SOFT_MEMBER_CHUNK;
+      const int ow = (o >> 8) & (kWaves - 1);
+      v[j] = xf[o];
+      if (v[j] != -INFINITY) {
+        const float mw = wm[ow];
+        under = under || v[j] - mw < -80.0f;
+        atomicAdd(&wsum[ow * C + int32_t(mm[j] & 0xFFFFu)], exp_shift(v[j], mw));
+      }
+    }
+  }
+  const bool exact = __syncthreads_or(under);
+  float* out = ws.mid + (b * G + g) * int64_t(C) * 2;
+  if (!exact) {
+    for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+      float cm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i)
+        if (wsum[i * C + c] > 0.0f) cm = fmaxf(cm, wm[i]);
+      float cs = 0.0f;
+      if (cm != -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i)
+          if (wsum[i * C + c] > 0.0f) cs += wsum[i * C + c] * exp_shift(wm[i], cm);
+      }
+      out[2 * c] = cm;
+      out[2 * c + 1] = cs;
+    }
+    return;
+  }
+  // exact path: per-class maximum over the members, then the sums
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    cmax[c] = ord_of(-INFINITY);
+    esum[c] = 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2 * kHalf; ++j)
+    if (v[j] != -INFINITY) atomicMax(&cmax[int32_t(mm[j] & 0xFFFFu)], ord_of(v[j]));
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2 * kHalf; ++j) {
+    if (v[j] != -INFINITY) {
+      const int32_t c = int32_t(mm[j] & 0xFFFFu);
+      atomicAdd(&esum[c], exp_shift(v[j], float_of_ord(cmax[c])));
+    }
+  }
+  __syncthreads();
+  for (int32_t c = threadIdx.x; c < C; c += kPriorThreads) {
+    out[2 * c] = float_of_ord(cmax[c]);
+    out[2 * c + 1] = esum[c];
+  }
+}
+
 // Pieces stats, grid (G + Gp, rows): block g < G takes vocab chunk g
 // (partial row logsumexp), blocks G.. the class pieces (one wave per piece,
 // unnormalised piece logsumexp).
@@ -917,6 +1048,126 @@ __device__ inline float prior_value(float x, float lse, int64_t t, float z, bool
   return alpha != 0.0f ? fmaf(alpha, z, lp) : lp;
 }
 
+// The rounds and the epilogue of the prior lookahead for row b, by the
+// kRoundThreads threads of its block: lc holds the class logsumexps of the
+// row (LDS, reused for zcls), z0 / z1 the state values (z0 initialised: 0
+// for live states, -inf else), flag / so the state flags and pair offsets,
+// pr the pairs (PairsInLds); writes zcls[b] and lse[b] to the workspace.
+template <bool PairsInLds>
+__device__ __forceinline__ void prior_rounds_tail(float* lc, float* z0, float* z1, const uint8_t* flag,
+                                                  const int32_t* so, const uint32_t* pr,
+                                                  const BpdSoftClasses& cls, int32_t S, int32_t rounds,
+                                                  float lse, float lp_eos, int32_t sb, int64_t b,
+                                                  const PriorWs& ws) {
+  const int tid = threadIdx.x;
+  const int32_t C = cls.num_classes;
+  // eight lanes per state: lane l folds pairs l, l + 8, ... of its state
+  constexpr int kLanes = 8;
+  constexpr int kGroups = kRoundThreads / kLanes;
+  constexpr int kRegPairs = 16;  // pairs per lane kept in registers across the rounds
+  const int grp = tid / kLanes, gl = tid % kLanes;
+  float* zc = z0;
+  float* zn = z1;
+  // the fold of one (value, ...) into a running (max, sum of exp(v - max))
+  auto fold = [](float& m, float& sm, float x) {
+    if (x == -INFINITY) return;
+    if (x > m) {
+      sm = (m == -INFINITY ? 0.0f : sm * exp_shift(m, x)) + 1.0f;
+      m = x;
+    } else {
+      sm += exp_shift(x, m);
+    }
+  };
+  // the group's (max, sum) into zn[s]
+  auto finish = [&](int32_t s, bool on, float m, float sm) {
+    quad_lse_step<kDppQuadXor1>(m, sm);
+    quad_lse_step<kDppQuadXor2>(m, sm);
+    {
+      // the two quads of the state
+      const float mo = __shfl_xor(m, 4), so4 = __shfl_xor(sm, 4);
+      const float nm = fmaxf(m, mo);
+      if (nm != -INFINITY) sm = sm * exp_shift(m, nm) + so4 * exp_shift(mo, nm);
+      m = nm;
+    }
+    if (on && gl == 0) {
+      const uint8_t f = flag[s];
+      float v = m == -INFINITY ? -INFINITY : m + logf(sm) - lse;
+      if (f & 2) v = log_add_exp(v, lp_eos);
+      zn[s] = (f & 1) ? v : -INFINITY;
+    }
+  };
+  if (S <= kGroups) {
+    // one state per group; a lane's first kRegPairs pairs are gathered once
+    // as (class logsumexp, next state), so a round reads only zc for them
+    const int32_t s = grp;
+    const bool on = s < S;
+    const int32_t i0 = on ? so[s] : 0, i1 = on ? so[s + 1] : 0;
+    float w[kRegPairs];
+    int32_t nx[kRegPairs];
+#pragma unroll
+    for (int u = 0; u < kRegPairs; ++u) {
+      const int32_t i = i0 + gl + kLanes * u;
+      const uint32_t p = i < i1 ? prior_pair<PairsInLds>(pr, cls, i) : 0u;
+      w[u] = i < i1 ? lc[p >> 16] : -INFINITY;
+      nx[u] = i < i1 ? int32_t(p & 0xFFFFu) : 0;
+    }
+    const int32_t i_rest = i0 + kLanes * kRegPairs;
+    for (int32_t j = 0; j < rounds; ++j) {
+      float v[kRegPairs];
+#pragma unroll
+      for (int u = 0; u < kRegPairs; ++u) v[u] = w[u] + zc[nx[u]];  // zc is never +inf
+      float m = v[0];
+#pragma unroll
+      for (int u = 1; u < kRegPairs; ++u) m = fmaxf(m, v[u]);
+      float sm = 0.0f;
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < kRegPairs; ++u) sm += exp_shift(v[u], m);
+      }
+      for (int32_t i = i_rest + gl; i < i1; i += kLanes) {
+        const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
+        fold(m, sm, lc[p >> 16] + zc[p & 0xFFFFu]);
+      }
+      finish(s, on, m, sm);
+      __syncthreads();
+      float* t = zc;
+      zc = zn;
+      zn = t;
+    }
+  } else {
+    for (int32_t j = 0; j < rounds; ++j) {
+      for (int32_t s0 = 0; s0 < S; s0 += kGroups) {
+        const int32_t s = s0 + grp;
+        const bool on = s < S;
+        const int32_t i1 = on ? so[s + 1] : 0;
+        float m = -INFINITY, sm = 0.0f;
+        for (int32_t i = (on ? so[s] : 0) + gl; i < i1; i += kLanes) {
+          const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
+          fold(m, sm, lc[p >> 16] + zc[p & 0xFFFFu]);
+        }
+        finish(s, on, m, sm);
+      }
+      __syncthreads();
+      float* t = zc;
+      zc = zn;
+      zn = t;
+    }
+  }
+
+  // zcls[b, c] = logZ(next state of class c from s_b), -inf when rejected
+  for (int32_t c = tid; c < C; c += kRoundThreads) lc[c] = -INFINITY;
+  __syncthreads();
+  if (sb >= 0 && sb < S) {
+    for (int32_t i = so[sb] + tid; i < so[sb + 1]; i += kRoundThreads) {
+      const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
+      lc[p >> 16] = zc[p & 0xFFFFu];
+    }
+  }
+  __syncthreads();
+  for (int32_t c = tid; c < C; c += kRoundThreads) ws.zcls[b * C + c] = lc[c];
+  if (tid == 0) ws.lse[b] = lse;
+}
+
 template <bool PairsInLds, bool ClassStats>
 __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
     const float* __restrict__ logits, int64_t ld, int32_t S, int G, BpdSoftClasses cls,
@@ -1039,112 +1290,7 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
   __syncthreads();
   const float lse = lse_sh;
   const float lp_eos = eos >= 0 ? x_eos - lse : -INFINITY;
-
-  // eight lanes per state: lane l folds pairs l, l + 8, ... of its state
-  constexpr int kLanes = 8;
-  constexpr int kGroups = kRoundThreads / kLanes;
-  constexpr int kRegPairs = 16;  // pairs per lane kept in registers across the rounds
-  const int grp = tid / kLanes, gl = tid % kLanes;
-  float* zc = z0;
-  float* zn = z1;
-  // the fold of one (value, ...) into a running (max, sum of exp(v - max))
-  auto fold = [](float& m, float& sm, float x) {
-    if (x == -INFINITY) return;
-    if (x > m) {
-      sm = (m == -INFINITY ? 0.0f : sm * exp_shift(m, x)) + 1.0f;
-      m = x;
-    } else {
-      sm += exp_shift(x, m);
-    }
-  };
-  // the group's (max, sum) into zn[s]
-  auto finish = [&](int32_t s, bool on, float m, float sm) {
-    quad_lse_step<kDppQuadXor1>(m, sm);
-    quad_lse_step<kDppQuadXor2>(m, sm);
-    {
-      // the two quads of the state
-      const float mo = __shfl_xor(m, 4), so4 = __shfl_xor(sm, 4);
-      const float nm = fmaxf(m, mo);
-      if (nm != -INFINITY) sm = sm * exp_shift(m, nm) + so4 * exp_shift(mo, nm);
-      m = nm;
-    }
-    if (on && gl == 0) {
-      const uint8_t f = flag[s];
-      float v = m == -INFINITY ? -INFINITY : m + logf(sm) - lse;
-      if (f & 2) v = log_add_exp(v, lp_eos);
-      zn[s] = (f & 1) ? v : -INFINITY;
-    }
-  };
-  if (S <= kGroups) {
-    // one state per group; a lane's first kRegPairs pairs are gathered once
-    // as (class logsumexp, next state), so a round reads only zc for them
-    const int32_t s = grp;
-    const bool on = s < S;
-    const int32_t i0 = on ? so[s] : 0, i1 = on ? so[s + 1] : 0;
-    float w[kRegPairs];
-    int32_t nx[kRegPairs];
-#pragma unroll
-    for (int u = 0; u < kRegPairs; ++u) {
-      const int32_t i = i0 + gl + kLanes * u;
-      const uint32_t p = i < i1 ? prior_pair<PairsInLds>(pr, cls, i) : 0u;
-      w[u] = i < i1 ? lc[p >> 16] : -INFINITY;
-      nx[u] = i < i1 ? int32_t(p & 0xFFFFu) : 0;
-    }
-    const int32_t i_rest = i0 + kLanes * kRegPairs;
-    for (int32_t j = 0; j < rounds; ++j) {
-      float v[kRegPairs];
-#pragma unroll
-      for (int u = 0; u < kRegPairs; ++u) v[u] = w[u] + zc[nx[u]];  // zc is never +inf
-      float m = v[0];
-#pragma unroll
-      for (int u = 1; u < kRegPairs; ++u) m = fmaxf(m, v[u]);
-      float sm = 0.0f;
-      if (m != -INFINITY) {
-#pragma unroll
-        for (int u = 0; u < kRegPairs; ++u) sm += exp_shift(v[u], m);
-      }
-      for (int32_t i = i_rest + gl; i < i1; i += kLanes) {
-        const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
-        fold(m, sm, lc[p >> 16] + zc[p & 0xFFFFu]);
-      }
-      finish(s, on, m, sm);
-      __syncthreads();
-      float* t = zc;
-      zc = zn;
-      zn = t;
-    }
-  } else {
-    for (int32_t j = 0; j < rounds; ++j) {
-      for (int32_t s0 = 0; s0 < S; s0 += kGroups) {
-        const int32_t s = s0 + grp;
-        const bool on = s < S;
-        const int32_t i1 = on ? so[s + 1] : 0;
-        float m = -INFINITY, sm = 0.0f;
-        for (int32_t i = (on ? so[s] : 0) + gl; i < i1; i += kLanes) {
-          const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
-          fold(m, sm, lc[p >> 16] + zc[p & 0xFFFFu]);
-        }
-        finish(s, on, m, sm);
-      }
-      __syncthreads();
-      float* t = zc;
-      zc = zn;
-      zn = t;
-    }
-  }
-
-  // zcls[b, c] = logZ(next state of class c from s_b), -inf when rejected
-  for (int32_t c = tid; c < C; c += kRoundThreads) lc[c] = -INFINITY;
-  __syncthreads();
-  if (sb >= 0 && sb < S) {
-    for (int32_t i = so[sb] + tid; i < so[sb + 1]; i += kRoundThreads) {
-      const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
-      lc[p >> 16] = zc[p & 0xFFFFu];
-    }
-  }
-  __syncthreads();
-  for (int32_t c = tid; c < C; c += kRoundThreads) ws.zcls[b * C + c] = lc[c];
-  if (tid == 0) ws.lse[b] = lse;
+  prior_rounds_tail<PairsInLds>(lc, z0, z1, flag, so, pr, cls, S, rounds, lse, lp_eos, sb, b, ws);
 }
 
 constexpr int kOutLoads = 4;          // float4 loads in flight per thread (prior_out_kernel)
@@ -1230,6 +1376,77 @@ __global__ __launch_bounds__(kPriorOutThreads) void prior_out_kernel(
 }
 
 
+// Member-list output, grid (ceil(V / 4096), rows): block g rewrites the
+// 4096-token member chunk g of its row.  The chunk is staged in LDS as -inf;
+// the threads take the chunk's member list (Cap slots, 0xFFFFFFFF empty),
+// gather the logits of the members whose class has a finite lookahead value
+// from the row's state and write x - lse + alpha * z there (EOS: its log
+// softmax when the state accepts); the chunk then goes out as coalesced
+// float4 stores (every 128-byte line written whole).  Needs vocab, ld and
+// the logits aligned to 4 floats.
+template <int Cap>
+__global__ __launch_bounds__(kPriorOutThreads) void prior_out_list_kernel(
+    float* __restrict__ logits, int64_t ld, int64_t V, const uint32_t* __restrict__ members, int32_t C,
+    const float* __restrict__ lse_in, const float* __restrict__ zcls, int32_t S,
+    const uint8_t* __restrict__ accept, int32_t eos, const int32_t* __restrict__ states,
+    const int64_t* __restrict__ slots, float alpha, int32_t* __restrict__ err) {
+  constexpr int kSlots = Cap / kPriorOutThreads;
+  constexpr int kGroups = BPD_SOFT_MEMBER_CHUNK / 4 / kPriorOutThreads;  // float4 groups per thread
+  __shared__ float4 outs[BPD_SOFT_MEMBER_CHUNK / 4];
+  __shared__ float zs[kLdsClasses];
+  const int64_t b = blockIdx.y;
+  const int64_t base = int64_t(blockIdx.x) * BPD_SOFT_MEMBER_CHUNK;
+  const int32_t s = states[slots ? slots[b] : b];
+  float* row = logits + b * ld;
+  const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  if (s < 0 || s >= S) {
+    if (s >= S && err && blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, BPD_FLAG_STATE_RANGE);
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) {
+      const int64_t t = base + (int64_t(q) * kPriorOutThreads + threadIdx.x) * 4;
+      if (t < V) *reinterpret_cast<float4*>(row + t) = ninf;
+    }
+    return;
+  }
+  uint32_t mm[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) mm[j] = members[int64_t(blockIdx.x) * Cap + j * kPriorOutThreads + threadIdx.x];
+  const float* zrow = zcls + b * C;
+  for (int32_t c = threadIdx.x; c < C; c += kPriorOutThreads) zs[c] = zrow[c];
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) outs[q * kPriorOutThreads + threadIdx.x] = ninf;
+  const float lse = lse_in[b];
+  const bool acc_s = accept[s] != 0;
+  __syncthreads();
+  // gathers of the members that keep a finite value (all issued, then used)
+  float xv[kSlots], zv[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    zv[j] = -INFINITY;
+    if (mm[j] != 0xFFFFFFFFu) {
+      const int64_t t = base + int64_t(mm[j] >> 16);
+      if (t != eos) zv[j] = zs[mm[j] & 0xFFFFu];
+    }
+    xv[j] = zv[j] != -INFINITY ? row[base + int64_t(mm[j] >> 16)] : 0.0f;
+  }
+  float* of = reinterpret_cast<float*>(outs);
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    if (zv[j] != -INFINITY) {
+      const float lp = xv[j] - lse;
+      of[mm[j] >> 16] = alpha != 0.0f ? fmaf(alpha, zv[j], lp) : lp;
+    }
+  }
+  if (threadIdx.x == 0 && eos >= base && eos < base + BPD_SOFT_MEMBER_CHUNK && eos < V)
+    of[eos - base] = acc_s ? row[eos] - lse : -INFINITY;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    const int64_t t = base + (int64_t(q) * kPriorOutThreads + threadIdx.x) * 4;
+    if (t < V) *reinterpret_cast<float4*>(row + t) = outs[q * kPriorOutThreads + threadIdx.x];
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool force_pieces() {
@@ -1237,15 +1454,17 @@ bool force_pieces() {
   return e && *e && std::strcmp(e, "0") != 0;
 }
 
-// BPD_SOFT_STATS=members / classes selects the 4096-token class statistics
-// (the member lists / the class map) instead of the wave-shift kernel (tests
-// of those paths); BPD_SOFT_MEMBERS=0 selects the class map too
+// BPD_SOFT_STATS=wave selects the wave-shift statistics over the class map
+// (with the class-map output pass), members / classes the 4096-token class
+// statistics (the member lists / the class map) instead of the member-list
+// statistics and output (tests of those paths); BPD_SOFT_MEMBERS=0 selects
+// the class map too
 const char* stats_choice() {
   const char* e = std::getenv("BPD_SOFT_STATS");
   if (e && *e) return e;
   const char* me = std::getenv("BPD_SOFT_MEMBERS");
   if (me && std::strcmp(me, "0") == 0) return "classes";
-  return "wave";
+  return "list";
 }
 
 }  // namespace
@@ -1288,9 +1507,16 @@ int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int3
                   cls.piece_off && cls.state_off && cls.token_class,
               "null pointer argument");
   const char* choice = stats_choice();
-  const bool wide_ok = std::strcmp(choice, "wave") == 0 && cls.token_class16 != nullptr &&
-                       cls.num_classes < 65535 && vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) &&
-                       (reinterpret_cast<uintptr_t>(cls.token_class16) & 7u) == 0;
+  // member lists: statistics over each 8192-token block's members and the
+  // output pass over each 4096-token chunk's members (the default)
+  const bool list_ok = std::strcmp(choice, "list") == 0 && cls.chunk_members != nullptr &&
+                       cls.num_classes < 65535 &&
+                       (cls.chunk_cap == 256 || cls.chunk_cap == 512 || cls.chunk_cap == 1024) &&
+                       vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits);
+  const bool wide_ok = (std::strcmp(choice, "wave") == 0 && cls.token_class16 != nullptr &&
+                        cls.num_classes < 65535 && vocab % 4 == 0 && ld % 4 == 0 && aligned16(logits) &&
+                        (reinterpret_cast<uintptr_t>(cls.token_class16) & 7u) == 0) ||
+                       list_ok;
   const PriorPlan pl = prior_plan(rows, vocab, cls.num_classes, cls.num_pieces, force_pieces(), wide_ok);
   const bool pieces = !pl.class_stats;
   const bool pairs_in_lds =
@@ -1316,7 +1542,17 @@ int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int3
                          cls.num_classes < 65535 && std::strcmp(choice, "classes") != 0 &&
                          (cls.chunk_cap == 256 || cls.chunk_cap == 512 || cls.chunk_cap == 1024);
     const size_t mlds = size_t(kStatChunk) * sizeof(float) + size_t(cls.num_classes) * 8;
-    if (pl.wide)
+    const size_t llds = (size_t(kWideChunk) + size_t(kPriorThreads / 64 + 2) * cls.num_classes) * 4;
+    if (pl.wide && list_ok && cls.chunk_cap == 256)
+      prior_stats_list_kernel<256><<<grid, kPriorThreads, llds, st>>>(logits, ld, vocab, cls.chunk_members,
+                                                                      cls.num_classes, ws);
+    else if (pl.wide && list_ok && cls.chunk_cap == 512)
+      prior_stats_list_kernel<512><<<grid, kPriorThreads, llds, st>>>(logits, ld, vocab, cls.chunk_members,
+                                                                      cls.num_classes, ws);
+    else if (pl.wide && list_ok)
+      prior_stats_list_kernel<1024><<<grid, kPriorThreads, llds, st>>>(logits, ld, vocab, cls.chunk_members,
+                                                                       cls.num_classes, ws);
+    else if (pl.wide)
       prior_stats_wave_kernel<<<grid, kPriorThreads, size_t(cls.num_classes) * (kPriorThreads / 64 + 2) * 4, st>>>(
           logits, ld, vocab, cls.token_class16, cls.num_classes, ws);
     else if (members && cls.chunk_cap == 256)
@@ -1360,13 +1596,22 @@ int soft_prior_impl(float* logits, int64_t rows, int64_t vocab, int64_t ld, int3
   prior_out_kernel<VEC, ZL, NW><<<ogrid, kPriorOutThreads, 0, st>>>(                            \
       logits, ld, vocab, cls.token_class, cls.token_class16, cls.num_classes, ws.lse, ws.zcls,   \
       num_states, accept, eos_id, states, slots, alpha, err)
-  if (onarrow && z_lds) BPD_PRIOR_OUT(true, true, true);
+  const dim3 lgrid = dim3(unsigned((vocab + BPD_SOFT_MEMBER_CHUNK - 1) / BPD_SOFT_MEMBER_CHUNK), unsigned(rows));
+#define BPD_PRIOR_OUT_LIST(CAP)                                                                      \
+  prior_out_list_kernel<CAP><<<lgrid, kPriorOutThreads, 0, st>>>(                                   \
+      logits, ld, vocab, cls.chunk_members, cls.num_classes, ws.lse, ws.zcls, num_states, accept, eos_id, \
+      states, slots, alpha, err)
+  if (list_ok && pl.class_stats && cls.chunk_cap == 256) BPD_PRIOR_OUT_LIST(256);
+  else if (list_ok && pl.class_stats && cls.chunk_cap == 512) BPD_PRIOR_OUT_LIST(512);
+  else if (list_ok && pl.class_stats) BPD_PRIOR_OUT_LIST(1024);
+  else if (onarrow && z_lds) BPD_PRIOR_OUT(true, true, true);
   else if (onarrow) BPD_PRIOR_OUT(true, false, true);
   else if (vec && z_lds) BPD_PRIOR_OUT(true, true, false);
   else if (vec) BPD_PRIOR_OUT(true, false, false);
   else if (z_lds) BPD_PRIOR_OUT(false, true, false);
   else BPD_PRIOR_OUT(false, false, false);
 #undef BPD_PRIOR_OUT
+#undef BPD_PRIOR_OUT_LIST
   BPD_LAUNCHED();
   return BPD_OK;
 }

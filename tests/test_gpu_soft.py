@@ -132,13 +132,14 @@ def test_prior_unaligned_vocab(dev):
     assert torch.equal(w[:, V:].cpu(), wide[:, V:])
 
 
-@pytest.mark.parametrize("stats", ["wave", "members", "classes"])
+@pytest.mark.parametrize("stats", ["list", "wave", "members", "classes"])
 def test_prior_email_serving(dev, stats, monkeypatch):
     """B=128, V=151,936, k=4 over the email DFA: four rows against the
     oracle, every row against the alpha-free identity (alpha = 0 leaves
     log_softmax on tokens whose k-1 lookahead is finite); class statistics
-    with wave shifts over 8192-token chunks, from the chunk
-    member lists and from the class map."""
+    with wave shifts over 8192-token chunks from the chunk member lists (and
+    the member-list output pass) or from the class map, and over
+    4096-token chunks from the member lists and from the class map."""
     monkeypatch.setenv("BPD_SOFT_STATS", stats)
     vocab = synth.serving_vocab(151_936, seed=1)
     fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
@@ -198,9 +199,10 @@ def test_prior_pieces_path_email(dev, monkeypatch):
 @pytest.mark.parametrize("vocab", ["v17", "v20"])
 def test_prior_wide_class_map_and_extreme_logits(dev, monkeypatch, vocab):
     """Every statistics path gives the oracle's results: wave shifts over the
-    uint16 class map (the -1e4 logits sit far below their wave's maximum, so
-    those blocks take the exact per-class maximum), the chunk member lists,
-    the uint16 class map and the int32 one.  Rows mixing -inf, very negative
+    member lists (with the member-list output pass) and over the uint16
+    class map (the -1e4 logits sit far below their wave's maximum, so those
+    blocks take the exact per-class maximum), the 4096-token chunk member
+    lists, the uint16 class map and the int32 one.  Rows mixing -inf, very negative
     and large logits keep every class sum exact."""
     fsa = FsaTensors.build("-?[0-9]+(\\.[0-9]+)?", TOY_VOCAB if vocab == "v17" else TOY_VOCAB20).densify()
     S, V = fsa.tok_next.shape
@@ -218,7 +220,7 @@ def test_prior_wide_class_map_and_extreme_logits(dev, monkeypatch, vocab):
     a = x.to(dev)
     ops.apply_soft_prior_(a, fd, st.to(dev), 4, 0.8)
     assert close(a.cpu().double().numpy(), want)
-    for stats in ("members", "classes"):
+    for stats in ("wave", "members", "classes"):
         monkeypatch.setenv("BPD_SOFT_STATS", stats)
         m = x.to(dev)
         ops.apply_soft_prior_(m, fd, st.to(dev), 4, 0.8)
