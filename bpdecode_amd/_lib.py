@@ -94,6 +94,9 @@ _SIGNATURES = {
     "bpd_pda_init": (cint, [C.POINTER(PdaTableC), vp]),
     "bpd_pda_feed": (cint, [C.POINTER(PdaTableC), vp, C.c_char_p, i64]),
     "bpd_host_frame_classify": (cint, [vp, i32, vp, vp, i32, i32, vp, vp, vp, vp, vp, i32]),
+    "bpd_host_frame_lists": (cint, [C.POINTER(PdaTableC), i32, vp, vp, vp]),
+    "bpd_frame_classify": (cint, [vp, i32, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
+    "bpd_frame_classify_blocks": (i32, [i32]),
     "bpd_pda_workspace_bytes": (sz, [i64, i32]),
     "bpd_pda_apply_mask": (cint, [C.POINTER(PdaTableC), C.POINTER(TokenBytesC), vp, vp, vp,
                                   i64, vp, cint, i64, f64, vp, sz, vp]),

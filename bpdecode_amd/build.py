@@ -19,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = CSRC / "_build"
 LIB = PKG / "libbpdecode_hip.so"
-SOURCES = ["dense.hip", "fsa.hip", "pda.hip", "soft.hip", "stage.hip", "host.cpp"]
+SOURCES = ["dense.hip", "fsa.hip", "pda.hip", "soft.hip", "stage.hip", "frames.hip", "host.cpp"]
 ARCH = os.environ.get("BPDECODE_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [

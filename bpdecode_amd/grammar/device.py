@@ -166,14 +166,11 @@ class PdaTensors:
             order, runs = _walk_order(off, tb, self.vocab_size, self.eos_id)
             keep = [off, tb, order.to(off.device), runs.to(off.device)]
             frames = None
-            fl = frame_lists(self, order.numpy())
+            fl = frame_lists(self, order)
             if fl is not None and fl.num_lists > 0:
                 dev = off.device
-                arrs = [torch.from_numpy(fl.keys).to(dev), torch.from_numpy(fl.slots.view("<i4")).to(dev),
-                        torch.from_numpy(fl.trans).to(dev),
-                        torch.from_numpy(fl.allowed.view("<i4")).to(dev),
-                        torch.from_numpy(fl.seed_off).to(dev),
-                        torch.from_numpy(fl.seeds if fl.seeds.size else np.zeros(1, np.int32)).to(dev)]
+                seeds = fl.seeds if fl.seeds.numel() else torch.zeros(1, dtype=torch.int32)
+                arrs = [a.to(dev).contiguous() for a in (fl.keys, fl.slots, fl.trans, fl.allowed, fl.seed_off, seeds)]
                 keep += arrs
                 frames = _lib.PdaFramesC(fl.num_lists, fl.allowed.shape[1], *(ptr(a) for a in arrs))
                 self._c["frames"] = frames

@@ -26,34 +26,53 @@ below it (most specific first), through a hash table of the keys.
 
 from __future__ import annotations
 
+import ctypes as C
+import os
 from dataclasses import dataclass
 
 import numpy as np
+import torch
 
-MAX_SUFFIX = 4  # frames of a suffix
+from .. import _lib
+
+MAX_SUFFIX = 4  # frames of a suffix (BPD_PDA_FRAME_SUFFIX)
 SLOTS = 1024  # hash-table slots (staged in LDS by the mask kernel)
 MAX_LISTS = 700  # at most 0.7 * SLOTS keys
 KEY_WORDS = 48  # n, 8 suffix lengths, 8 x MAX_SUFFIX frames, padding
 SAT = 0x10000  # transition flag: the step dropped a config at the 8-config cap
 EMPTY = 0xFFFFFFFF
-_EPS, _BYTE, _CALL = 0, 1, 2
-_DEAD, _BOUNDARY = -1, -2
 _CAP = 8  # configs per set
 _MAXD = 32  # frames per config
 
 
 @dataclass
 class FrameLists:
-    keys: np.ndarray  # int32 [L, KEY_WORDS]
-    slots: np.ndarray  # uint32 [SLOTS]: list id | fingerprint << 12, EMPTY
-    trans: np.ndarray  # int32 [L, 256]: list reached (| SAT), -1 empty, -2 boundary
-    allowed: np.ndarray  # uint32 [L, ceil(V/32)]
-    seed_off: np.ndarray  # int32 [L + 1]
-    seeds: np.ndarray  # int32 walk positions
+    """The lists on the tables' device: ``keys`` int32 [L, KEY_WORDS],
+    ``slots`` int32 [SLOTS] (uint32 words: list id | fingerprint << 12, or
+    EMPTY), ``trans`` int32 [L, 256] (list reached | SAT, -1 empty, -2
+    boundary), ``allowed`` int32 [L, ceil(V/32)] (uint32 words), ``seed_off``
+    int32 [L + 1] and ``seeds`` int32 walk positions."""
+
+    keys: torch.Tensor
+    slots: torch.Tensor
+    trans: torch.Tensor
+    allowed: torch.Tensor
+    seed_off: torch.Tensor
+    seeds: torch.Tensor
 
     @property
     def num_lists(self) -> int:
         return int(self.keys.shape[0])
+
+    def host(self) -> dict:
+        """numpy copies of the arrays (slots and allowed as uint32)."""
+        h = self.__dict__.get("_host")
+        if h is None:
+            h = {n: getattr(self, n).cpu().numpy() for n in ("keys", "slots", "trans", "allowed", "seed_off", "seeds")}
+            h["slots"] = h["slots"].view(np.uint32)
+            h["allowed"] = h["allowed"].view(np.uint32)
+            self.__dict__["_host"] = h
+        return h
 
 
 # ------------------------------------------------------------------ hash --
@@ -79,171 +98,96 @@ def list_hash(lst) -> int:
     return _mix32(h & 0xFFFFFFFF)
 
 
-# ------------------------------------------------------------- the steps --
-class _Tables:
-    def __init__(self, g) -> None:
-        c = lambda t: t.cpu().numpy()  # noqa: E731
-        self.accept = c(g.accept).astype(bool)
-        self.live = c(g.live).astype(bool)
-        off = c(g.edge_offsets).astype(np.int64)
-        kind, lo, hi = c(g.edge_kind), c(g.edge_lo), c(g.edge_hi)
-        dst, callee = c(g.edge_dst), c(g.edge_callee)
-        n = len(self.accept)
-        # per state: byte edges (lo, hi, dst) and closure edges (kind, dst, callee), in edge order
-        self.byte = [[(int(lo[e]), int(hi[e]), int(dst[e])) for e in range(off[s], off[s + 1])
-                      if kind[e] == _BYTE] for s in range(n)]
-        self.clos = [[(int(kind[e]), int(dst[e]), int(callee[e])) for e in range(off[s], off[s + 1])
-                      if kind[e] != _BYTE] for s in range(n)]
+# ------------------------------------------------------------ the build --
+def _np_ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
 
 
-def _add(nxt: list, x: tuple) -> bool:
-    """Append x unless present; False when the list is full (x dropped)."""
-    if x in nxt:
-        return True
-    if len(nxt) >= _CAP:
-        return False
-    nxt.append(x)
-    return True
-
-
-def _close(t: _Tables, nxt: list, sat: bool, lmax: int):
-    """Closure and compaction of a suffix list (close() and prune_dead() of
-    pda_core.hpp over the suffixes), and whether a config was dropped at the
-    cap; BOUNDARY when a config pops into the common stack or pushes beyond
-    ``lmax`` frames, DEAD when no config is left."""
-    i = 0
-    while i < len(nxt):
-        sfx = nxt[i]
-        top = sfx[-1]
-        if t.accept[top]:
-            if len(sfx) == 1:
-                return _BOUNDARY, sat
-            sat = not _add(nxt, sfx[:-1]) or sat
-        for kind, dst, callee in t.clos[top]:
-            if kind == _EPS:
-                sat = not _add(nxt, sfx[:-1] + (dst,)) or sat
-            else:
-                if len(sfx) + 1 > lmax:
-                    return _BOUNDARY, sat
-                sat = not _add(nxt, sfx[:-1] + (dst, callee)) or sat
-        i += 1
-    out = tuple(s for s in nxt if t.live[s[-1]])
-    return (out if out else _DEAD), sat
-
-
-def _step(t: _Tables, lst: tuple, byte: int, lmax: int):
-    nxt: list = []
-    sat = False
-    for sfx in lst:
-        for lo, hi, dst in t.byte[sfx[-1]]:
-            if lo <= byte <= hi:
-                sat = not _add(nxt, sfx[:-1] + (dst,)) or sat
-    return _close(t, nxt, sat, lmax)
-
-
-def _enumerate(t: _Tables, lmax: int, limit: int) -> tuple[list, np.ndarray]:
-    """Lists reachable from the closure of every single state (breadth
-    first, at most ``limit``) and their byte transitions."""
-    lists: list = []
-    index: dict = {}
-    for s in range(len(t.accept)):
-        r, _ = _close(t, [(s,)], False, lmax)
-        if isinstance(r, tuple) and r not in index and len(lists) < limit:
-            index[r] = len(lists)
-            lists.append(r)
-    rows = []
-    head = 0
-    while head < len(lists):
-        row = []
-        memo: dict = {}
-        lst = lists[head]
-        for byte in range(256):
-            # bytes over the same byte edges step alike
-            sig = tuple(lo <= byte <= hi for sfx in lst for lo, hi, _ in t.byte[sfx[-1]])
-            if sig in memo:
-                row.append(memo[sig])
-                continue
-            nx, sat = _step(t, lst, byte, lmax)
-            if isinstance(nx, tuple):
-                if nx not in index:
-                    if len(lists) >= limit:
-                        memo[sig] = _BOUNDARY
-                        row.append(_BOUNDARY)
-                        continue
-                    index[nx] = len(lists)
-                    lists.append(nx)
-                code = index[nx] | (SAT if sat else 0)
-            else:
-                code = nx
-            memo[sig] = code
-            row.append(code)
-        rows.append(row)
-        head += 1
-    return lists, np.array(rows, dtype=np.int32).reshape(len(lists), 256)
-
-
-def _classify(codes: np.ndarray, g, order: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """Inside-token bitmaps, seed offsets and seeds of every list, from the
-    native classifier (every token walked from every list)."""
-    import ctypes as C
-    import os
-
-    from .. import _lib
-
-    L, V = codes.shape[0], g.vocab_size
+def _classify_host(trans: np.ndarray, g, order: np.ndarray):
+    """Inside-token bitmaps, seed offsets and seeds from the native host
+    classifier (every token walked from every list, 16 threads at most)."""
+    L, V = trans.shape[0], g.vocab_size
     off = np.ascontiguousarray(g.tok_offsets.cpu().numpy().astype(np.int32))
     tb = np.ascontiguousarray(g.tok_bytes.cpu().numpy().astype(np.uint8))
     if tb.size == 0:
         tb = np.zeros(1, np.uint8)
     order = np.ascontiguousarray(order.astype(np.int32))
-    codes = np.ascontiguousarray(codes.astype(np.int32))
     allowed = np.zeros((L, (V + 31) // 32), dtype=np.uint32)
     count = np.zeros(L, dtype=np.int32)
     threads = min(16, os.cpu_count() or 1)
-    p = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
     lib = _lib.lib()
-    _lib.check(lib.bpd_host_frame_classify(p(codes), L, p(off), p(tb), V, g.eos_id, p(order), p(allowed),
-                                           p(count), None, None, threads))
+    _lib.check(lib.bpd_host_frame_classify(_np_ptr(trans), L, _np_ptr(off), _np_ptr(tb), V, g.eos_id, _np_ptr(order),
+                                           _np_ptr(allowed), _np_ptr(count), None, None, threads))
     seed_off = np.zeros(L + 1, dtype=np.int32)
     np.cumsum(count, out=seed_off[1:])
     seeds = np.zeros(max(int(seed_off[-1]), 1), dtype=np.int32)
-    _lib.check(lib.bpd_host_frame_classify(p(codes), L, p(off), p(tb), V, g.eos_id, p(order), p(allowed),
-                                           p(count), p(seed_off), p(seeds), threads))
-    return allowed, seed_off, seeds[:int(seed_off[-1])]
+    _lib.check(lib.bpd_host_frame_classify(_np_ptr(trans), L, _np_ptr(off), _np_ptr(tb), V, g.eos_id, _np_ptr(order),
+                                           _np_ptr(allowed), _np_ptr(count), _np_ptr(seed_off), _np_ptr(seeds),
+                                           threads))
+    t = torch.from_numpy
+    return t(allowed.view(np.int32)), t(seed_off), t(seeds[:int(seed_off[-1])])
 
 
-def frame_lists(g, order: np.ndarray, limit: int = MAX_LISTS) -> FrameLists | None:
+def _classify_device(trans: torch.Tensor, g, order: torch.Tensor):
+    """The same on the tables' device: a counting pass (bitmaps and seeds
+    per block of walk positions), prefix sums, a filling pass."""
+    dev = g.device
+    L, V = int(trans.shape[0]), g.vocab_size
+    lib = _lib.lib()
+    blocks = int(lib.bpd_frame_classify_blocks(V))
+    off = g.tok_offsets.to(dev, torch.int32).contiguous()
+    tb = g.tok_bytes.contiguous()
+    if tb.numel() == 0:
+        tb = torch.zeros(1, dtype=torch.uint8, device=dev)
+    order = order.to(dev, torch.int32).contiguous()
+    allowed = torch.zeros((L, (V + 31) // 32), dtype=torch.int32, device=dev)
+    counts = torch.empty((L, blocks), dtype=torch.int32, device=dev)
+    stream = _lib.stream_of(dev)
+    p = _lib.ptr
+    _lib.check(lib.bpd_frame_classify(p(trans), L, p(off), p(tb), V, g.eos_id, p(order), p(allowed), p(counts),
+                                      None, None, stream))
+    flat = counts.view(-1).to(torch.int64)
+    offsets = torch.cumsum(flat, 0) - flat
+    total = int(flat.sum().item())
+    seeds = torch.empty(max(total, 1), dtype=torch.int32, device=dev)
+    _lib.check(lib.bpd_frame_classify(p(trans), L, p(off), p(tb), V, g.eos_id, p(order), p(allowed), p(counts),
+                                      p(offsets), p(seeds), stream))
+    seed_off = torch.empty(L + 1, dtype=torch.int32, device=dev)
+    seed_off[:L] = offsets.view(L, blocks)[:, 0].to(torch.int32)
+    seed_off[L] = total
+    return allowed, seed_off, seeds[:total]
+
+
+def frame_lists(g, order, limit: int = MAX_LISTS) -> FrameLists | None:
     """Keys, hash table, transitions, inside-token bitmaps and boundary seeds
     (walk positions of ``order``) of the stack-relative lists of ``g`` (a
-    :class:`~bpdecode_amd.grammar.device.PdaTensors`)."""
+    :class:`~bpdecode_amd.grammar.device.PdaTensors`), on its device: the
+    lists are enumerated on the host, the tokens classified where the tables
+    are."""
     if g.num_states == 0 or g.vocab_size == 0:
         return None
-    t = _Tables(g)
-    lists, codes = _enumerate(t, MAX_SUFFIX, min(limit, MAX_LISTS))
-    if not lists:
+    host = g if g.device.type == "cpu" else g.to("cpu")
+    limit = min(limit, MAX_LISTS)
+    keys = np.zeros((limit, KEY_WORDS), dtype=np.int32)
+    trans = np.zeros((limit, 256), dtype=np.int32)
+    slots = np.zeros(SLOTS, dtype=np.uint32)
+    L = int(_lib.lib().bpd_host_frame_lists(C.byref(host.c_table()), limit, _np_ptr(keys), _np_ptr(trans),
+                                            _np_ptr(slots)))
+    if L < 0:
+        _lib.check(L)
+    if L == 0:
         return None
-    L = len(lists)
-    allowed, seed_off, seeds = _classify(codes, g, order)
-    keys = np.zeros((L, KEY_WORDS), dtype=np.int32)
-    slots = np.full(SLOTS, EMPTY, dtype=np.uint32)
-    for i, lst in enumerate(lists):
-        keys[i, 0] = len(lst)
-        for c, sfx in enumerate(lst):
-            keys[i, 1 + c] = len(sfx)
-            keys[i, 9 + c * MAX_SUFFIX:9 + c * MAX_SUFFIX + len(sfx)] = sfx
-        h = list_hash(lst)
-        s = h & (SLOTS - 1)
-        while slots[s] != EMPTY:
-            s = (s + 1) & (SLOTS - 1)
-        slots[s] = np.uint32(i | (((h >> 10) & 0xFFFFF) << 12))
-    return FrameLists(
-        keys=keys,
-        slots=slots,
-        trans=np.ascontiguousarray(codes),
-        allowed=allowed,
-        seed_off=seed_off,
-        seeds=seeds,
-    )
+    keys, trans = np.ascontiguousarray(keys[:L]), np.ascontiguousarray(trans[:L])
+    order_t = torch.as_tensor(order)
+    if g.device.type == "cpu":
+        allowed, seed_off, seeds = _classify_host(trans, g, order_t.numpy())
+        dev_t = torch.from_numpy
+    else:
+        trans_d = torch.from_numpy(trans).to(g.device)
+        allowed, seed_off, seeds = _classify_device(trans_d, g, order_t)
+        dev_t = lambda a: torch.from_numpy(a).to(g.device)  # noqa: E731
+    return FrameLists(keys=dev_t(keys), slots=dev_t(slots.view(np.int32)), trans=dev_t(trans),
+                      allowed=allowed, seed_off=seed_off, seeds=seeds)
 
 
 def frame_match(cfg: np.ndarray, fl: FrameLists) -> tuple[int, int]:
@@ -253,6 +197,7 @@ def frame_match(cfg: np.ndarray, fl: FrameLists) -> tuple[int, int]:
     ``MAX_SUFFIX - 1`` frames shorter, shortest first (longest suffixes),
     each with every suffix at most ``MAX_SUFFIX`` frames and the stack plus
     ``MAX_SUFFIX`` frames within the depth limit."""
+    h = fl.host()
     n = int(cfg[0])
     if n < 1 or n > _CAP:
         return -1, -1
@@ -268,12 +213,12 @@ def frame_match(cfg: np.ndarray, fl: FrameLists) -> tuple[int, int]:
         if b + MAX_SUFFIX > _MAXD or max(depth) - b > MAX_SUFFIX:
             continue
         lst = tuple(tuple(int(x) for x in frames[i, b:depth[i]]) for i in range(n))
-        h = list_hash(lst)
-        s = h & (SLOTS - 1)
-        while fl.slots[s] != EMPTY:
-            e = int(fl.slots[s])
-            if (e >> 12) == ((h >> 10) & 0xFFFFF):
-                key = fl.keys[e & 0xFFF]
+        hv = list_hash(lst)
+        s = hv & (SLOTS - 1)
+        while h["slots"][s] != EMPTY:
+            e = int(h["slots"][s])
+            if (e >> 12) == ((hv >> 10) & 0xFFFFF):
+                key = h["keys"][e & 0xFFF]
                 if int(key[0]) == n and all(
                         int(key[1 + i]) == len(lst[i]) and
                         list(key[9 + i * MAX_SUFFIX:9 + i * MAX_SUFFIX + len(lst[i])]) == list(lst[i])

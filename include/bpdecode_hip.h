@@ -312,6 +312,29 @@ int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out);
  * through pda_advance_byte directly, test_pda.cpp:46-51). */
 int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data, int64_t n);
 
+/* bpd_host_frame_lists: host only (no counterpart in the reference: it
+ * builds the frame lists of BpdPdaFrames).  Enumerates the stack-relative
+ * config lists of the tables breadth first from the closure of every single
+ * state (at most max_lists <= BPD_PDA_MAX_FRAME_LISTS) and writes their keys
+ * [max_lists, BPD_PDA_FRAME_KEY_WORDS], byte transitions [max_lists, 256]
+ * and the keys' slot table [BPD_PDA_FRAME_SLOTS]; returns the number of
+ * lists, or a negative error code. */
+int bpd_host_frame_lists(const BpdPdaTable* g, int32_t max_lists, int32_t* keys, int32_t* trans,
+                         uint32_t* slots);
+
+/* bpd_frame_classify: bpd_host_frame_classify on the device, in two passes
+ * on `stream` (device pointers).  Count pass (block_offsets NULL): `allowed`
+ * (zeroed by the caller) gets the inside tokens and block_counts
+ * [num_lists, bpd_frame_classify_blocks(vocab_size)] the seeds of each
+ * list's block of walk positions.  Fill pass: with block_offsets the
+ * exclusive prefix sums of those counts in the same order (int64), seeds
+ * gets each list's seeds in walk order at its offsets. */
+int bpd_frame_classify(const int32_t* trans, int32_t num_lists, const int32_t* tok_offsets,
+                       const uint8_t* tok_bytes, int32_t vocab_size, int32_t eos_id, const int32_t* order,
+                       uint32_t* allowed, int32_t* block_counts, const int64_t* block_offsets,
+                       int32_t* seeds, void* stream);
+int32_t bpd_frame_classify_blocks(int32_t vocab_size);
+
 /* bpd_host_frame_classify: host only (no counterpart in the reference: it
  * builds the frame lists' bitmaps and seeds, BpdPdaFrames).  Walks every
  * token from every list through trans [num_lists, 256] on up to `threads`

@@ -92,6 +92,38 @@ def _json_configs(g, n, seed):
     return torch.stack(rows)
 
 
+def _frame_build_equal(g, dev):
+    from bpdecode_amd.grammar.device import _walk_order
+    from bpdecode_amd.grammar.frames import frame_lists
+
+    order, _ = _walk_order(g.tok_offsets, g.tok_bytes, g.vocab_size, g.eos_id)
+    host = frame_lists(g, order)
+    on_dev = frame_lists(g.to(dev), order)
+    assert (host is None) == (on_dev is None)
+    if host is None:
+        return 0
+    assert on_dev.allowed.device.type == dev.type
+    for n in ("keys", "slots", "trans", "allowed", "seed_off", "seeds"):
+        assert torch.equal(getattr(host, n), getattr(on_dev, n).cpu()), n
+    return host.num_lists
+
+
+def test_frame_lists_device_build_equals_host(dev, json_case):
+    """The frame lists' token classification on the device (count pass,
+    prefix sums, fill pass) gives the host classifier's bitmaps, seed
+    offsets and seeds word for word: recursive JSON at V=151,936 (700
+    lists), its unreduced tables, and the toy grammars."""
+    vocab, g, _ = json_case
+    _log("case frame lists json V=151936 reduced")
+    assert _frame_build_equal(g, dev) == 700
+    _log("case frame lists json V=151936 unreduced")
+    comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
+    assert _frame_build_equal(build_pda_tensors(comp, vocab, eps_reduce=False), dev) > 0
+    for idx, src in enumerate(GRAMMARS):
+        _log(f"case frame lists toy grammar {idx}")
+        _frame_build_equal(build_pda_tensors(CompiledGrammar.build(parse_gbnf(src)), VOCAB), dev)
+
+
 def test_json_full_vocab_masks_and_commits(dev, json_case):
     vocab, g, t = json_case
     _log("case json V=151936 B=12 mask+commit 4 steps")

@@ -338,14 +338,15 @@ def _meaningful(cfg: np.ndarray) -> list:
 
 
 def _check_list(t, fl, order_np, cfg, l, base, vsize, what):
+    fl = fl.host()
     """A set over list l at common-stack depth `base`: every token outside the
     list's seeds gets the oracle's verdict from the bitmap, and the oracle's
     step by each byte reaches the coded list over the same stack (saturation
     flag included) or empties the set."""
     want = np.unpackbits(OP.compute_mask(t, cfg[None].copy())[0].view(np.uint8), bitorder="little")
-    have = np.unpackbits(fl.allowed[l].view(np.uint8), bitorder="little")
+    have = np.unpackbits(fl["allowed"][l].view(np.uint8), bitorder="little")
     seeded = np.zeros(want.size, dtype=bool)
-    seeded[order_np[fl.seeds[fl.seed_off[l]:fl.seed_off[l + 1]]]] = True
+    seeded[order_np[fl["seeds"][fl["seed_off"][l]:fl["seed_off"][l + 1]]]] = True
     V = vsize
     assert not (have[:V].astype(bool) & seeded[:V]).any(), what
     off = ~seeded[:V]
@@ -353,7 +354,7 @@ def _check_list(t, fl, order_np, cfg, l, base, vsize, what):
     assert not have[V:].any()
     stack = cfg[10:10 + base].copy()
     for byte in range(256):
-        code = int(fl.trans[l, byte])
+        code = int(fl["trans"][l, byte])
         nxt = cfg.copy()
         ok = OP.advance_byte(t, nxt, byte)
         if code == -1:
@@ -361,7 +362,7 @@ def _check_list(t, fl, order_np, cfg, l, base, vsize, what):
         elif code >= 0:
             assert ok, (what, byte)
             sat = int(cfg[1]) | (1 if code & 0x10000 else 0)
-            exp = _compose(fl.keys[code & 0xFFFF], stack, sat)
+            exp = _compose(fl["keys"][code & 0xFFFF], stack, sat)
             assert _meaningful(nxt) == _meaningful(exp), (what, byte)
 
 
@@ -416,7 +417,7 @@ number ::= "-"? [0-9]+ ( "." [0-9]+ )?
             _check_list(t, fl, order_np, cfg, l, base, vocab.size, p)
         for l in range(fl.num_lists):
             for stack in (np.zeros(0, np.int32), np.array([0, 1, 2], np.int32) % g.num_states):
-                cfg = _compose(fl.keys[l], stack, 0)
+                cfg = _compose(fl.host()["keys"][l], stack, 0)
                 assert frame_match(cfg, fl)[0] >= 0, l
                 _check_list(t, fl, order_np, cfg, l, stack.size, vocab.size, (l, stack.size))
         assert hits >= need, (src[:20], reduce, hits)
