@@ -201,16 +201,33 @@ struct MemoWs {
                       // (ids flagged kTExact where the step's raw words are the set's)
   uint4* recs;        // [vocab] first 16 bytes of the token at walk position k, zero padded
   int2* tmeta;        // [vocab] (token id, length) of the token at walk position k
-  uint2* queue;       // [rows, 2, vocab] paused tokens of the row-wide walk (two buffers)
+  uint2* queue;       // [rows, 2, qcap] paused tokens of the row-wide walk (two buffers)
+  int32_t qcap;       // entries per queue buffer (queue_cap)
 };
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Entries of each of a row's two queue buffers: the whole vocab up to 4096
+// tokens, a quarter of it above (a row that pauses more tokens in one pass
+// starts again in tile mode).  The bench rows pause at most 2,692 of 151,936
+// tokens in their first pass.
+int32_t queue_cap(int64_t vocab) {
+  const int64_t v = vocab > 0 ? vocab : 0;
+  int64_t cap = v <= 4096 ? v : (v + 3) / 4;
+  // BPD_PDA_QUEUE_CAP lowers it (tests of the full-queue path; read by the
+  // workspace size and the launch alike)
+  if (const char* e = std::getenv("BPD_PDA_QUEUE_CAP")) {
+    const long q = std::atol(e);
+    if (q > 0 && q < cap) cap = q;
+  }
+  return int32_t(cap);
+}
 
 size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
   return 256 + sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
-         v * sizeof(int2) + r * 2 * v * sizeof(uint2);
+         v * sizeof(int2) + r * 2 * size_t(queue_cap(vocab)) * sizeof(uint2);
 }
 
 MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
@@ -230,6 +247,7 @@ MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   w.tmeta = reinterpret_cast<int2*>(p);
   p += size_t(vocab) * sizeof(int2);
   w.queue = reinterpret_cast<uint2*>(p);
+  w.qcap = queue_cap(vocab);
   return w;
 }
 
@@ -1199,12 +1217,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   // each round then resolves all of the row's requests at once and walks the
   // queue again into the other buffer.  A row needs as many rounds as its
   // longest chain of new sets (7 on recursive JSON) rather than that many per
-  // tile.  A row whose sets overflow the pool, or that pauses a token of
-  // 65536 bytes or more, starts again in tile mode.
+  // tile.  A row whose sets overflow the pool, that pauses a token of 65536
+  // bytes or more, or that pauses more tokens in one pass than a queue
+  // buffer holds, starts again in tile mode.
   bool tiles = row_mode == 0;
   if (!tiles) {
-    uint2* qin = ws.queue + b * 2 * V;
-    uint2* qout = qin + V;
+    const int64_t Q = ws.qcap;
+    uint2* qin = ws.queue + b * 2 * Q;
+    uint2* qout = qin + Q;
     const int lane = tid & (kWave - 1);
     // queue entry e for the lanes with p set (every lane of the wave calls it)
     auto enqueue = [&](bool p, uint2 e, uint2* q) {
@@ -1216,7 +1236,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       base = __shfl(base, leader);
       if (p) {
         const int idx = base + __popcll(m & ((uint64_t(1) << lane) - 1u));
-        if (idx < V) q[idx] = e;
+        if (idx < Q)
+          q[idx] = e;
+        else
+          row_fail = 1;  // the buffer is full: the row starts again in tile mode
       }
     };
     // one step of a token from set cur by `byte`: false when the entry is

@@ -198,6 +198,37 @@ def test_json_memo_overflow_rows_match_oracle(dev, json_case, monkeypatch, limit
     assert np.array_equal(got.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("cap", ["16", "512"])
+def test_json_full_queue_rows_match_oracle(dev, json_case, monkeypatch, cap):
+    """With the queue buffers lowered to a few entries, rows that pause more
+    tokens in one pass start again in tile mode; masks and commits stay the
+    oracle's (the workspace is sized for the lowered buffers)."""
+    vocab, g, t = json_case
+    _log(f"case json V=151936 B=8 queue cap {cap}")
+    monkeypatch.setenv("BPD_PDA_QUEUE_CAP", cap)
+    cfgs = _json_configs(g, 8, seed=23)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    lg = synth.logits(8, vocab.size, 3.0, torch.float32, seed=6)
+    got = lg.to(dev)
+    pda_mask_(got, gd, pool)
+    ref = lg.numpy().copy()
+    OP.apply_mask(t, cfgs.numpy().copy(), ref)
+    assert np.array_equal(got.cpu().numpy(), ref)
+    cb = CFGConstraintBatch(gd, capacity=8, device=dev)
+    for i in range(8):
+        cb.add(i)
+    cb._configs.copy_(pool)
+    x = synth.logits(8, vocab.size, 3.0, torch.float32, seed=7).to(dev)
+    cb.apply_mask(list(range(8)), x)
+    toks = torch.argmax(x, dim=1).to(torch.int32)
+    cb.commit(list(range(8)), toks)
+    want = cfgs.numpy().copy()
+    ok = OP.advance(t, want, toks.cpu().numpy())
+    assert ok.all()
+    assert np.array_equal(cb._configs.cpu().numpy(), want)
+
+
 def test_json_row_walk_equals_tile_walk(dev, json_case, monkeypatch):
     """The row-wide walk (default) and the tile-by-tile walk of the memoised
     kernel give the oracle's bits on 48 rows (string, number, after-value and
