@@ -871,6 +871,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
   __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail, loop_n, row_list;
+  __shared__ int n_stepped, n_cheap;
   __shared__ uint32_t h0_sh;
   __shared__ uint8_t loop0[256];  // T[0][c] == 0: byte c keeps set 0 (row-wide walk)
   // first pass of the row-wide walk: pass index i -> walk position
@@ -967,6 +968,29 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     __syncthreads();
     const int n = nreq < kMemoReq ? nreq : kMemoReq;
+    {
+      // the requests a wave steps (no frame-list composition) first: waves
+      // take requests r = wave, wave + 16, ..., so each wave gets at most
+      // one more of them than another
+      uint32_t entry = 0u;
+      bool cheap = true;
+      if (tid < n) {
+        entry = uint32_t(req_list[tid]);
+        const int sl = set_list[entry >> 8];
+        cheap = sl >= 0 && a.frames.trans[(sl & (BPD_PDA_FRAME_SAT - 1)) * 256 + int(entry & 255u)] != -2;
+      }
+      if (tid == 0) {
+        n_stepped = 0;
+        n_cheap = 0;
+      }
+      __syncthreads();
+      int slot = 0;
+      if (tid < n && !cheap) slot = atomicAdd(&n_stepped, 1);
+      __syncthreads();
+      if (tid < n && cheap) slot = n_stepped + atomicAdd(&n_cheap, 1);
+      if (tid < n) req_list[slot] = int32_t(entry);
+      __syncthreads();
+    }
     if (tid < n) {
       // every byte of the request's elementary interval [lo, hi] shares
       // its result: the first request of an interval computes it and
