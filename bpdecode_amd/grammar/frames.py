@@ -35,10 +35,10 @@ import torch
 
 from .. import _lib
 
-MAX_SUFFIX = 4  # frames of a suffix (BPD_PDA_FRAME_SUFFIX)
-SLOTS = 1024  # hash-table slots (staged in LDS by the mask kernel)
-MAX_LISTS = 700  # at most 0.7 * SLOTS keys
-KEY_WORDS = 48  # n, 8 suffix lengths, 8 x MAX_SUFFIX frames, padding
+MAX_SUFFIX = 5  # frames of a suffix (BPD_PDA_FRAME_SUFFIX)
+SLOTS = 2048  # hash-table slots (staged in LDS by the mask kernel)
+MAX_LISTS = 1400  # at most 0.7 * SLOTS keys
+KEY_WORDS = 56  # n, 8 suffix lengths, 8 x MAX_SUFFIX frames, padding
 SAT = 0x10000  # transition flag: the step dropped a config at the 8-config cap
 EMPTY = 0xFFFFFFFF
 _CAP = 8  # configs per set

@@ -256,10 +256,10 @@ typedef struct BpdPdaTable {
  * up to BPD_PDA_FRAME_SUFFIX - 1 frames less.  Built by grammar/frames.py
  * for the default walk order: the device trusts the contents (seed_off
  * non-decreasing within the seeds array; wrong lists give wrong verdicts). */
-#define BPD_PDA_MAX_FRAME_LISTS 700
-#define BPD_PDA_FRAME_SLOTS 1024
-#define BPD_PDA_FRAME_SUFFIX 4
-#define BPD_PDA_FRAME_KEY_WORDS 48
+#define BPD_PDA_MAX_FRAME_LISTS 1400
+#define BPD_PDA_FRAME_SLOTS 2048
+#define BPD_PDA_FRAME_SUFFIX 5
+#define BPD_PDA_FRAME_KEY_WORDS 56
 #define BPD_PDA_FRAME_SAT 0x10000
 #define BPD_PDA_FRAME_EMPTY 0xFFFFFFFFu
 typedef struct BpdPdaFrames {

@@ -111,11 +111,13 @@ def _frame_build_equal(g, dev):
 def test_frame_lists_device_build_equals_host(dev, json_case):
     """The frame lists' token classification on the device (count pass,
     prefix sums, fill pass) gives the host classifier's bitmaps, seed
-    offsets and seeds word for word: recursive JSON at V=151,936 (700
-    lists), its unreduced tables, and the toy grammars."""
+    offsets and seeds word for word: recursive JSON at V=151,936 (as many
+    lists as the cap allows), its unreduced tables, and the toy grammars."""
     vocab, g, _ = json_case
     _log("case frame lists json V=151936 reduced")
-    assert _frame_build_equal(g, dev) == 700
+    from bpdecode_amd.grammar.frames import MAX_LISTS
+
+    assert _frame_build_equal(g, dev) == MAX_LISTS
     _log("case frame lists json V=151936 unreduced")
     comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
     assert _frame_build_equal(build_pda_tensors(comp, vocab, eps_reduce=False), dev) > 0
