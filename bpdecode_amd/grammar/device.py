@@ -37,8 +37,13 @@ PDA_CONFIG_FLAT = PDA_CONFIG_WORDS
 _EPS, _BYTE, _CALL = 0, 1, 2
 
 
+_WALK_ORDERS: dict = {}  # walk orders by the content of the token tables (a few vocabularies)
+
+
 def _walk_order(off: torch.Tensor, tb: torch.Tensor, vocab: int, eos_id: int):
-    """Walk order of the memoised device mask and its first-byte runs.
+    """Walk order of the memoised device mask and its first-byte runs (kept
+    for the token tables' content: every grammar over one vocabulary shares
+    them).
 
     Tokens are ordered by first byte, then byte length, then their next 15
     bytes; EOS and empty tokens come last (group 256).  Consecutive lanes of
@@ -47,8 +52,17 @@ def _walk_order(off: torch.Tensor, tb: torch.Tensor, vocab: int, eos_id: int):
     together.  ``runs[c]`` is the first position of group ``c`` (257
     entries; group 256 ends at ``vocab``), so a row skips at once every
     group whose first byte empties its config-set."""
-    o = off.cpu().numpy().astype(np.int64)
+    o32 = off.cpu().numpy()
     b = tb.cpu().numpy()
+    h = hashlib.blake2b(digest_size=16)
+    h.update(np.int64([vocab, eos_id]).tobytes())
+    h.update(np.ascontiguousarray(o32[: vocab + 1]).tobytes())
+    h.update(np.ascontiguousarray(b).tobytes())
+    key = h.digest()
+    hit = _WALK_ORDERS.get(key)
+    if hit is not None:
+        return hit[0].clone(), hit[1].clone()
+    o = o32.astype(np.int64)
     start, length = o[:vocab], o[1 : vocab + 1] - o[:vocab]
     lead = b[np.minimum(start, max(b.size - 1, 0))].astype(np.int64) if b.size else np.zeros(vocab, np.int64)
     group = np.where(length > 0, lead, 256).astype(np.int64)
@@ -62,7 +76,10 @@ def _walk_order(off: torch.Tensor, tb: torch.Tensor, vocab: int, eos_id: int):
     keys.append(group)  # primary key last
     order = np.lexsort(keys).astype(np.int32)
     runs = np.searchsorted(group[order], np.arange(257), side="left").astype(np.int32)
-    return torch.from_numpy(order), torch.from_numpy(runs)
+    if len(_WALK_ORDERS) >= 8:
+        _WALK_ORDERS.pop(next(iter(_WALK_ORDERS)))
+    _WALK_ORDERS[key] = (torch.from_numpy(order), torch.from_numpy(runs))
+    return torch.from_numpy(order.copy()), torch.from_numpy(runs.copy())
 
 
 @dataclass
