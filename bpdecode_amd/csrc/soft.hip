@@ -416,7 +416,7 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Launch geometry of one call.
 constexpr int kWideLoads = 8;                                   // float4 groups per thread (wave-shift stats)
-constexpr int64_t kWideChunk = kPriorThreads * 4 * kWideLoads;  // 16384 tokens per block
+constexpr int64_t kWideChunk = kPriorThreads * 4 * kWideLoads;  // 8192 tokens per block
 
 struct PriorPlan {
   bool class_stats;  // class-atomic stats (else pieces)
@@ -1001,9 +1001,12 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_pieces_kernel(
 constexpr int kRoundThreads = 1024;
 constexpr int kPairRegs = 8;     // pairs per thread held in registers while they load
 
-// DPP quad permutations: lane i reads lane i ^ 1, lane i ^ 2 of its quad
+// DPP quad permutations: lane i reads lane i ^ 1, lane i ^ 2 of its quad;
+// row_half_mirror: lane i of each aligned group of eight reads lane 7 - i
+// (a lane of the other quad: after a quad reduction, that quad's result)
 constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
 constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
 
 template <int Ctrl>
 __device__ inline float quad_read(float x) {
@@ -1026,12 +1029,12 @@ __device__ inline void quad_lse_step(float& m, float& s) {
 __device__ inline float group8_max(float x) {
   x = fmaxf(x, quad_read<kDppQuadXor1>(x));
   x = fmaxf(x, quad_read<kDppQuadXor2>(x));
-  return fmaxf(x, __shfl_xor(x, 4));
+  return fmaxf(x, quad_read<kDppHalfMirror>(x));
 }
 __device__ inline float group8_sum(float x) {
   x += quad_read<kDppQuadXor1>(x);
   x += quad_read<kDppQuadXor2>(x);
-  return x + __shfl_xor(x, 4);
+  return x + quad_read<kDppHalfMirror>(x);
 }
 
 template <bool PairsInLds>
@@ -1084,7 +1087,7 @@ __device__ __forceinline__ void prior_rounds_tail(float* lc, float* z0, float* z
     quad_lse_step<kDppQuadXor2>(m, sm);
     {
       // the two quads of the state
-      const float mo = __shfl_xor(m, 4), so4 = __shfl_xor(sm, 4);
+      const float mo = quad_read<kDppHalfMirror>(m), so4 = quad_read<kDppHalfMirror>(sm);
       const float nm = fmaxf(m, mo);
       if (nm != -INFINITY) sm = sm * exp_shift(m, nm) + so4 * exp_shift(mo, nm);
       m = nm;
@@ -1121,8 +1124,16 @@ __device__ __forceinline__ void prior_rounds_tail(float* lc, float* z0, float* z
       for (int u = 1; u < kRegPairs; ++u) m = fmaxf(m, v[u]);
       float sm = 0.0f;
       if (m != -INFINITY) {
+        // pairwise: four dependent adds instead of sixteen
+        float e[kRegPairs];
 #pragma unroll
-        for (int u = 0; u < kRegPairs; ++u) sm += exp_shift(v[u], m);
+        for (int u = 0; u < kRegPairs; ++u) e[u] = exp_shift(v[u], m);
+#pragma unroll
+        for (int w = kRegPairs / 2; w > 0; w /= 2) {
+#pragma unroll
+          for (int u = 0; u < w; ++u) e[u] += e[u + w];
+        }
+        sm = e[0];
       }
       for (int32_t i = i_rest + gl; i < i1; i += kLanes) {
         const uint32_t p = prior_pair<PairsInLds>(pr, cls, i);
