@@ -198,8 +198,12 @@ __global__ __launch_bounds__(kClassifyThreads) void frame_classify_kernel(
 
 using namespace bpd;
 
-extern "C" int bpd_host_frame_lists(const BpdPdaTable* g, int32_t max_lists, int32_t* keys, int32_t* trans,
-                                    uint32_t* slots) {
+namespace {
+
+// The enumeration behind bpd_host_frame_lists: 0 or an error code, the
+// number of lists in *count.
+int frame_lists_impl(const BpdPdaTable* g, int32_t max_lists, int32_t* keys, int32_t* trans, uint32_t* slots,
+                     int32_t* count) {
   BPD_REQUIRE(g && keys && trans && slots, "null pointer argument");
   BPD_REQUIRE(max_lists >= 0 && max_lists <= BPD_PDA_MAX_FRAME_LISTS, "max_lists %d outside [0, %d]", max_lists,
               BPD_PDA_MAX_FRAME_LISTS);
@@ -274,7 +278,17 @@ extern "C" int bpd_host_frame_lists(const BpdPdaTable* g, int32_t max_lists, int
     slots[s] = uint32_t(i) | (((h >> 10) & 0xFFFFFu) << 12);
   }
   std::copy(rows.begin(), rows.end(), trans);
-  return L;
+  *count = L;
+  return BPD_OK;
+}
+
+}  // namespace
+
+extern "C" int bpd_host_frame_lists(const BpdPdaTable* g, int32_t max_lists, int32_t* keys, int32_t* trans,
+                                    uint32_t* slots) {
+  int32_t count = 0;
+  const int rc = frame_lists_impl(g, max_lists, keys, trans, slots, &count);
+  return rc != BPD_OK ? -rc : count;
 }
 
 extern "C" int bpd_frame_classify(const int32_t* trans, int32_t num_lists, const int32_t* tok_offsets,

@@ -174,7 +174,7 @@ def frame_lists(g, order, limit: int = MAX_LISTS) -> FrameLists | None:
     L = int(_lib.lib().bpd_host_frame_lists(C.byref(host.c_table()), limit, _np_ptr(keys), _np_ptr(trans),
                                             _np_ptr(slots)))
     if L < 0:
-        _lib.check(L)
+        _lib.check(-L)
     if L == 0:
         return None
     keys, trans = np.ascontiguousarray(keys[:L]), np.ascontiguousarray(trans[:L])

@@ -421,3 +421,33 @@ number ::= "-"? [0-9]+ ( "." [0-9]+ )?
                 assert frame_match(cfg, fl)[0] >= 0, l
                 _check_list(t, fl, order_np, cfg, l, stack.size, vocab.size, (l, stack.size))
         assert hits >= need, (src[:20], reduce, hits)
+
+
+def test_frame_lists_reject_bad_tables():
+    """The enumeration's argument checks come back as errors (a negative
+    count from the C ABI), never as a list count."""
+    import dataclasses
+
+    from bpdecode_amd import _lib
+    from bpdecode_amd.grammar.frames import SLOTS, KEY_WORDS, frame_lists
+
+    g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(GRAMMARS[0])), VOCAB)
+    order, _ = _walk_order(g.tok_offsets, g.tok_bytes, g.vocab_size, g.eos_id)
+    assert frame_lists(g, order.numpy()) is not None
+    dst = g.edge_dst.clone()
+    dst[0] = g.num_states
+    bad = dataclasses.replace(g, edge_dst=dst, _c={})
+    with pytest.raises(RuntimeError, match="out of range"):
+        frame_lists(bad, order.numpy())
+    # the library's own check, past the Python validation
+    bad._validate = lambda: None
+    keys = np.zeros((4, KEY_WORDS), np.int32)
+    trans = np.zeros((4, 256), np.int32)
+    slots = np.zeros(SLOTS, np.uint32)
+    ptr = lambda a: a.ctypes.data_as(_lib.C.c_void_p)  # noqa: E731
+    lib = _lib.lib()
+    assert lib.bpd_host_frame_lists(_lib.C.byref(bad.c_table()), 4, ptr(keys), ptr(trans),
+                                    ptr(slots)) == -_lib.ERR_INVALID
+    assert b"destination out of range" in lib.bpd_last_error()
+    assert lib.bpd_host_frame_lists(None, 4, ptr(keys), ptr(trans), ptr(slots)) == -_lib.ERR_INVALID
+    assert lib.bpd_host_frame_lists(_lib.C.byref(g.c_table()), 4, ptr(keys), ptr(trans), ptr(slots)) > 0
