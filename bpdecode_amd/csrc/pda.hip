@@ -1998,24 +1998,39 @@ extern "C" size_t bpd_pda_workspace_bytes(int64_t rows, int32_t vocab) {
   return memo_ws_bytes(rows, vocab);
 }
 
-extern "C" int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data,
-                            int64_t n) {
+namespace {
+
+// bpd_pda_feed's walk: 0 or an error code, whether every byte kept the set
+// non-empty in *kept.
+int pda_feed_impl(const BpdPdaTable* g, int32_t* config, const uint8_t* data, int64_t n, bool* kept) {
   BPD_REQUIRE(g && config, "null argument");
   BPD_REQUIRE(g->num_states > 0, "empty PDA table");
+  BPD_REQUIRE(n >= 0 && (n == 0 || data), "bad byte buffer");
   BPD_REQUIRE(host_config_ok(config, g->num_states), "config-set is malformed");
   const PdaTableView gv = table_view(*g);
   std::vector<int32_t> x(kConfigWords), y(kConfigWords);
   FlatView cur{x.data()}, nxt{y.data()};
   std::copy(config, config + kConfigWords, x.data());
+  *kept = false;
   for (int64_t i = 0; i < n; ++i) {
     nxt.reset_all();
-    if (!advance_byte(gv, cur, nxt, data[i])) return 0;
+    if (!advance_byte(gv, cur, nxt, data[i])) return BPD_OK;
     const FlatView tmp = cur;
     cur = nxt;
     nxt = tmp;
   }
   std::copy(cur.w, cur.w + kConfigWords, config);
-  return 1;
+  *kept = true;
+  return BPD_OK;
+}
+
+}  // namespace
+
+extern "C" int bpd_pda_feed(const BpdPdaTable* g, int32_t* config, const uint8_t* data,
+                            int64_t n) {
+  bool kept = false;
+  const int rc = pda_feed_impl(g, config, data, n, &kept);
+  return rc != BPD_OK ? -rc : (kept ? 1 : 0);
 }
 
 extern "C" int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out) {

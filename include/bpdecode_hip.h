@@ -4,6 +4,8 @@
  *
  * Plain pointers and sizes only.  Every entry point returns BPD_OK (0) or an
  * error code; bpd_last_error() then describes the failure (thread-local).
+ * The two that return a value on success (bpd_pda_feed, a verdict;
+ * bpd_host_frame_lists, a count) return their error codes negated.
  * Device entry points take device pointers and a hipStream_t (as void*),
  * enqueue work on that stream and return without synchronising.  Host entry
  * points (bpd_host_*) take host pointers and run on the calling thread; they

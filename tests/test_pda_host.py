@@ -451,3 +451,16 @@ def test_frame_lists_reject_bad_tables():
     assert b"destination out of range" in lib.bpd_last_error()
     assert lib.bpd_host_frame_lists(None, 4, ptr(keys), ptr(trans), ptr(slots)) == -_lib.ERR_INVALID
     assert lib.bpd_host_frame_lists(_lib.C.byref(g.c_table()), 4, ptr(keys), ptr(trans), ptr(slots)) > 0
+
+
+def test_feed_rejects_a_malformed_config_set():
+    """bpd_pda_feed's argument checks come back as errors (negative codes),
+    not as its 'every byte kept' result."""
+    g = build_pda_tensors(CompiledGrammar.build(parse_gbnf(GRAMMARS[0])), VOCAB)
+    c = g.init_config()
+    assert g.feed(c, b"((x")
+    bad = c.clone()
+    bad[0] = 99  # more configs than a set holds
+    with pytest.raises(RuntimeError, match="malformed"):
+        g.feed(bad, b"x")
+    assert not g.feed(c, b"]")
