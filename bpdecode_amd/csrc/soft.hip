@@ -362,6 +362,7 @@ constexpr int kStatLoads = 4;                              // float4 loads per t
 constexpr int64_t kStatChunk = kPriorThreads * 4 * kStatLoads;  // tokens per block
 constexpr size_t kPriorMaxLds = 60 * 1024;
 constexpr float kLog2e = 1.4426950408889634f;
+typedef float F4v __attribute__((ext_vector_type(4)));  // float4 for the non-temporal builtins
 
 // 2^x by the hardware exponential (v_exp_f32); used for x <= 0.
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -1393,8 +1394,9 @@ __global__ __launch_bounds__(kPriorOutThreads) void prior_out_kernel(
 // gather the logits of the members whose class has a finite lookahead value
 // from the row's state and write x - lse + alpha * z there (EOS: its log
 // softmax when the state accepts); the chunk then goes out as coalesced
-// float4 stores (every 128-byte line written whole).  Needs vocab, ld and
-// the logits aligned to 4 floats.
+// float4 non-temporal stores (every 128-byte line written whole; nothing
+// reads the rows again in this call).  Needs vocab, ld and the logits
+// aligned to 4 floats.
 template <int Cap>
 __global__ __launch_bounds__(kPriorOutThreads) void prior_out_list_kernel(
     float* __restrict__ logits, int64_t ld, int64_t V, const uint32_t* __restrict__ members, int32_t C,
@@ -1454,7 +1456,10 @@ __global__ __launch_bounds__(kPriorOutThreads) void prior_out_list_kernel(
 #pragma unroll
   for (int q = 0; q < kGroups; ++q) {
     const int64_t t = base + (int64_t(q) * kPriorOutThreads + threadIdx.x) * 4;
-    if (t < V) *reinterpret_cast<float4*>(row + t) = outs[q * kPriorOutThreads + threadIdx.x];
+    if (t < V) {
+      const float4 o = outs[q * kPriorOutThreads + threadIdx.x];
+      __builtin_nontemporal_store(F4v{o.x, o.y, o.z, o.w}, reinterpret_cast<F4v*>(row + t));
+    }
   }
 }
 
