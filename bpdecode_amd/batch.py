@@ -13,7 +13,6 @@ from __future__ import annotations
 
 import array
 import operator
-from collections import OrderedDict, defaultdict
 from collections.abc import Hashable, Sequence
 
 import torch
@@ -27,56 +26,77 @@ FREE = -2  # slot holds no sequence
 BROKEN = -1  # a committed token left the grammar (matches step() == -1)
 
 
+class _RecencyMap:
+    """A bounded map that forgets its least recently used key: a dict's
+    insertion order is its recency order (a hit is popped and re-inserted at
+    the end), so the oldest key is always the first one."""
+
+    __slots__ = ("_d", "_cap")
+
+    def __init__(self, capacity: int) -> None:
+        self._d: dict = {}
+        self._cap = capacity
+
+    def lookup(self, key):
+        val = self._d.pop(key, None)
+        if val is not None:
+            self._d[key] = val
+        return val
+
+    def insert(self, key, val) -> None:
+        self._d[key] = val
+        while len(self._d) > self._cap:
+            del self._d[next(iter(self._d))]
+
+    def __len__(self) -> int:
+        return len(self._d)
+
+
 class MaskCache:
-    """LRU of allowed-token ids per DFA state (batch.py:35-86 of the
-    reference); the ids come from the packed allow-bit kernel."""
+    """Allowed-token ids per DFA state, kept for the ``max_states`` most
+    recently asked states (the API of batch.py:35-86 of the reference).  A
+    state's ids are read from the packed allow bits of that state; the
+    device mask does not need them (it masks every row in one launch from
+    the grammar's allow-bit table)."""
 
     def __init__(self, fsa: FsaTensors, max_states: int = 512) -> None:
         self._fsa = fsa
-        self._vocab = int(fsa.offsets.numel() - 1)
-        self._max = max_states
-        self._allowed: OrderedDict[int, torch.Tensor] = OrderedDict()
+        self._vocab = fsa.vocab_size
+        self._ids = _RecencyMap(max_states)
 
     def _compute(self, state: int) -> torch.Tensor:
-        st = torch.tensor([state], dtype=torch.int32, device=self._fsa.device)
+        dev = self._fsa.device
         if state < 0:
-            return torch.empty(0, dtype=torch.long, device=self._fsa.device)
-        bits = ops.compute_mask(self._fsa, st)[0].to(torch.int64) & 0xFFFFFFFF
-        t = torch.arange(self._vocab, device=bits.device)
-        on = (bits[t >> 5] >> (t & 31)) & 1
-        return on.nonzero(as_tuple=False).squeeze(1).to(torch.long)
+            return torch.empty(0, dtype=torch.long, device=dev)
+        words = ops.compute_mask(self._fsa, torch.tensor([state], dtype=torch.int32, device=dev))[0]
+        shifts = torch.arange(32, dtype=torch.int64, device=dev)
+        flags = (words.to(torch.int64).unsqueeze(1) >> shifts) & 1  # [words, 32], LSB first
+        return flags.reshape(-1)[: self._vocab].nonzero().view(-1)
 
     def allowed_ids(self, state: int) -> torch.Tensor:
-        hit = self._allowed.get(state)
-        if hit is not None:
-            self._allowed.move_to_end(state)
-            return hit
-        ids = self._compute(state)
-        self._allowed[state] = ids
-        if len(self._allowed) > self._max:
-            self._allowed.popitem(last=False)
+        ids = self._ids.lookup(state)
+        if ids is None:
+            ids = self._compute(state)
+            self._ids.insert(state, ids)
         return ids
 
     def __len__(self) -> int:
-        return len(self._allowed)
+        return len(self._ids)
 
     def apply(self, states: torch.Tensor, logits: torch.Tensor, neg_inf: float = float("-inf")):
         """In place: mask ``logits`` [n, vocab] given one state per row.  On
         the device the grammar's packed allow-bit table (every state's mask,
         built once) or the walking kernel masks all rows in one launch, with
-        no host round trip; on the host rows are grouped by state and the
-        cached id lists applied."""
+        no host round trip.  On the host each distinct state's cached ids
+        set its row of a keep table, and one ``masked_fill_`` through the
+        rows' index into that table masks the batch."""
         if logits.device.type == "cuda":
             return ops.apply_mask_(logits, self._fsa, states.to(logits.device), neg_inf)
-        by_state: dict[int, list[int]] = defaultdict(list)
-        for i, s in enumerate(states.tolist()):
-            by_state[s].append(i)
-        for state, rows in by_state.items():
-            allowed = self.allowed_ids(state).to(logits.device)
-            r = torch.tensor(rows, device=logits.device)
-            keep = logits.index_select(0, r).index_select(1, allowed)
-            logits[r] = neg_inf
-            logits[r.unsqueeze(1), allowed] = keep
+        uniq, row_of = torch.unique(states.reshape(-1).cpu(), return_inverse=True)
+        keep = torch.zeros((uniq.numel(), logits.shape[1]), dtype=torch.bool)
+        for i, st in enumerate(uniq.tolist()):
+            keep[i, self.allowed_ids(st).cpu()] = True
+        logits.masked_fill_(~keep[row_of].to(logits.device), neg_inf)
         return logits
 
 
@@ -89,27 +109,24 @@ def build_bundle(pattern, vocab: Vocabulary, device: torch.device) -> FsaTensors
 
 
 class GrammarCache:
-    """LRU of compiled grammars for one vocabulary and device."""
+    """Compiled grammars of one vocabulary on one device, keyed by pattern;
+    the ``max_size`` most recently used are kept (batch.py:89-115 of the
+    reference)."""
 
     def __init__(self, vocab: Vocabulary, device: torch.device | str = "cpu", max_size: int = 128) -> None:
         self._vocab = vocab
         self._device = torch.device(device)
-        self._max = max_size
-        self._cache: OrderedDict[str, FsaTensors] = OrderedDict()
+        self._bundles = _RecencyMap(max_size)
 
     def get(self, pattern: str) -> FsaTensors:
-        hit = self._cache.get(pattern)
-        if hit is not None:
-            self._cache.move_to_end(pattern)
-            return hit
-        fsa = build_bundle(pattern, self._vocab, self._device)
-        self._cache[pattern] = fsa
-        if len(self._cache) > self._max:
-            self._cache.popitem(last=False)
+        fsa = self._bundles.lookup(pattern)
+        if fsa is None:
+            fsa = build_bundle(pattern, self._vocab, self._device)
+            self._bundles.insert(pattern, fsa)
         return fsa
 
     def __len__(self) -> int:
-        return len(self._cache)
+        return len(self._bundles)
 
 
 def _stage(values: array.array, device: torch.device) -> torch.Tensor:
@@ -147,7 +164,8 @@ class ConstraintBatch:
         self._pool = torch.full((capacity,), FREE, dtype=torch.int32, device=self.device)
         self._pending: dict[int, int] = {}
         self._slot_of: dict[Hashable, int] = {}
-        self._free: list[int] = list(reversed(range(capacity)))
+        self._recycled: list[int] = []  # evicted slots, reused last-in first-out
+        self._fresh = 0  # slots [fresh, capacity) were never handed out
         self._version = 0
         self._ids: list | None = None  # seq ids the cached slot tensor holds
         self._ids_version = -1
@@ -203,13 +221,19 @@ class ConstraintBatch:
         return self._pool
 
     # --- lifecycle -------------------------------------------------------
+    def _take_slot(self) -> int:
+        if self._recycled:
+            return self._recycled.pop()
+        if self._fresh >= self.capacity:
+            raise RuntimeError(f"ConstraintBatch is at capacity ({self.capacity} sequences)")
+        self._fresh += 1
+        return self._fresh - 1
+
     def add(self, seq_id: Hashable) -> int:
+        """Give ``seq_id`` a slot at the grammar's start state."""
         if seq_id in self._slot_of:
-            raise KeyError(f"sequence {seq_id!r} already in the batch")
-        if not self._free:
-            raise RuntimeError("ConstraintBatch is at capacity")
-        slot = self._free.pop()
-        self._slot_of[seq_id] = slot
+            raise KeyError(f"sequence {seq_id!r} is already in the batch")
+        slot = self._slot_of[seq_id] = self._take_slot()
         self._pending[slot] = self.fsa.start
         self._version += 1
         return slot
@@ -217,7 +241,7 @@ class ConstraintBatch:
     def evict(self, seq_id: Hashable) -> None:
         slot = self._slot_of.pop(seq_id)
         self._pending[slot] = FREE
-        self._free.append(slot)
+        self._recycled.append(slot)
         self._version += 1
 
     def reset(self, seq_id: Hashable) -> None:

@@ -478,27 +478,33 @@ class CFGConstraintBatch:
         self._configs = self.g.init_batch(capacity)
         self._broken = torch.zeros(capacity, dtype=torch.bool, device=self.device)
         self._slot_of: dict[Hashable, int] = {}
-        self._free: list[int] = list(reversed(range(capacity)))
+        self._recycled: list[int] = []  # evicted slots, reused last-in first-out
+        self._fresh = 0  # slots [fresh, capacity) were never handed out
         self._version = 0
         self._slot_key = None
         self._slot_tensor = None
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device) if self.device.type == "cuda" else None
 
+    def _take_slot(self) -> int:
+        if self._recycled:
+            return self._recycled.pop()
+        if self._fresh >= self.capacity:
+            raise RuntimeError(f"CFGConstraintBatch is at capacity ({self.capacity} sequences)")
+        self._fresh += 1
+        return self._fresh - 1
+
     def add(self, seq_id: Hashable) -> int:
+        """Give ``seq_id`` a slot holding the grammar's initial config-set."""
         if seq_id in self._slot_of:
-            raise KeyError(f"sequence {seq_id!r} already in the batch")
-        if not self._free:
-            raise RuntimeError("CFGConstraintBatch is at capacity")
-        slot = self._free.pop()
-        self._slot_of[seq_id] = slot
+            raise KeyError(f"sequence {seq_id!r} is already in the batch")
+        slot = self._slot_of[seq_id] = self._take_slot()
         self._configs[slot] = self.g.init_config()
         self._broken[slot] = False
         self._version += 1
         return slot
 
     def evict(self, seq_id: Hashable) -> None:
-        slot = self._slot_of.pop(seq_id)
-        self._free.append(slot)
+        self._recycled.append(self._slot_of.pop(seq_id))
         self._version += 1
 
     def reset(self, seq_id: Hashable) -> None:

@@ -183,6 +183,26 @@ def test_mask_cache_matches_uncached(pattern):
     assert torch.equal(want, got2) and len(mc) == fsa.num_states
 
 
+def test_mask_cache_bounded_and_negative_states():
+    """Rows at FREE / BROKEN are masked whole; with room for two states the
+    least recently asked one is dropped and recomputed on its next use."""
+    fsa = GrammarCache(VOCAB).get("[01]+")
+    st = torch.tensor([FREE, 0, BROKEN, 1, 0], dtype=torch.int32)
+    mc = MaskCache(fsa, max_states=2)
+    base = torch.randn(len(st), VOCAB.size)
+    want = base.clone()
+    ops.apply_mask_(want, fsa, st)
+    got = mc.apply(st, base.clone())
+    assert torch.equal(want, got)
+    assert torch.isneginf(got[0]).all() and torch.isneginf(got[2]).all()
+    assert len(mc) == 2
+    first = mc.allowed_ids(1)
+    mc.allowed_ids(0)
+    mc.allowed_ids(FREE)  # drops state 1, the least recently asked
+    assert len(mc) == 2 and 1 not in mc._ids._d
+    assert torch.equal(mc.allowed_ids(1), first)
+
+
 def test_churn_matches_oracle_replay():
     """Continuous batching (add / evict / commit) vs a numpy replay."""
     fsa = FsaTensors.build("[a-c]*b|a+1", TOY_VOCAB)
