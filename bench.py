@@ -142,18 +142,21 @@ def parse_args(argv=None):
     p.add_argument("--cpu-steps", type=int, default=8, help="recorded dense steps replayed on the CPU")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument("--no-flush", action="store_true", help="keep caches warm between steps")
-    p.add_argument("--workload", choices=["all", "dense", "pda", "soft", "schema"], default="all",
+    p.add_argument("--workload", choices=["all", "dense", "pda", "soft", "schema", "regex"], default="all",
                    help="all (default): the dense headline with pda, soft and schema nested; or one "
                         "workload alone")
+    p.add_argument("--regex-steps", type=int, default=64)
     p.add_argument("--schema-rows", type=int, default=512)
     p.add_argument("--schema-steps", type=int, default=64)
     p.add_argument("--pda-rows", type=int, default=256)
     p.add_argument("--pda-steps", type=int, default=64)
-    p.add_argument("--pda-cpu-rows", type=int, default=4, help="rows of one step replayed on the CPU")
+    p.add_argument("--pda-cpu-rows", type=int, default=32,
+                   help="rows of one step replayed on one CPU thread (all rows run over the host threads)")
     p.add_argument("--soft-rows", type=int, default=128)
     p.add_argument("--soft-k", type=int, default=4)
     p.add_argument("--soft-steps", type=int, default=64)
-    p.add_argument("--soft-cpu-rows", type=int, default=2, help="rows replayed on the float64 oracle")
+    p.add_argument("--soft-cpu-rows", type=int, default=8,
+                   help="rows timed through the fp32 torch CPU restatement")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="instead: run a plain device copy of MB megabytes 20 times (PMC scale check)")
     return p.parse_args(argv)
@@ -191,10 +194,13 @@ def main(argv=None) -> int:
         out = bench_soft(args)
     elif args.workload == "schema":
         out = bench_schema(args)
+    elif args.workload == "regex":
+        out = bench_regex(args)
     else:
         out = bench_dense(args)
         if args.workload == "all":
-            for name, fn in (("pda", bench_pda), ("soft", bench_soft), ("schema", bench_schema)):
+            for name, fn in (("pda", bench_pda), ("soft", bench_soft), ("schema", bench_schema),
+                             ("regex_cpu", bench_regex)):
                 print(f"[bench] {name}", file=sys.stderr, flush=True)
                 out[name] = fn(args)
     print(json.dumps(out))
@@ -262,7 +268,7 @@ def _line_bytes_per_state(fsa, e: int):
     merged below the caches), a line of kept elements is not touched."""
     import numpy as np
 
-    bits = fsa.allow_bits.cpu().numpy().view(np.uint32)
+    bits = fsa.ensure_allow_bits().cpu().numpy().view(np.uint32)
     S, W = bits.shape
     V = fsa.vocab_size
     per = 128 // e  # elements per line
@@ -368,6 +374,7 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
     res["line_bytes"] = line_bytes[warmup:]
     res["passes_agree"] = parity
     res["recorded"] = recorded
+    res["committed"] = torch.cat(nxt_ref).cpu()  # every step's committed states, in order
     return res
 
 
@@ -511,18 +518,163 @@ def _dense_cpu_baseline(args, fsa, recorded, B, V):
     return base, parity
 
 
-# ----------------------------------------------------------------- schema --
-def bench_schema(args) -> dict:
-    """Flat JSON-Schema document DFA (826 states, forced dense) over the
-    serving vocab, B rows from random valid partial documents of 0-80 bytes,
-    bf16 logits N(0, 3), no churn, the dense step as in the headline; plus
-    the symbol-class walking kernel (no [states, vocab] table) on the same
-    inputs, compared bit for bit."""
+# ------------------------------------------------------------------ regex --
+def _aten_dense_step(tok_next, states, logits, tokens):
+    """The reference's dense step as it is written in ATen (ops.py:271-276
+    mask, ops.py:301-306 commit), on whatever device the tensors are on."""
+    import torch
+
+    s = states.long()
+    rejected = tok_next.index_select(0, s.clamp(min=0)) == -1
+    rejected |= (s < 0).unsqueeze(1)
+    logits.masked_fill_(rejected, float("-inf"))
+    nxt = tok_next[s.clamp(min=0), tokens.long()]
+    return torch.where(s < 0, torch.full_like(nxt, -1), nxt).to(torch.int32)
+
+
+def bench_regex(args) -> dict:
+    """The regex dense-DFA path on the CPU: ([0-9]{1,3}\.){3}[0-9]{1,3} over
+    a seeded V = 32,000 vocabulary, B = 8 rows from random valid prefixes,
+    fp32 logits N(0, 1), 64 steps of apply_mask then commit with the token
+    sampled from the masked softmax.  The value is the library's host path
+    (ConstraintBatch on CPU tensors -> bpd_host_dense_*); the reference's
+    ATen op sequence runs the same steps beside it (its CPU path), and the
+    device path the same trajectory on the GPU."""
     import numpy as np
     import torch
 
     from bpdecode_amd import synth
     from bpdecode_amd.batch import ConstraintBatch
+    from bpdecode_amd.ops import FsaTensors
+
+    B, V, steps, warm = 8, 32_000, args.regex_steps, args.warmup
+    vocab = synth.ipv4_vocab(V, seed=0)
+    fsa = FsaTensors.build(synth.IPV4, vocab)
+    starts = synth.random_walk_states(fsa.tok_next, fsa.start, vocab.eos_id, B, 3, seed=0)
+    n_total = warm + steps
+    logits = [synth.logits(B, V, 1.0, torch.float32, seed=300 + k) for k in range(n_total)]
+    gen = torch.Generator().manual_seed(3)
+    ids = list(range(B))
+
+    # the library's host path, tokens sampled from its masks
+    batch = ConstraintBatch(fsa, capacity=B)
+    for i in ids:
+        batch.add(i)
+    batch._state[:B] = starts
+    host_s, tokens, masks, committed = [], [], [], []
+    for k in range(n_total):
+        x = logits[k].clone()
+        c0 = time.perf_counter()
+        batch.apply_mask(ids, x)
+        t_mask = time.perf_counter() - c0
+        tok = torch.multinomial(torch.softmax(x, dim=-1), 1, generator=gen).view(-1)
+        c0 = time.perf_counter()
+        nxt = batch.commit(ids, tok)
+        host_s.append(t_mask + time.perf_counter() - c0)
+        tokens.append(tok)
+        masks.append(x)
+        committed.append(nxt.clone())
+
+    # the reference's ATen sequence on the same inputs
+    tn = fsa.tok_next
+    st = starts.clone().to(torch.int32)
+    aten_s, agree = [], True
+    for k in range(n_total):
+        x = logits[k].clone()
+        c0 = time.perf_counter()
+        nxt = _aten_dense_step(tn, st, x, tokens[k])
+        aten_s.append(time.perf_counter() - c0)
+        agree &= torch.equal(x, masks[k]) and torch.equal(nxt, committed[k])
+        st = nxt
+
+    dev_us = None
+    if torch.cuda.is_available():
+        dev_us, dev_agree = _regex_device(fsa, starts, logits, tokens, masks, committed, ids, warm)
+        agree &= dev_agree
+    host_us = statistics.fmean(host_s[warm:]) * 1e6
+    aten_us = statistics.fmean(aten_s[warm:]) * 1e6
+    return _regex_line(args, fsa, B, V, steps, host_s[warm:], host_us, aten_us, dev_us, agree)
+
+
+def _regex_device(fsa, starts, logits, tokens, masks, committed, ids, warm):
+    """The device path on the regex trajectory: (mean µs/step, agreement)."""
+    import torch
+
+    from bpdecode_amd.batch import ConstraintBatch
+
+    B, n_total = len(ids), len(logits)
+    dev = torch.device("cuda:0")
+    dbatch = ConstraintBatch(fsa, capacity=B, device=dev)
+    for i in ids:
+        dbatch.add(i)
+    dbatch._state[:B] = starts.to(dev)
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    ev = HipEvents(2 * n_total)
+    dev_logits = [x.to(dev) for x in logits]
+    dev_tokens = [t.to(dev) for t in tokens]
+    dev_next = []
+    for k in range(n_total):
+        dbatch.prepare(ids)
+        ev.record(2 * k, sh)
+        dbatch.apply_mask(ids, dev_logits[k])
+        dev_next.append(dbatch.commit(ids, dev_tokens[k]))
+        ev.record(2 * k + 1, sh)
+    torch.cuda.synchronize()
+    dev_ms = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in range(warm, n_total)]
+    ev.destroy()
+    agree = all(torch.equal(dev_logits[k].cpu(), masks[k]) and torch.equal(dev_next[k].cpu(), committed[k])
+                for k in range(n_total))
+    return statistics.fmean(dev_ms) * 1e3, agree
+
+
+def _regex_line(args, fsa, B, V, steps, host_s, host_us, aten_us, dev_us, agree) -> dict:
+    import torch
+
+    return {
+        "metric": "µs/step apply_mask+commit on the CPU, IPv4 regex DFA, B=8 V=32000 fp32",
+        "value": round(host_us, 2),
+        "unit": "us/step",
+        "steps": steps,
+        "dtype": "fp32",
+        "config": {"workload": "regex dense-DFA path on the CPU (library host entry points via "
+                               "ConstraintBatch on CPU tensors)",
+                   "batch_rows": B, "vocab": V, "dfa_states": fsa.num_states, "logits": "fp32 N(0,1)"},
+        "median_us_per_step": round(statistics.median(host_s) * 1e6, 2),
+        "us_per_token_per_sequence": round(host_us / B, 2),
+        "cores": 1,
+        "cpu_baseline": {
+            "value": round(aten_us, 2),
+            "unit": "us/step",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"the same {steps} steps through the reference's ATen op sequence "
+                       "(ops.py:271-276 mask, ops.py:301-306 commit) on CPU tensors"),
+            "us_per_token_per_sequence": round(aten_us / B, 2),
+            "host_cpus": os.cpu_count(),
+            "host_cpu_model": _cpu_model(),
+        },
+        "device_us_per_step": None if dev_us is None else round(dev_us, 3),
+        "reference_published_cpu_us_per_token_per_sequence": {
+            "value": 92, "hardware": "Apple M-series CPU, batch 8, V=151,643 (Qwen2.5 tokenizer)",
+            "source": "bench/RESULTS.md:38-46 (ipv4)"},
+        "parity_host_aten_device_every_step": bool(agree),
+    }
+
+
+# ----------------------------------------------------------------- schema --
+def bench_schema(args) -> dict:
+    """Flat JSON-Schema document DFA (826 states) over the serving vocab, B
+    rows from random valid partial documents of 0-80 bytes, bf16 logits
+    N(0, 3), no churn.  Three bundles of the same grammar on the same
+    inputs: forced dense (the value: tok_next and its allow-bit table), the
+    default ``auto`` bundle (S * V is above the density limit, so no
+    tok_next: the allow-bit table built from trans, the fused walking
+    commit) and the symbol-class walking kernels alone; all three commit the
+    same states step for step."""
+    import torch
+
+    from bpdecode_amd import ops, synth
+    from bpdecode_amd.batch import ConstraintBatch, build_bundle
     from bpdecode_amd.grammar.json_schema import json_schema_to_grammar
     from bpdecode_amd.grammar.pda import CompiledGrammar
     from bpdecode_amd.grammar.regular import residual_dfa
@@ -543,9 +695,26 @@ def bench_schema(args) -> dict:
     d_step = [B * V * 2 * 2 + u * V * 4 + 16 * B for u in U]
     t_step = statistics.fmean(r["kernel_ms"])
 
-    # the walking kernel on the same logits and tokens, compared every step
+    # the default auto bundle: no tok_next, allow bits built from trans
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    auto = build_bundle(dfa, vocab, dev)
+    auto.ensure_allow_bits()
+    torch.cuda.synchronize()
+    auto_setup_s = time.perf_counter() - t0
+    assert auto.tok_next is None
+    ra = _dense_trajectory(args, auto, B, V, torch.bfloat16, 0.0, starts, 6, steps, args.warmup)
+    t_auto = statistics.fmean(ra["kernel_ms"])
+    auto_agree = bool(torch.equal(ra["committed"], r["committed"])) and ra["passes_agree"]
+
+    # the walking kernels alone (no allow-bit table) on the same logits and tokens
     sh = torch.cuda.current_stream(dev).cuda_stream
-    walk = ConstraintBatch(plain, capacity=B, device=dev)
+    limit, ops.ALLOW_BITS_LIMIT = ops.ALLOW_BITS_LIMIT, 0
+    try:
+        walk = ConstraintBatch(plain, capacity=B, device=dev)
+    finally:
+        ops.ALLOW_BITS_LIMIT = limit
+    assert not walk._fast
     ref = ConstraintBatch(dense, capacity=B, device=dev)
     for bt in (walk, ref):
         for i in range(B):
@@ -577,6 +746,25 @@ def bench_schema(args) -> dict:
     torch.cuda.synchronize()
     walk_ms = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in range(args.warmup, n_total)]
     ev.destroy()
+    side = _memory_side(r, U, B, V, t_step)
+    traffic = _profiled_traffic("dense_fill_schema_b512_v151936.traffic.json", "dense_fill_kernel<2, true>")
+    roof = _roofline(side["bytes_per_step_mean"], t_step * 1e-3, traffic=traffic,
+                     scope="apply_mask + commit step (one event bracket)",
+                     bytes_basis=side["basis"],
+                     algorithmic_bytes_per_step_mean=side["bytes_per_step_mean"],
+                     kernel="dense_fill_kernel<2, true>",
+                     mask_kernel=_roofline(statistics.fmean(r["line_bytes"]) + statistics.fmean(U) * V / 8,
+                                           statistics.fmean(r["mask_ms"]) * 1e-3,
+                                           scope="mask launch alone (record pass bracket)",
+                                           duration_us=round(statistics.fmean(r["mask_ms"]) * 1e3, 3)),
+                     survey_formula={"bytes_per_step_mean": round(statistics.fmean(d_step), 1),
+                                     "formula": "B*V*2e + U*V*4 + 16*B",
+                                     "frac": round(statistics.fmean(d_step) / (t_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                     "note": ("charges a read and a write of every logit; the mask "
+                                              "kernel reads none and writes only rejected ones, and "
+                                              "rows inside the name string keep most of the "
+                                              "vocabulary, so this figure exceeds the peak and is "
+                                              "not a measure of this kernel")})
     return {
         "metric": "µs/step apply_mask+commit, flat JSON-Schema DFA, B=512 V=151936 bf16",
         "value": round(t_step * 1e3, 3),
@@ -586,22 +774,26 @@ def bench_schema(args) -> dict:
         "config": {"workload": "dense tok_next apply_mask+commit, flat JSON-Schema document DFA, "
                                "starting rows = random valid partial documents of 0-80 bytes",
                    "batch_rows": B, "vocab": V, "dfa_states": plain.num_states,
-                   "symbol_classes": plain.num_symbols, "logits": "bf16 N(0,3)"},
+                   "symbol_classes": plain.num_symbols, "logits": "bf16 N(0,3)",
+                   "bundle": "forced dense (tok_next + allow-bit table)"},
         "mask_us": round(statistics.fmean(r["mask_ms"]) * 1e3, 3),
         "commit_us": round(statistics.fmean(r["commit_ms"]) * 1e3, 3),
         "api_us_per_step": round(statistics.fmean(r["api_ms"]) * 1e3, 3),
+        "auto_bundle": {
+            "bundle": "GrammarCache default (dense='auto'): no tok_next; allow-bit table built "
+                      "from trans on the device, dense fill mask, fused walking commit",
+            "us_per_step": round(t_auto * 1e3, 3),
+            "mask_us": round(statistics.fmean(ra["mask_ms"]) * 1e3, 3),
+            "commit_us": round(statistics.fmean(ra["commit_ms"]) * 1e3, 3),
+            "api_us_per_step": round(statistics.fmean(ra["api_ms"]) * 1e3, 3),
+            "setup_s": round(auto_setup_s, 4),
+            "table_bytes": int(auto.allow_bits.numel() * 4),
+            "same_states_as_dense_every_step": auto_agree,
+        },
         "walking_kernel_us_per_step": round(statistics.fmean(walk_ms) * 1e3, 3),
         "distinct_live_states_mean": round(statistics.fmean(U), 2),
         "row_vocab_entries_per_s": round(B * V / (t_step * 1e-3), 1),
-        "roofline": _roofline(statistics.fmean(d_step), t_step * 1e-3, traffic=None,
-                              scope="apply_mask + commit step (one event bracket)",
-                              algorithmic_bytes_per_step_mean=round(statistics.fmean(d_step), 1),
-                              kernel="dense_fill_kernel<2, true>",
-                              memory_side=_memory_side(r, U, B, V, t_step),
-                              note=("D charges a read and a write of every logit; the kernel writes "
-                                    "only rejected logits and reads none, and rows inside the name "
-                                    "string keep most of the vocabulary, so D/t can exceed the peak; "
-                                    "memory_side counts the bytes the memory system moves")),
+        "roofline": roof,
         "passes_agree": r["passes_agree"],
         "parity_dense_vs_walking_kernel_every_step": agree,
     }
@@ -646,12 +838,15 @@ def bench_pda(args) -> dict:
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+    flush64 = None if args.no_flush else torch.zeros(512 << 20, dtype=torch.uint8, device=dev).view(torch.int64)
     first = None
     for k in range(n_total):
         logits.copy_(torch.randn((B, V), generator=gen, device=dev).mul_(3.0))
         batch._slots(ids)
         if k == args.warmup:
             first = (batch._configs.cpu(), logits.cpu())
+        if flush64 is not None:
+            flush64.sum()
         kev.record(4 * k, sh)
         batch.apply_mask(ids, logits)
         kev.record(4 * k + 1, sh)
@@ -661,6 +856,8 @@ def bench_pda(args) -> dict:
         kev.record(4 * k + 2, sh)
         batch.commit(ids, toks)
         kev.record(4 * k + 3, sh)
+        if k == args.warmup:
+            first = first + (toks.cpu(), batch._configs.cpu())
     torch.cuda.synchronize()
     timed = range(args.warmup, n_total)
     mask_ms = [kev.elapsed_ms(4 * k, 4 * k + 1) for k in timed]
@@ -688,58 +885,85 @@ def bench_pda(args) -> dict:
                                     "instructions, not by HBM)",
                               algorithmic_bytes=d_bytes, kernel="pda_memo_mask_kernel"),
     }
-    if not args.no_cpu and args.pda_cpu_rows:
-        from oracle import pda as OP
-        from oracle import ref as OR
-
-        t = OP.Table(g)
-        cfgs, raw, masked = first
-        n = min(args.pda_cpu_rows, B)
-        sub = cfgs[:n].numpy().copy()
-        lg = raw[:n].numpy().copy()
-        # the reference's own apply_mask_pda_batch (pda_cpu.cpp, compiled from
-        # its sources into oracle/_ref) where that build is present, else the
-        # C restatement
-        use_ref = OR.available()
-        c0 = time.perf_counter()
-        if use_ref:
-            OR.pda_apply_mask(t, sub, lg)
-        else:
-            OP.apply_mask(t, sub, lg)
-        cpu_s = time.perf_counter() - c0
-        out["cpu_baseline"] = {
-            "value": round(cpu_s / n * B * 1e6, 1),
-            "unit": "us/step",
-            "cores": 1,
-            "kind": "reference" if use_ref else "port",
-            "sample": (f"mask of {n} rows of the first timed step through "
-                       + ("the reference's pda_cpu.cpp apply_mask_pda_batch (oracle/_ref, one thread)"
-                          if use_ref else "oracle/pda_oracle.c (C restatement of pda_cpu.cpp, one thread)")
-                       + f", scaled to B={B}"),
-            "host_cpus": os.cpu_count(),
-            "host_cpu_model": _cpu_model(),
-        }
-        out["parity_vs_reference_sampled_rows" if use_ref else "parity_vs_oracle_sampled_rows"] = bool(
-            np.array_equal(lg, masked[:n].numpy()))
-        if use_ref:
-            threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", "16") or 16), os.cpu_count() or 1, 16))
-            npar = min(2 * threads, B)
-            subp = cfgs[:npar].numpy().copy()
-            lgp = raw[:npar].numpy().copy()
-            c0 = time.perf_counter()
-            OR.pda_apply_mask_threads(t, subp, lgp, threads)
-            par_s = time.perf_counter() - c0
-            out["cpu_baseline_rows_parallel"] = {
-                "value": round(par_s / npar * B * 1e6, 1),
-                "unit": "us/step",
-                "cores": threads,
-                "kind": "reference",
-                "sample": (f"mask of {npar} rows of the first timed step through the reference's "
-                           f"apply_mask_pda_batch, rows split over {threads} host threads "
-                           f"(oracle/_ref), scaled to B={B}"),
-                "parity_vs_device": bool(np.array_equal(lgp, masked[:npar].numpy())),
-            }
+    if not args.no_cpu:
+        out.update(_pda_cpu_baseline(args, g, first, B))
     return out
+
+
+def _pda_cpu_baseline(args, g, first, B) -> dict:
+    """The reference's own CPU step -- apply_mask_pda_batch and
+    advance_state_pda_batch of pda_cpu.cpp, compiled from its sources into
+    oracle/_ref -- on the first timed step's config-sets, logits and tokens:
+    every row of the batch over the host threads (no scaling), and a fixed
+    sample of rows on one thread (the reference runs one), scaled to B.
+    Without that build, the C restatement (oracle/pda_oracle.c) stands in."""
+    import numpy as np
+
+    from oracle import pda as OP
+    from oracle import ref as OR
+
+    t = OP.Table(g)
+    cfgs, raw, masked, toks, after = first
+    use_ref = OR.available()
+    kind = "reference" if use_ref else "port"
+    src = ("the reference's pda_cpu.cpp (oracle/_ref)" if use_ref
+           else "oracle/pda_oracle.c (C restatement of pda_cpu.cpp)")
+    threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", "16") or 16), os.cpu_count() or 1, 16))
+    tk = toks.numpy().astype(np.int32)
+    res = {}
+    # every row, rows split over the host threads; then the commit of every row
+    lg = raw.numpy().copy()
+    sub = cfgs.numpy().copy()
+    c0 = time.perf_counter()
+    if use_ref:
+        OR.pda_apply_mask_threads(t, sub, lg, threads)
+    else:
+        OP.apply_mask(t, sub, lg)
+    mask_s = time.perf_counter() - c0
+    c0 = time.perf_counter()
+    ok = OR.pda_advance(t, sub, tk) if use_ref else OP.advance(t, sub, tk)
+    commit_s = time.perf_counter() - c0
+    res["cpu_baseline"] = {
+        "value": round((mask_s + commit_s) * 1e6, 1),
+        "unit": "us/step",
+        "cores": threads if use_ref else 1,
+        "kind": kind,
+        "sample": (f"one whole step (all {B} rows, no scaling) of the first timed step through {src}: "
+                   f"apply_mask_pda_batch with the rows split over {threads if use_ref else 1} host "
+                   "threads, then advance_state_pda_batch on one thread"),
+        "mask_us": round(mask_s * 1e6, 1),
+        "commit_us": round(commit_s * 1e6, 1),
+        "host_cpus": os.cpu_count(),
+        "host_cpu_model": _cpu_model(),
+    }
+    res["parity_cpu_vs_device"] = {
+        "masks_all_rows": bool(np.array_equal(lg, masked.numpy())),
+        "committed_configs_all_rows": bool(np.array_equal(sub, after.numpy())),
+        "all_tokens_accepted": bool(ok.all()),
+    }
+    # a fixed sample of rows on one thread, mask + commit, scaled to B
+    n = min(args.pda_cpu_rows, B)
+    lg1 = raw[:n].numpy().copy()
+    sub1 = cfgs[:n].numpy().copy()
+    c0 = time.perf_counter()
+    if use_ref:
+        OR.pda_apply_mask(t, sub1, lg1)
+        OR.pda_advance(t, sub1, tk[:n])
+    else:
+        OP.apply_mask(t, sub1, lg1)
+        OP.advance(t, sub1, tk[:n])
+    one_s = time.perf_counter() - c0
+    res["cpu_baseline_single_thread"] = {
+        "value": round(one_s / n * B * 1e6, 1),
+        "unit": "us/step",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"rows 0-{n - 1} of the first timed step (mask + commit) through {src} on one "
+                   f"thread, scaled to B={B}"),
+        "parity_vs_device": bool(np.array_equal(lg1, masked[:n].numpy())
+                                 and np.array_equal(sub1, after[:n].numpy())),
+    }
+    return res
 
 
 # ------------------------------------------------------------------- soft --
@@ -801,30 +1025,64 @@ def bench_soft(args) -> dict:
     if not args.no_cpu and args.soft_cpu_rows:
         from oracle import soft as OS
 
+        torch.set_num_threads(max(1, min(16, os.cpu_count() or 1)))
         n = min(args.soft_cpu_rows, B)
-        x = src[:n].double().cpu().numpy()
-        tn = fsa.tok_next.numpy()
+        x = src.cpu()
+        tn, live, acc = fsa.tok_next, fsa.live, fsa.accept
+        OS.prior_lookahead_torch(x, tn, live, acc, fsa.eos_id, states, K, 1.0, rows=[0])  # warm-up
         c0 = time.perf_counter()
-        want = OS.prior_lookahead(x, tn, fsa.live.numpy(), fsa.accept.numpy(), fsa.eos_id,
-                                  states[:n].numpy(), K, 1.0)
+        part = OS.prior_lookahead_torch(x, tn, live, acc, fsa.eos_id, states, K, 1.0, rows=range(n))
         cpu_s = time.perf_counter() - c0
-        got = work[:n].double().cpu().numpy()
-        fin = np.isfinite(want)
-        ok = np.array_equal(np.isneginf(got), np.isneginf(want)) and bool(
-            np.all(np.abs(got[fin] - want[fin]) <= 1e-5 * np.abs(want[fin]) + 1e-5))
+        got = work.cpu()
+        rel = ((got[:n] - part[:n]).abs() / part[:n].abs().clamp(min=1.0))[torch.isfinite(part[:n])]
         out["cpu_baseline"] = {
             "value": round(cpu_s / n * B * 1e6, 1),
             "unit": "us/step",
-            "cores": 1,
+            "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{n} rows through oracle/soft.py prior_lookahead (float64 numpy, dense "
-                      f"[S, V] gathers per round), scaled to B={B}",
+            "sample": (f"{n} rows through the fp32 torch restatement of the reference's lookahead "
+                       f"(ops.py:200-259: [S, V] gathers of logZ through tok_next, logsumexp, "
+                       f"logaddexp) with the row's log-softmax as prior, on CPU tensors with "
+                       f"{torch.get_num_threads()} threads; a row costs the same at any state, "
+                       f"scaled to B={B}"),
+            "max_rel_diff_vs_device": float(rel.max()) if rel.numel() else 0.0,
             "host_cpus": os.cpu_count(),
             "host_cpu_model": _cpu_model(),
         }
-        out["parity_vs_oracle_sampled_rows"] = ok
+        out["parity_vs_oracle_all_rows"] = _soft_parity_all_rows(
+            src.double().cpu().numpy(), got.double().numpy(), fsa, states.numpy(), K)
     return out
 
+
+def _soft_parity_all_rows(x, got, fsa, states, K) -> dict:
+    """Every row of the step against the float64 oracle (oracle/soft.py),
+    rows split over host threads (numpy releases the interpreter lock in
+    its array loops): relative 1e-5 with an absolute floor of 1e-5, -inf
+    pattern exact."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    from oracle import soft as OS
+
+    tn, live, acc = fsa.tok_next.numpy(), fsa.live.numpy(), fsa.accept.numpy()
+    threads = max(1, min(16, os.cpu_count() or 1, x.shape[0]))
+    c0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        want = np.concatenate(list(ex.map(
+            lambda b: OS.prior_lookahead(x[b:b + 1], tn, live, acc, fsa.eos_id, states[b:b + 1], K, 1.0),
+            range(x.shape[0]))))
+    fin = np.isfinite(want)
+    err = np.abs(got[fin] - want[fin])
+    return {
+        "rows": int(x.shape[0]),
+        "ok": bool(np.array_equal(np.isneginf(got), np.isneginf(want))
+                   and np.all(err <= 1e-5 * np.abs(want[fin]) + 1e-5)),
+        "max_abs_err": float(err.max()) if err.size else 0.0,
+        "max_rel_err": float((err / np.maximum(np.abs(want[fin]), 1.0)).max()) if err.size else 0.0,
+        "oracle": f"oracle/soft.py prior_lookahead (float64 numpy) over {threads} host threads",
+        "oracle_s": round(time.perf_counter() - c0, 2),
+    }
 
 if __name__ == "__main__":
     raise SystemExit(main())

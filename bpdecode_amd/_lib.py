@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libbpdecode_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 OK, ERR_INVALID, ERR_HIP, ERR_OVERFLOW, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
@@ -85,8 +85,10 @@ _SIGNATURES = {
     "bpd_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp, vp]),
     "bpd_fsa_apply_mask": (cint, [C.POINTER(FsaTableC), vp, cint, i64, i64, vp, vp, f64, vp, vp]),
     "bpd_fsa_compute_mask": (cint, [C.POINTER(FsaTableC), vp, vp, i64, vp, vp, vp]),
-    "bpd_fsa_advance": (cint, [C.POINTER(FsaTableC), vp, vp, vp, cint, i64, vp, cint, vp, vp]),
+    "bpd_fsa_advance": (cint, [C.POINTER(FsaTableC), vp, vp, vp, i64, vp, cint, i64, vp, cint, vp,
+                                vp]),
     "bpd_host_dense_apply_mask": (cint, [vp, cint, i64, i64, i64, vp, i32, vp, vp, f64]),
+    "bpd_host_dense_apply_mask_bits": (cint, [vp, cint, i64, i64, i64, vp, i64, i32, vp, vp, f64]),
     "bpd_host_dense_advance": (cint, [vp, i32, i64, vp, vp, vp, cint, i64, vp, cint]),
     "bpd_host_dense_compute_mask": (cint, [vp, i32, i64, vp, vp, i64, vp]),
     "bpd_host_build_tok_next": (cint, [vp, i32, i32, i32, vp, vp, vp, vp, i64, i32, vp, i32, vp]),

@@ -12,6 +12,7 @@ applies them itself, so per-request churn costs no launch of its own.
 from __future__ import annotations
 
 import array
+import ctypes as C
 import operator
 from collections.abc import Hashable, Sequence
 
@@ -179,21 +180,29 @@ class ConstraintBatch:
         if mask_cache is True:
             mask_cache = MaskCache(self.fsa)
         self.cache: MaskCache | None = mask_cache or None
-        on_dev = self.device.type == "cuda" and self.fsa.tok_next is not None
-        if on_dev:
-            self.fsa.ensure_allow_bits()
-        # arguments of the device dense path that do not change per call
-        self._dense = on_dev
-        if on_dev:
-            tn, bits = self.fsa.tok_next, self.fsa.allow_bits
-            if tn.dtype != torch.int32 or not tn.is_contiguous():
+        # the device fast path: the mask from the packed allow-bit table, the
+        # commit from tok_next or, for a bundle without it, by the fused
+        # walking kernel; both apply the queued pool writes themselves
+        bits = self.fsa.allow_bits_or_none() if self.device.type == "cuda" else None
+        self._fast = bits is not None
+        if self.device.type == "cpu" and self.fsa.tok_next is not None:
+            self.fsa.ensure_allow_bits()  # the host mask reads V/8 bytes per row from it
+        if self._fast:
+            tn = self.fsa.tok_next
+            if tn is not None and (tn.dtype != torch.int32 or not tn.is_contiguous()):
                 self.fsa.tok_next = tn = tn.to(torch.int32).contiguous()
-            self._S, self._V = int(tn.shape[0]), int(tn.shape[1])
+            self._S, self._V = self.fsa.num_states, self.fsa.vocab_size
             self._W = int(bits.shape[1])
-            self._tn_ptr, self._bits_ptr = tn.data_ptr(), bits.data_ptr()
+            self._bits_ptr = bits.data_ptr()
             self._pool_ptr, self._err_ptr = self._pool.data_ptr(), self._err.data_ptr()
             self._f_mask = lib().bpd_dense_apply_mask_bits
-            self._f_advance = lib().bpd_dense_advance
+            if tn is not None:
+                self._tn_ptr = tn.data_ptr()
+                self._f_advance = lib().bpd_dense_advance
+                self._walk_table = None
+            else:
+                self._walk_table = C.byref(self.fsa.c_fsa_table())
+                self._f_advance = lib().bpd_fsa_advance
 
     # --- pool -----------------------------------------------------------
     def _unstage(self) -> None:
@@ -333,7 +342,7 @@ class ConstraintBatch:
         go to the device in one copy now (e.g. while the model computes the
         logits), and the next launch for the same ids applies them.  Calling
         it is optional; later add / evict / reset calls are merged in."""
-        if self._dense:
+        if self._fast:
             self._slots_fused(seq_ids, True)
         else:
             self._slots(seq_ids)
@@ -342,7 +351,7 @@ class ConstraintBatch:
                    neg_inf: float = float("-inf")) -> torch.Tensor:
         """In place: every grammar-disallowed logit of ``logits``
         [len(seq_ids), vocab] becomes ``neg_inf``."""
-        if self._dense and self.cache is None and self._fast_logits(logits, len(seq_ids)):
+        if self._fast and self.cache is None and self._fast_logits(logits, len(seq_ids)):
             code = _DENSE_CODES.get(logits.dtype)
             if code is None:
                 raise RuntimeError(f"logits dtype {logits.dtype} is not supported")
@@ -360,7 +369,7 @@ class ConstraintBatch:
         pool = self._state
         if self.cache is not None:
             self.cache.apply(pool[slots], logits, neg_inf)
-        elif self.fsa.allow_bits is not None and logits.device.type == "cuda":
+        elif self.fsa.allow_bits is not None and logits.device == pool.device:
             ops.dense_mask_bits_(logits, self.fsa.allow_bits, pool, slots, neg_inf, self._err)
         elif self.fsa.tok_next is not None:
             ops.dense_mask_(logits, self.fsa.tok_next, pool, slots, neg_inf, self._err)
@@ -403,16 +412,22 @@ class ConstraintBatch:
         by their low 32 bits, as the reference's ``tokens.to(torch.int32)``
         does."""
         B = len(seq_ids)
-        if (self._dense and tokens.device == self.device and tokens.dim() == 1
+        if (self._fast and tokens.device == self.device and tokens.dim() == 1
                 and tokens.numel() == B and tokens.is_contiguous()):
             code = _TOKEN_CODES.get(tokens.dtype)
             if code is not None:
                 slots, pend, n = self._slots_fused(seq_ids, B <= _COMMIT_FUSED_ROWS)
                 out = torch.empty(B, dtype=torch.int32, device=self.device)
-                check(self._f_advance(
-                    self._tn_ptr, self._S, self._V, self._pool_ptr, slots.data_ptr(),
-                    None if pend is None else pend.data_ptr(), n, tokens.data_ptr(), code, B,
-                    out.data_ptr(), 1, self._err_ptr, _lib.stream_of(self.device)))
+                pp = None if pend is None else pend.data_ptr()
+                if self._walk_table is None:
+                    check(self._f_advance(
+                        self._tn_ptr, self._S, self._V, self._pool_ptr, slots.data_ptr(), pp, n,
+                        tokens.data_ptr(), code, B, out.data_ptr(), 1, self._err_ptr,
+                        _lib.stream_of(self.device)))
+                else:
+                    check(self._f_advance(
+                        self._walk_table, self._pool_ptr, slots.data_ptr(), pp, n, tokens.data_ptr(),
+                        code, B, out.data_ptr(), 1, self._err_ptr, _lib.stream_of(self.device)))
                 if n:
                     self._launched()
                 return out

@@ -8,6 +8,7 @@
 // from every row state of the block.  Verdicts become fill stores (logits)
 // or wave64 ballots (packed bits).
 
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -25,6 +26,13 @@ constexpr int kFsaRows = 8;    // rows per block
 constexpr size_t kFsaMaxLds = 16 * 1024;
 constexpr int32_t kNoRow = INT32_MIN;
 constexpr int kFsaAdvThreads = 256;
+// The fused commit (one block: gather, queued pool writes, walk, scatter)
+// stages the transition table in LDS as uint16 up to this size; above it,
+// or with 65535 states or more, the walk reads it through L2.
+constexpr int kFsaCommitThreads = 1024;
+constexpr int kFsaCommitPerThread = 4;
+constexpr size_t kFsaCommitLds = 112 * 1024;
+constexpr uint16_t kReject16 = 0xFFFFu;
 
 struct FsaView {
   const int32_t* trans;
@@ -181,11 +189,130 @@ __global__ __launch_bounds__(kFsaAdvThreads) void fsa_advance_kernel(
   next_out[b] = res;
 }
 
+// Commit of up to kFsaCommitThreads * kFsaCommitPerThread rows in one block:
+// each thread reads its rows' slot, state (or the queued value of its slot)
+// and token before the table is staged, so those loads overlap the staging;
+// the queued pool writes land after the walks have read the pool and before
+// the rows write back -- the order of the calls, as in the dense commit.
+// InLds: the [S, NS] table is copied to LDS as uint16 (entries outside
+// [0, S) read as kReject16) and every walk step is one LDS read.
+template <bool InLds>
+__global__ __launch_bounds__(kFsaCommitThreads) void fsa_advance_block_kernel(
+    FsaView f, int32_t* __restrict__ states, const int64_t* __restrict__ slots,
+    const int64_t* __restrict__ pending, int32_t num_pending, const void* __restrict__ tokens,
+    int tok_dtype, int64_t rows, int32_t* __restrict__ next_out, int write_back,
+    int32_t* __restrict__ err) {
+  extern __shared__ __align__(16) uint16_t tr16[];
+  __shared__ int64_t pslot[BPD_MAX_FUSED_PENDING];
+  __shared__ int32_t pval[BPD_MAX_FUSED_PENDING];
+  const int tid = threadIdx.x;
+  for (int32_t i = tid; i < num_pending; i += kFsaCommitThreads) {
+    pslot[i] = pending[i];
+    pval[i] = int32_t(pending[num_pending + i]);
+  }
+  int32_t st[kFsaCommitPerThread];
+  int64_t tk[kFsaCommitPerThread];
+  int64_t slot[kFsaCommitPerThread];
+#pragma unroll
+  for (int i = 0; i < kFsaCommitPerThread; ++i) {
+    const int64_t b = int64_t(i) * kFsaCommitThreads + tid;
+    slot[i] = -1;
+    st[i] = -1;
+    tk[i] = 0;
+    if (b < rows) {
+      slot[i] = slots ? slots[b] : b;
+      st[i] = states[slot[i]];
+      tk[i] = read_token(tokens, tok_dtype, b);
+    }
+  }
+  if (InLds) {
+    const int64_t n = int64_t(f.S) * f.NS;
+    for (int64_t j = tid; j < n; j += kFsaCommitThreads) {
+      const int32_t v = f.trans[j];
+      tr16[j] = (v >= 0 && v < f.S) ? uint16_t(v) : kReject16;
+    }
+  }
+  __syncthreads();
+  int32_t nxt[kFsaCommitPerThread];
+#pragma unroll
+  for (int i = 0; i < kFsaCommitPerThread; ++i) {
+    const int64_t b = int64_t(i) * kFsaCommitThreads + tid;
+    nxt[i] = -1;
+    if (b >= rows) continue;
+    int32_t s = st[i];
+    for (int32_t k = 0; k < num_pending; ++k)
+      if (pslot[k] == slot[i]) s = pval[k];
+    int64_t t = tk[i];
+    if (t < 0) t += f.V;
+    int32_t res = -1;
+    if (t < 0 || t >= f.V) {
+      if (err) atomicOr(err, BPD_FLAG_TOKEN_RANGE);
+    } else if (s >= f.S) {
+      if (err) atomicOr(err, BPD_FLAG_STATE_RANGE);
+    } else if (s >= 0) {
+      if (t == f.eos) {
+        res = f.accept[s] ? s : -1;
+      } else {
+        const int32_t b0 = f.off[t], len = f.off[t + 1] - b0;
+        int32_t cur = s;
+        bool ok = true;
+        for (int32_t j = 0; j < len && ok; ++j) {
+          const int k = f.sym[b0 + j];
+          if (k >= f.NS) {
+            ok = false;
+          } else if (InLds) {
+            const uint16_t v = tr16[cur * f.NS + k];
+            ok = v != kReject16 && int32_t(v) != f.dead;
+            cur = v;
+          } else {
+            cur = f.trans[int64_t(cur) * f.NS + k];
+            ok = cur != f.dead && cur >= 0 && cur < f.S;
+          }
+        }
+        res = ok && f.live[cur] ? cur : -1;
+      }
+    }
+    nxt[i] = res;
+    if (next_out) next_out[b] = res;
+  }
+  __syncthreads();
+  for (int32_t i = tid; i < num_pending; i += kFsaCommitThreads) states[pslot[i]] = pval[i];
+  if (!write_back) return;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kFsaCommitPerThread; ++i)
+    if (slot[i] >= 0) states[slot[i]] = nxt[i];
+}
+
 __global__ void fsa_scatter_kernel(int32_t* __restrict__ states, const int64_t* __restrict__ slots,
                                    const int32_t* __restrict__ next, int64_t rows) {
   const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (b >= rows) return;
   states[slots ? slots[b] : b] = next[b];
+}
+
+// Dynamic LDS the fused commit may take on the current device: the device's
+// per-block limit less the kernel's static arrays (queried once per device).
+int commit_lds_room(size_t* room) {
+  constexpr int kDevices = 64;
+  static std::atomic<long long> cache[kDevices];  // room + 1; 0: not queried yet
+  int dev = 0;
+  BPD_HIP(hipGetDevice(&dev));
+  const bool cached = dev >= 0 && dev < kDevices;
+  if (cached) {
+    const long long c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *room = size_t(c - 1);
+      return BPD_OK;
+    }
+  }
+  int max_lds = 0;
+  BPD_HIP(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+  hipFuncAttributes fa{};
+  BPD_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&fsa_advance_block_kernel<true>)));
+  *room = size_t(max_lds) > fa.sharedSizeBytes ? size_t(max_lds) - fa.sharedSizeBytes : 0;
+  if (cached) cache[dev].store((long long)(*room) + 1, std::memory_order_relaxed);
+  return BPD_OK;
 }
 
 int check_fsa(const BpdFsaTable* t) {
@@ -265,18 +392,44 @@ extern "C" int bpd_fsa_compute_mask(const BpdFsaTable* table, const int32_t* sta
 }
 
 extern "C" int bpd_fsa_advance(const BpdFsaTable* table, int32_t* states, const int64_t* slots,
-                               const void* tokens, int token_dtype, int64_t rows, int32_t* next_out,
-                               int write_back, int32_t* err, void* stream) {
+                               const int64_t* pending, int64_t num_pending, const void* tokens,
+                               int token_dtype, int64_t rows, int32_t* next_out, int write_back,
+                               int32_t* err, void* stream) {
   if (int rc = check_fsa(table)) return rc;
   BPD_REQUIRE(token_dtype_ok(token_dtype), "unknown token dtype code %d", token_dtype);
   BPD_REQUIRE(table->vocab > 0, "empty vocabulary");
   BPD_REQUIRE(rows >= 0, "negative row count");
+  BPD_REQUIRE(num_pending >= 0 && num_pending <= BPD_MAX_FUSED_PENDING,
+              "at most %d queued pool writes per launch (got %lld)", BPD_MAX_FUSED_PENDING,
+              (long long)num_pending);
+  BPD_REQUIRE(num_pending == 0 || (pending && slots && write_back),
+              "queued writes need a slot map and write_back");
+  BPD_REQUIRE(rows > 0 || num_pending == 0, "queued writes need at least one row");
   if (rows == 0) return BPD_OK;
-  BPD_REQUIRE(states && tokens && next_out, "null pointer argument");
+  BPD_REQUIRE(states && tokens, "null pointer argument");
+  BPD_REQUIRE(next_out || write_back, "advance with neither next_out nor write_back");
   hipStream_t s = as_stream(stream);
+  const FsaView v = view_of(*table);
+  if (rows <= int64_t(kFsaCommitThreads) * kFsaCommitPerThread) {
+    const size_t lds = size_t(table->num_states) * size_t(table->num_symbols) * 2;
+    size_t room = 0;
+    if (int rc = commit_lds_room(&room)) return rc;
+    if (table->num_states < 65535 && lds <= kFsaCommitLds && lds <= room)
+      fsa_advance_block_kernel<true><<<1, kFsaCommitThreads, lds, s>>>(
+          v, states, slots, pending, int32_t(num_pending), tokens, token_dtype, rows, next_out,
+          write_back, err);
+    else
+      fsa_advance_block_kernel<false><<<1, kFsaCommitThreads, 0, s>>>(
+          v, states, slots, pending, int32_t(num_pending), tokens, token_dtype, rows, next_out,
+          write_back, err);
+    BPD_LAUNCHED();
+    return BPD_OK;
+  }
+  BPD_REQUIRE(next_out, "batches above %d rows need next_out", kFsaCommitThreads * kFsaCommitPerThread);
+  BPD_REQUIRE(num_pending == 0, "batches above %d rows take no queued writes",
+              kFsaCommitThreads * kFsaCommitPerThread);
   const unsigned g = unsigned((rows + kFsaAdvThreads - 1) / kFsaAdvThreads);
-  fsa_advance_kernel<<<g, kFsaAdvThreads, 0, s>>>(view_of(*table), states, slots, tokens, token_dtype, rows,
-                                                   next_out, err);
+  fsa_advance_kernel<<<g, kFsaAdvThreads, 0, s>>>(v, states, slots, tokens, token_dtype, rows, next_out, err);
   BPD_LAUNCHED();
   if (write_back) {
     fsa_scatter_kernel<<<g, kFsaAdvThreads, 0, s>>>(states, slots, next_out, rows);

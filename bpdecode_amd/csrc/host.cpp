@@ -28,20 +28,99 @@ inline int64_t host_token(const void* tokens, int dtype, int64_t b) {
   return read_token(tokens, dtype, b);
 }
 
+// One row's mask: a select per element (rejected -> fill, else the element
+// itself), with no branch in the loop so the compiler vectorises it.
+// Work units of the host masks: a span of kHostSpan columns of one row.
+constexpr int64_t kHostElemsPerWorker = int64_t(1) << 20;
+constexpr int64_t kHostSpan = int64_t(1) << 13;
+
+template <typename T>
+void mask_span(T* __restrict__ row, const int32_t* __restrict__ tn, int64_t n, const T fill) {
+  for (int64_t t = 0; t < n; ++t) row[t] = tn[t] == -1 ? fill : row[t];
+}
+
+// Runs task(k) for k in [0, tasks) on the calling thread, or spread over up
+// to 16 host threads, one per kHostElemsPerWorker elements of the batch (a
+// thread costs tens of microseconds to start, more while torch's own pool
+// still spins after an operator, so small batches stay on the caller).
+template <typename F>
+void for_tasks(int64_t tasks, int64_t elems, F&& task) {
+  // hardware_concurrency reads a sysfs file: asked once per process
+  static const unsigned hw = std::thread::hardware_concurrency();
+  const int64_t workers =
+      std::min<int64_t>({hw ? int64_t(hw) : 1, 16, tasks, elems / kHostElemsPerWorker});
+  if (workers <= 1) {
+    for (int64_t k = 0; k < tasks; ++k) task(k);
+    return;
+  }
+  std::vector<std::thread> pool;
+  pool.reserve(size_t(workers - 1));
+  for (int64_t w = 1; w < workers; ++w)
+    pool.emplace_back([&, w] {
+      for (int64_t k = w; k < tasks; k += workers) task(k);
+    });
+  for (int64_t k = 0; k < tasks; k += workers) task(k);  // the calling thread takes a share
+  for (auto& th : pool) th.join();
+}
+
 template <typename T>
 void mask_rows(T* logits, int64_t rows, int64_t vocab, int64_t ld, const int32_t* tok_next,
                const int32_t* states, const int64_t* slots, T fill) {
-  for (int64_t b = 0; b < rows; ++b) {
+  const int64_t spans = vocab == 0 ? 0 : (vocab + kHostSpan - 1) / kHostSpan;
+  for_tasks(rows * spans, rows * vocab, [=](int64_t task) {
+    const int64_t b = task / spans, c0 = (task - b * spans) * kHostSpan;
+    const int64_t n = std::min(kHostSpan, vocab - c0);
     const int32_t s = states[slots ? slots[b] : b];
-    T* row = logits + b * ld;
-    if (s < 0) {
-      std::fill(row, row + vocab, fill);
+    T* row = logits + b * ld + c0;
+    if (s < 0)
+      std::fill(row, row + n, fill);
+    else
+      mask_span(row, tok_next + int64_t(s) * vocab + c0, n, fill);
+  });
+}
+
+// The same mask from the packed allow bits over columns [c0, c1) of one row:
+// a word with no allowed token is 32 plain fill stores (its logits are not
+// read), a word with all allowed is skipped, a mixed word keeps its few
+// allowed elements aside around a fill or fills its few rejected ones.
+// Arguments by value and restrict pointers, so the fill loops vectorise.
+template <typename T>
+void mask_span_bits(T* __restrict__ row, const uint32_t* __restrict__ rb, int64_t c0, int64_t c1,
+                    const T fill) {
+  for (int64_t w = c0 >> 5; w << 5 < c1; ++w) {
+    const uint32_t m = rb[w];
+    T* __restrict__ p = row + (w << 5);
+    const int n = int(std::min<int64_t>(32, c1 - (w << 5)));
+    if (n < 32) {
+      for (int i = 0; i < n; ++i) p[i] = ((m >> i) & 1u) ? p[i] : fill;
+    } else if (m == 0u) {
+      for (int i = 0; i < 32; ++i) p[i] = fill;
+    } else if (m == 0xFFFFFFFFu) {
       continue;
+    } else if (__builtin_popcount(m) <= 16) {
+      T keep[32];
+      for (uint32_t r = m; r; r &= r - 1) keep[__builtin_ctz(r)] = p[__builtin_ctz(r)];
+      for (int i = 0; i < 32; ++i) p[i] = fill;
+      for (uint32_t r = m; r; r &= r - 1) p[__builtin_ctz(r)] = keep[__builtin_ctz(r)];
+    } else {
+      for (uint32_t r = ~m; r; r &= r - 1) p[__builtin_ctz(r)] = fill;
     }
-    const int32_t* tn = tok_next + int64_t(s) * vocab;
-    for (int64_t t = 0; t < vocab; ++t)
-      if (tn[t] == -1) row[t] = fill;
   }
+}
+
+template <typename T>
+void mask_rows_bits(T* logits, int64_t rows, int64_t vocab, int64_t ld, const uint32_t* bits,
+                    int64_t words, const int32_t* states, const int64_t* slots, T fill) {
+  const int64_t spans = vocab == 0 ? 0 : (vocab + kHostSpan - 1) / kHostSpan;
+  for_tasks(rows * spans, rows * vocab, [=](int64_t task) {
+    const int64_t b = task / spans, c0 = (task - b * spans) * kHostSpan;
+    const int64_t c1 = std::min(c0 + kHostSpan, vocab);
+    const int32_t s = states[slots ? slots[b] : b];
+    if (s < 0)
+      std::fill(logits + b * ld + c0, logits + b * ld + c1, fill);
+    else
+      mask_span_bits(logits + b * ld, bits + int64_t(s) * words, c0, c1, fill);
+  });
 }
 
 }  // namespace
@@ -51,7 +130,7 @@ using namespace bpd;
 
 extern "C" const char* bpd_last_error(void) { return g_error; }
 
-extern "C" int bpd_abi_version(void) { return 8; }
+extern "C" int bpd_abi_version(void) { return 9; }
 
 extern "C" int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab,
                                          int64_t ld, const int32_t* tok_next,
@@ -76,6 +155,35 @@ extern "C" int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, 
   else
     mask_rows(static_cast<uint16_t*>(logits), rows, vocab, ld, tok_next, states, slots,
               static_cast<uint16_t>(fill));
+  return BPD_OK;
+}
+
+extern "C" int bpd_host_dense_apply_mask_bits(void* logits, int dtype, int64_t rows,
+                                              int64_t vocab, int64_t ld,
+                                              const uint32_t* allow_bits, int64_t words,
+                                              int32_t num_states, const int32_t* states,
+                                              const int64_t* slots, double neg_inf) {
+  const int E = dense_elem_bytes(dtype);
+  BPD_REQUIRE(E != 0, "unknown logits dtype code %d", dtype);
+  BPD_REQUIRE(rows >= 0 && vocab >= 0 && ld >= vocab, "bad logits shape");
+  BPD_REQUIRE(num_states > 0, "empty grammar table");
+  BPD_REQUIRE(words == (vocab + 31) / 32, "allow-bit rows must hold ceil(vocab/32) words");
+  uint64_t fill = 0;
+  if (int rc = fill_bits64(dtype, neg_inf, &fill)) return rc;
+  for (int64_t b = 0; b < rows; ++b) {
+    const int32_t s = states[slots ? slots[b] : b];
+    BPD_REQUIRE(s < num_states, "index %d is out of bounds for dimension 0 with size %d", s,
+                num_states);
+  }
+  if (E == 8)
+    mask_rows_bits(static_cast<uint64_t*>(logits), rows, vocab, ld, allow_bits, words, states,
+                   slots, fill);
+  else if (E == 4)
+    mask_rows_bits(static_cast<uint32_t*>(logits), rows, vocab, ld, allow_bits, words, states,
+                   slots, static_cast<uint32_t>(fill));
+  else
+    mask_rows_bits(static_cast<uint16_t*>(logits), rows, vocab, ld, allow_bits, words, states,
+                   slots, static_cast<uint16_t>(fill));
   return BPD_OK;
 }
 

@@ -39,6 +39,10 @@ from .tokenizer import Vocabulary
 HAVE_NATIVE = True  # the library is required; loading failures raise at first use
 
 DENSE_AUTO_LIMIT = 32_000_000  # S * V at or below which build() densifies (ops.py:137-139)
+# A device bundle without tok_next gets a packed allow-bit table (S rows of
+# ceil(V/32) words, built from trans by the walking kernel) when it takes at
+# most this many bytes; above it, masks walk every token per call.
+ALLOW_BITS_LIMIT = 256 << 20
 
 
 _SOFT_ARRAYS = ("class_off", "class_tok", "class_piece", "piece_off", "state_off", "pair_class",
@@ -213,14 +217,31 @@ class FsaTensors:
         return c
 
     def ensure_allow_bits(self) -> torch.Tensor:
-        """The packed allow-bit table (built once from tok_next and kept on
-        this bundle; derived data, so sharing bundles is unaffected)."""
+        """The packed allow-bit table (built once and kept on this bundle;
+        derived data, so sharing bundles is unaffected): from tok_next when
+        the bundle has it, else, on the device, straight from ``trans`` by
+        the walking kernel (every state's row; no [states, vocab] int32
+        table).  A host bundle without tok_next is densified first."""
         if self.allow_bits is None:
-            base = self.densify()
-            st = torch.arange(base.num_states, dtype=torch.int32, device=base.device)
-            self.tok_next = base.tok_next
-            self.allow_bits = dense_compute_mask(base.tok_next, st)
+            st = torch.arange(self.num_states, dtype=torch.int32, device=self.device)
+            if self.tok_next is None and self.device.type == "cuda":
+                self.allow_bits = fsa_compute_mask(self, st)
+            else:
+                base = self.densify()
+                self.tok_next = base.tok_next
+                self.allow_bits = dense_compute_mask(base.tok_next, st)
         return self.allow_bits
+
+    def allow_bits_or_none(self) -> torch.Tensor | None:
+        """The allow-bit table of a device bundle (built on first use), or
+        None for a bundle without tok_next whose table would exceed
+        ``ALLOW_BITS_LIMIT`` bytes (its masks walk the tokens instead)."""
+        if self.allow_bits is None and self.tok_next is None:
+            if self.device.type != "cuda":
+                return None
+            if self.num_states * ((self.vocab_size + 31) // 32) * 4 > ALLOW_BITS_LIMIT:
+                return None
+        return self.ensure_allow_bits()
 
     def ensure_soft_classes(self) -> SoftClasses:
         """Token classes of the prior-weighted lookahead (built once on the
@@ -422,11 +443,9 @@ def dense_mask_(logits, tok_next, states, slots=None, neg_inf=float("-inf"), err
 
 def dense_mask_bits_(logits, allow_bits, states, slots=None, neg_inf=float("-inf"), err=None,
                      pending=None):
-    """Device mask from the packed allow-bit table (same result as
-    :func:`dense_mask_`)."""
+    """Mask from the packed allow-bit table (same result as
+    :func:`dense_mask_`), on the device or on the host."""
     dev = _same_device(logits, allow_bits, states, slots)
-    if dev.type != "cuda":
-        raise RuntimeError("the allow-bit mask runs on the device; use dense_mask_ on the host")
     work, copied = _unit_stride_rows(logits)
     B, V = work.shape
     S, W = allow_bits.shape
@@ -440,10 +459,16 @@ def dense_mask_bits_(logits, allow_bits, states, slots=None, neg_inf=float("-inf
     sl = None if slots is None else slots.to(torch.int64).contiguous()
     code = _lib.dtype_code(work.dtype, dense=True)
     ld = work.stride(0) if B > 1 else V
-    pp, np_ = _pending_args(pending)
-    check(lib().bpd_dense_apply_mask_bits(ptr(work), code, B, V, ld, ptr(allow_bits), W, S, ptr(st),
-                                          ptr(sl), pp, np_, float(neg_inf), ptr(err),
-                                          _lib.stream_of(dev)))
+    if dev.type == "cuda":
+        pp, np_ = _pending_args(pending)
+        check(lib().bpd_dense_apply_mask_bits(ptr(work), code, B, V, ld, ptr(allow_bits), W, S,
+                                              ptr(st), ptr(sl), pp, np_, float(neg_inf), ptr(err),
+                                              _lib.stream_of(dev)))
+    else:
+        if pending is not None and pending.numel():
+            raise RuntimeError("queued writes are applied by device launches only")
+        check(lib().bpd_host_dense_apply_mask_bits(ptr(work), code, B, V, ld, ptr(allow_bits), W, S,
+                                                   ptr(st), ptr(sl), float(neg_inf)))
     if copied:
         logits.copy_(work)
     return logits
@@ -548,9 +573,11 @@ def fsa_compute_mask(fsa: FsaTensors, states, slots=None, err=None) -> torch.Ten
     return out
 
 
-def fsa_advance(fsa: FsaTensors, states, tokens, slots=None, write_back=False, err=None):
+def fsa_advance(fsa: FsaTensors, states, tokens, slots=None, write_back=False, err=None, pending=None):
     """Next state per row by the walking kernel; with ``write_back`` the
-    pool ``states`` is updated at the rows' slots as well."""
+    pool ``states`` is updated at the rows' slots as well.  ``pending``:
+    queued pool writes applied by the same launch (as in
+    :func:`dense_advance`)."""
     tk = tokens.contiguous()
     if tk.dtype not in (torch.int32, torch.int64):
         tk = tk.to(torch.int64)
@@ -567,8 +594,10 @@ def fsa_advance(fsa: FsaTensors, states, tokens, slots=None, write_back=False, e
     st = states if write_back else _i32(states)
     sl = None if slots is None else slots.to(torch.int64).contiguous()
     out = torch.empty(B, dtype=torch.int32, device=dev)
-    check(lib().bpd_fsa_advance(C.byref(fsa.c_fsa_table()), ptr(st), ptr(sl), ptr(tk), _lib.index_code(tk.dtype),
-                                B, ptr(out), int(write_back), ptr(err), _lib.stream_of(dev)))
+    pp, np_ = _pending_args(pending)
+    check(lib().bpd_fsa_advance(C.byref(fsa.c_fsa_table()), ptr(st), ptr(sl), pp, np_, ptr(tk),
+                                _lib.index_code(tk.dtype), B, ptr(out), int(write_back), ptr(err),
+                                _lib.stream_of(dev)))
     return out.view(tokens.shape) if tokens.dim() else out.reshape(())
 
 
@@ -667,10 +696,13 @@ def apply_mask_(logits: torch.Tensor, fsa: FsaTensors, states: torch.Tensor,
     """In place: every disallowed logit of ``logits`` [batch, vocab] becomes
     ``neg_inf``, one grammar state per row (ops.py:262-281)."""
     if fsa.tok_next is not None:
-        if logits.device.type == "cuda":
+        if logits.device.type == "cuda" or fsa.allow_bits is not None:
             return dense_mask_bits_(logits, fsa.ensure_allow_bits(), states, neg_inf=neg_inf)
         return dense_mask_(logits, fsa.tok_next, states, neg_inf=neg_inf)
     if logits.device.type == "cuda":
+        bits = fsa.allow_bits_or_none()
+        if bits is not None:
+            return dense_mask_bits_(logits, bits, states, neg_inf=neg_inf)
         return fsa_mask_(logits, fsa, states, neg_inf=neg_inf)
     rows, idx = _walked_rows(fsa, states)
     return dense_mask_(logits, rows, idx, neg_inf=neg_inf)

@@ -180,16 +180,32 @@ int bpd_fsa_compute_mask(const BpdFsaTable* table, const int32_t* states, const 
 
 /* bpd_fsa_advance: next_out[b] = step(state(b), t(b)) (-1 off a valid path),
  * t(b) read as in bpd_dense_advance (int32 or int64, negative ids indexing
- * from the end); with write_back the pool slot is updated too.  Replaces
- * advance_state_batch_cuda (mask.hpp:99-105, torch_ops.cpp:191-229). */
+ * from the end); with write_back the pool slot is updated too.  `pending`
+ * (num_pending <= BPD_MAX_FUSED_PENDING queued pool writes: slots, then
+ * values) is applied as in bpd_dense_advance: a row whose slot has a queued
+ * write starts from that value, and the writes land before the rows write
+ * back.  Up to 4096 rows run as one fused launch (the table staged in LDS
+ * when it fits); larger batches take no queued writes and need next_out.
+ * Replaces advance_state_batch_cuda (mask.hpp:99-105, torch_ops.cpp:191-229)
+ * and, with the queued writes, ConstraintBatch.commit's pool update
+ * (batch.py:206-215) for bundles without tok_next. */
 int bpd_fsa_advance(const BpdFsaTable* table, int32_t* states, const int64_t* slots,
-                    const void* tokens, int token_dtype, int64_t rows, int32_t* next_out,
-                    int write_back, int32_t* err, void* stream);
+                    const int64_t* pending, int64_t num_pending, const void* tokens,
+                    int token_dtype, int64_t rows, int32_t* next_out, int write_back,
+                    int32_t* err, void* stream);
 
 /* Host (CPU-tensor) forms of the dense entry points. */
 int bpd_host_dense_apply_mask(void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                               const int32_t* tok_next, int32_t num_states,
                               const int32_t* states, const int64_t* slots, double neg_inf);
+/* bpd_host_dense_apply_mask_bits: the host twin of bpd_dense_apply_mask_bits
+ * (the mask from the packed allow-bit table; no queued writes): the CPU
+ * branch of apply_mask_ (ops.py:271-276), reading V/8 bytes of table per row
+ * instead of 4V. */
+int bpd_host_dense_apply_mask_bits(void* logits, int dtype, int64_t rows, int64_t vocab,
+                                   int64_t ld, const uint32_t* allow_bits, int64_t words,
+                                   int32_t num_states, const int32_t* states,
+                                   const int64_t* slots, double neg_inf);
 int bpd_host_dense_advance(const int32_t* tok_next, int32_t num_states, int64_t vocab,
                            int32_t* states, const int64_t* slots, const void* tokens,
                            int token_dtype, int64_t rows, int32_t* next_out, int write_back);

@@ -16,6 +16,12 @@ float64 numpy restatement of the soft lookahead:
   ``out[b, t] = logpi_b(t) + alpha * logZ_{k-1,b}(tok_next[s_b, t])`` on
   allowed tokens (EOS: ``logpi_b(eos)`` when ``s_b`` accepts), ``-inf``
   elsewhere.  With ``logpi == 0`` the recurrence is exactly the uniform one.
+* :func:`prior_lookahead_torch`  the same prior variant as an fp32 torch
+  program on CPU tensors, op for op the reference's build_lookahead /
+  apply_soft_ sequence (ops.py:200-259: an ``[S, V]`` gather of ``logZ``
+  through ``tok_next``, ``logsumexp`` over the vocabulary, ``logaddexp`` for
+  accepting states) with the row's log-softmax added to every gathered
+  term: the timed CPU baseline of the prior lookahead.
 """
 
 from __future__ import annotations
@@ -82,4 +88,41 @@ def prior_lookahead(logits, tok_next, live, accept, eos, states, k, alpha):
         out[b] = np.where(np.isneginf(row), NEG, lp + alpha * np.where(np.isneginf(row), 0.0, row))
         if 0 <= eos < V:
             out[b, eos] = lp[eos] if accept[s] else NEG
+    return out
+
+
+def prior_lookahead_torch(logits, tok_next, live, accept, eos, states, k, alpha, rows=None):
+    """fp32 torch restatement of :func:`prior_lookahead` (see the module
+    header); ``rows`` limits the work to those row indices (the others stay
+    ``-inf``).  Returns a float32 CPU tensor."""
+    import torch
+
+    x = torch.as_tensor(logits, dtype=torch.float32)
+    tn = torch.as_tensor(tok_next).long()
+    live = torch.as_tensor(live).bool()
+    accept = torch.as_tensor(accept).bool()
+    S, V = tn.shape
+    neg = torch.tensor(float("-inf"))
+    rejected = tn < 0
+    idx = tn.clamp(min=0)
+    has_eos = eos is not None and 0 <= eos < V
+    out = torch.full(x.shape, float("-inf"), dtype=torch.float32)
+    st = torch.as_tensor(states).long()
+    for b in (range(x.shape[0]) if rows is None else rows):
+        lp = torch.log_softmax(x[b], dim=0)
+        logz = torch.where(live, torch.zeros(S), neg.expand(S))
+        for _ in range(max(k - 1, 0)):
+            cand = torch.where(rejected, neg, logz[idx] + lp)  # [S, V]
+            nxt = torch.logsumexp(cand, dim=1)
+            if has_eos:
+                nxt = torch.where(accept, torch.logaddexp(nxt, lp[eos]), nxt)
+            logz = torch.where(live, nxt, neg.expand(S))
+        s = int(st[b])
+        if s < 0:
+            continue
+        row = torch.where(rejected[s], neg, logz[idx[s]])
+        dis = torch.isneginf(row)
+        out[b] = torch.where(dis, neg, lp + alpha * row.masked_fill(dis, 0.0))
+        if has_eos:
+            out[b, eos] = lp[eos] if bool(accept[s]) else neg
     return out

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from bpdecode_amd import ops
+from bpdecode_amd import ops, synth
 from bpdecode_amd.batch import BROKEN, FREE, ConstraintBatch, GrammarCache, MaskCache
 from bpdecode_amd.ops import FsaTensors
 from bpdecode_amd.tokenizer import Vocabulary
@@ -233,3 +233,31 @@ def test_churn_matches_oracle_replay():
             batch.evict(i)
             del pool[i]
     assert all(batch.state_of(i) == s for i, s in pool.items())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("vocab_size", [300, 320, 2048 + 5])
+def test_host_allow_bit_mask_matches_table_mask(dtype, vocab_size):
+    """The host mask from the packed allow bits (all-rejected words filled,
+    all-allowed words skipped, mixed words element by element) equals the
+    tok_next host mask and the oracle, on rows at every state, FREE and
+    BROKEN, with a row stride wider than the vocabulary."""
+    vocab = synth.serving_vocab(vocab_size, seed=5)
+    fsa = FsaTensors.build("[a-z0-9]{1,6}(\\.[a-z]+)?|x*", vocab)
+    tn = oracle_table(fsa)
+    S, V = tn.shape
+    bits = fsa.ensure_allow_bits()
+    assert np.array_equal(bits.numpy().view(np.uint32), OD.compute_mask_bits(tn, np.arange(S, dtype=np.int32)))
+    st = np.array(list(range(S)) + [FREE, BROKEN] + list(range(S))[::-2], dtype=np.int32)
+    wide = (torch.randn(len(st), V + 9) * 3).to(dtype)
+    base = wide[:, :V]
+    want = OD.apply_mask(base.clone(), tn, st)
+    got_bits = base.clone()
+    ops.dense_mask_bits_(got_bits, bits, torch.from_numpy(st))
+    view = wide.clone()[:, :V]  # stride V + 9
+    ops.dense_mask_bits_(view, bits, torch.from_numpy(st))
+    got_table = base.clone()
+    ops.dense_mask_(got_table, fsa.tok_next, torch.from_numpy(st))
+    for got in (got_bits, view, got_table):
+        assert torch.equal(got.view(torch.uint8 if dtype != torch.float64 else torch.int64),
+                           want.view(torch.uint8 if dtype != torch.float64 else torch.int64))

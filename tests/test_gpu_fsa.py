@@ -1,10 +1,13 @@
-"""Symbol-class FSA walking kernels (bundles without tok_next, the
-reference's non-dense operators) on the device against the oracle: every
-state of the toy grammars in every logits dtype with the transition table
-in LDS and in global memory, the flat JSON-Schema DFA at serving scale
-(826 states, V = 151,936: its table, 256 symbols merged into fewer
-classes, is read through L2), ConstraintBatch with slots and churn, the
-range flags, and MaskCache without a host round trip.  Bit-exact."""
+"""Bundles without tok_next (the reference's non-dense operators) on the
+device against the oracle: the symbol-class walking kernels (every state of
+the toy grammars in every logits dtype, the transition table in LDS and in
+global memory) and the allow-bit path that replaces them under a size limit
+(the table built from trans by the walking kernel, masks by the dense fill
+kernel, commits by the fused walking commit); the flat JSON-Schema DFA at
+serving scale (826 states, V = 151,936) through both and through the
+default ``auto`` bundle over a 64-step trajectory with churn;
+ConstraintBatch with slots and churn, the range flags, and MaskCache without
+a host round trip.  Bit-exact."""
 
 from __future__ import annotations
 
@@ -28,13 +31,21 @@ def _log(msg):
     print(msg, flush=True)
 
 
+@pytest.fixture(params=["walk-lds", "walk-global", "bits"])
+def nondense_path(request, monkeypatch):
+    """walk-*: the walking kernels (no allow-bit table; the table in LDS or
+    read from global memory); bits: the allow-bit table built from trans."""
+    if request.param.startswith("walk"):
+        monkeypatch.setattr(ops, "ALLOW_BITS_LIMIT", 0)
+    if request.param == "walk-global":
+        monkeypatch.setenv("BPD_FSA_TABLE", "global")
+    return request.param
+
+
 @pytest.mark.parametrize("pattern", TOY_PATTERNS)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("table", [None, "global"])
-def test_toy_every_state(dev, pattern, dtype, table, monkeypatch):
-    _log(f"case fsa walk toy {pattern!r} {dtype} table={table}")
-    if table:
-        monkeypatch.setenv("BPD_FSA_TABLE", table)
+def test_toy_every_state(dev, pattern, dtype, nondense_path):
+    _log(f"case fsa toy {pattern!r} {dtype} path={nondense_path}")
     f = FsaTensors.build(pattern, TOY_VOCAB, dense=False)
     assert f.tok_next is None
     tn = oracle_table(f)
@@ -46,6 +57,10 @@ def test_toy_every_state(dev, pattern, dtype, table, monkeypatch):
     got = lg.to(dev)
     ops.apply_mask_(got, fd, torch.from_numpy(st).to(dev))
     assert np.array_equal(bits_of(got), bits_of(want))
+    assert (fd.allow_bits is not None) == (nondense_path == "bits")
+    if fd.allow_bits is not None:  # the table built from trans: every state's oracle row
+        every = np.arange(S, dtype=np.int32)
+        assert np.array_equal(fd.allow_bits.cpu().numpy().view(np.uint32), OD.compute_mask_bits(tn, every))
     bits = ops.compute_mask(fd, torch.from_numpy(st).to(dev)).cpu().numpy().view(np.uint32)
     assert np.array_equal(bits, OD.compute_mask_bits(tn, st))
     for k in range(3):
@@ -56,8 +71,9 @@ def test_toy_every_state(dev, pattern, dtype, table, monkeypatch):
         assert nxt.cpu().tolist() == OD.advance(tn, st, toks).tolist()
 
 
-def test_flat_schema_serving_scale(dev):
+def test_flat_schema_serving_scale(dev, monkeypatch):
     _log("case fsa walk flat-schema DFA V=151936 B=256 bf16")
+    monkeypatch.setattr(ops, "ALLOW_BITS_LIMIT", 0)  # the walking kernels
     vocab = synth.serving_vocab(151_936, seed=1)
     comp = CompiledGrammar.build(json_schema_to_grammar(synth.FLAT_SCHEMA))
     dfa = residual_dfa(comp, comp.root, comp.rules[comp.root].start)
@@ -89,14 +105,14 @@ def test_flat_schema_serving_scale(dev):
     assert nxt.cpu().tolist() == OD.advance(tn, st, toks.numpy()).tolist()
 
 
-def test_batch_churn_and_range_flags(dev):
-    _log("case fsa walk ConstraintBatch churn")
+def test_batch_churn_and_range_flags(dev, nondense_path):
+    _log(f"case fsa ConstraintBatch churn path={nondense_path}")
     vocab = synth.serving_vocab(8192, seed=3)
     f = FsaTensors.build(synth.EMAIL, vocab, dense=False)
     tn = OD.build_token_transitions(f.trans.numpy(), f.accept.numpy(), f.live.numpy(), f.num_symbols,
                                     f.offsets.numpy(), f.symbols.numpy(), f.eos_id)
     batch = ConstraintBatch(f, capacity=48, device=dev)
-    assert batch.fsa.tok_next is None
+    assert batch.fsa.tok_next is None and batch._fast == (nondense_path == "bits")
     state = {}
     for i in range(32):
         batch.add(i)
@@ -152,3 +168,70 @@ def test_mask_cache_on_device_matches_host(dev):
         got = devc.apply(st.to(dev), lg.to(dev))
         assert torch.equal(got.cpu(), host)
         assert len(devc) == 0  # no per-state id lists were materialised
+
+
+def test_flat_schema_auto_mode_churn_64_steps(dev):
+    """configs[2] through the default ``auto`` bundle (S * V above the
+    density limit, so no tok_next): the allow-bit table is built from trans
+    on the device, the mask runs the dense fill kernel over it and the
+    commit the fused walking kernel.  B = 512 rows from random valid partial
+    documents of 0-80 bytes, bf16 logits N(0, 3), 10 % of the rows evicted
+    and re-added at the start state every step (queued writes riding in the
+    launches), 64 steps; every mask is compared with ATen's masked_fill_
+    over the oracle's whole table (itself equal to the device-built allow
+    bits), every commit with the oracle's advance."""
+    from bpdecode_amd.batch import build_bundle
+
+    _log("case flat-schema auto bundle V=151936 B=512 bf16 churn 64 steps: oracle table")
+    vocab = synth.serving_vocab(151_936, seed=1)
+    comp = CompiledGrammar.build(json_schema_to_grammar(synth.FLAT_SCHEMA))
+    dfa = residual_dfa(comp, comp.root, comp.rules[comp.root].start)
+    fsa = build_bundle(dfa, vocab, dev)
+    assert fsa.tok_next is None and fsa.num_states * fsa.vocab_size > 32_000_000
+    host = fsa.to("cpu")
+    tn = OD.build_token_transitions(host.trans.numpy(), host.accept.numpy(), host.live.numpy(),
+                                    host.num_symbols, host.offsets.numpy(), host.symbols.numpy(),
+                                    host.eos_id)
+    B = 512
+    batch = ConstraintBatch(fsa, capacity=2 * B, device=dev)
+    assert batch._fast and batch._walk_table is not None
+    every = np.arange(fsa.num_states, dtype=np.int32)
+    assert np.array_equal(fsa.allow_bits.cpu().numpy().view(np.uint32), OD.compute_mask_bits(tn, every))
+    _log("case flat-schema auto bundle: trajectory")
+    tn_dev = torch.from_numpy(tn).to(dev)
+    starts = synth.random_byte_walk_states(torch.from_numpy(tn), fsa.start, B, 80, seed=4).numpy()
+    state, active = {}, []
+    for i in range(B):
+        batch.add(i)
+        active.append(i)
+        state[i] = int(starts[i])
+    batch._state[:B] = torch.from_numpy(starts).to(dev)
+    nid = B
+    rng = np.random.default_rng(7)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    for step in range(64):
+        ids = list(active)
+        st = np.array([state[i] for i in ids], dtype=np.int32)
+        lg = torch.randn((B, vocab.size), generator=gen, device=dev).mul_(3.0).to(torch.bfloat16)
+        s_ = torch.from_numpy(st).to(dev).long()
+        rejected = (tn_dev.index_select(0, s_.clamp(min=0)) == -1) | (s_ < 0)[:, None]
+        want = lg.clone().masked_fill_(rejected, float("-inf"))
+        got = lg.clone()
+        batch.apply_mask(ids, got)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        toks = torch.multinomial(torch.softmax(want.float(), dim=-1), 1, generator=gen).view(-1)
+        nxt = batch.commit(ids, toks)
+        exp = OD.advance(tn, st, toks.cpu().numpy())
+        assert nxt.cpu().numpy().tolist() == exp.tolist(), step
+        for i, s in zip(ids, exp.tolist()):
+            state[i] = s
+        for j in rng.choice(B, size=B // 10, replace=False).tolist():
+            batch.evict(active[j])
+            del state[active[j]]
+            active[j] = nid
+            batch.add(nid)
+            state[nid] = fsa.start
+            nid += 1
+    batch.check_errors()
+    pool = batch._state.cpu().numpy()
+    assert all(pool[batch._slot_of[i]] == s for i, s in state.items())

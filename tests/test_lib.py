@@ -76,9 +76,15 @@ def test_fsa_entry_points_validate_before_launching():
     assert lib.bpd_fsa_apply_mask(C.byref(ok), lg.data_ptr(), _lib.DTYPE_F16, 1, 1, st.data_ptr(),
                                   None, 0.0, None, None) != 0
     # unknown token dtype; zero rows is a no-op that touches nothing
-    assert lib.bpd_fsa_advance(C.byref(ok), st.data_ptr(), None, st.data_ptr(), 7, 1, st.data_ptr(),
-                               0, None, None) != 0
+    assert lib.bpd_fsa_advance(C.byref(ok), st.data_ptr(), None, None, 0, st.data_ptr(), 7, 1,
+                               st.data_ptr(), 0, None, None) != 0
+    # queued writes need a slot map and write_back, and at most 256 per launch
+    assert lib.bpd_fsa_advance(C.byref(ok), st.data_ptr(), None, st.data_ptr(), 1, st.data_ptr(),
+                               _lib.INDEX_I32, 1, st.data_ptr(), 1, None, None) != 0
+    assert "queued writes" in lib.bpd_last_error().decode()
+    assert lib.bpd_fsa_advance(C.byref(ok), st.data_ptr(), st.data_ptr(), st.data_ptr(), 300,
+                               st.data_ptr(), _lib.INDEX_I32, 1, st.data_ptr(), 1, None, None) != 0
     assert lib.bpd_fsa_apply_mask(C.byref(ok), None, _lib.DTYPE_F32, 0, 2, None, None, 0.0, None,
                                   None) == 0
-    assert lib.bpd_fsa_advance(C.byref(ok), None, None, None, _lib.INDEX_I32, 0, None, 0, None,
-                               None) == 0
+    assert lib.bpd_fsa_advance(C.byref(ok), None, None, None, 0, None, _lib.INDEX_I32, 0, None, 0,
+                               None, None) == 0

@@ -195,3 +195,21 @@ def test_prior_k1_alpha0_is_masked_log_softmax(pattern):
     assert np.array_equal(np.isneginf(out), np.isneginf(want))
     fin = np.isfinite(want)
     assert np.allclose(out[fin], want[fin], rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("pattern", PATTERNS)
+@pytest.mark.parametrize("k", [1, 2, 4])
+def test_prior_torch_fp32_restatement_matches_float64(pattern, k):
+    """The fp32 torch restatement timed as the CPU baseline computes the
+    pinned float64 oracle's values to fp32 accuracy, with the same -inf
+    pattern (rows at negative states included)."""
+    fsa, tn, live, acc = tables(pattern)
+    states = reachable(tn, fsa.start) + [-1]
+    logits = np.random.default_rng(3 + k).normal(0.0, 3.0, size=(len(states), VOCAB.size))
+    want = OS.prior_lookahead(logits, tn, live, acc, fsa.eos_id, states, k, 0.6)
+    got = OS.prior_lookahead_torch(logits, tn, live, acc, fsa.eos_id, states, k, 0.6).double().numpy()
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+    fin = np.isfinite(want)
+    assert np.allclose(got[fin], want[fin], rtol=2e-6, atol=2e-6)
+    part = OS.prior_lookahead_torch(logits, tn, live, acc, fsa.eos_id, states, k, 0.6, rows=[0])
+    assert torch.equal(part[0], torch.from_numpy(got[0]).float()) and torch.isneginf(part[1:]).all()
