@@ -272,16 +272,35 @@ def _line_bytes_per_state(fsa, e: int):
     S, W = bits.shape
     V = fsa.vocab_size
     per = 128 // e  # elements per line
-    allowed = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little")[:, :V].astype(np.int32)
+    allowed = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little")[:, :V]
     pad = (-V) % per
     if pad:
-        allowed = np.concatenate([allowed, np.ones((S, pad), np.int32)], axis=1)
-    counts = allowed.reshape(S, -1, per).sum(axis=2)
+        allowed = np.concatenate([allowed, np.ones((S, pad), np.uint8)], axis=1)
+    counts = allowed.reshape(S, -1, per).sum(axis=2, dtype=np.int32)
     full_rej = (counts == 0).sum(axis=1)
     mixed = ((counts > 0) & (counts < per)).sum(axis=1)
     out = full_rej * 128 + mixed * 256
     lines = -(-V // per)
     return np.concatenate([out, [lines * 128]]).astype(np.float64)
+
+
+def _write_bytes_per_state(fsa, e: int, gran: int):
+    """Per state (index S: a negative state), the bytes of one row's logits
+    that lie in ``gran``-byte segments holding at least one rejected element
+    -- what the mask kernel's stores dirty at that granularity, for
+    comparison with the WRITE_SIZE counter."""
+    import numpy as np
+
+    bits = fsa.ensure_allow_bits().cpu().numpy().view(np.uint32)
+    S, W = bits.shape
+    V = fsa.vocab_size
+    per = gran // e
+    allowed = np.unpackbits(bits.view(np.uint8), axis=1, bitorder="little")[:, :V]
+    pad = (-V) % per
+    if pad:
+        allowed = np.concatenate([allowed, np.ones((S, pad), np.uint8)], axis=1)
+    dirty = (allowed.reshape(S, -1, per).sum(axis=2, dtype=np.int32) < per).sum(axis=1) * gran
+    return np.concatenate([dirty, [-(-V // per) * gran]]).astype(np.float64)
 
 
 def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup, record_cpu=0):
@@ -298,7 +317,10 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
         flush64 = torch.zeros(512 << 20, dtype=torch.uint8, device=fsa.device).view(torch.int64)
     sh = torch.cuda.current_stream(fsa.device).cuda_stream
     tokens, distinct, recorded, nxt_ref, line_bytes = [], [], [], [], []
-    per_state = _line_bytes_per_state(fsa, torch.tensor([], dtype=dtype).element_size())
+    esize = torch.tensor([], dtype=dtype).element_size()
+    per_state = _line_bytes_per_state(fsa, esize)
+    dirty_tab = {g: _write_bytes_per_state(fsa, esize, g) for g in (32, 64, 128)}
+    dirty = {g: [] for g in dirty_tab}
 
     # record pass: two brackets, sampling between them
     run = DenseRun(fsa, B, V, dtype, churn, starts, seed)
@@ -311,7 +333,10 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
         st = run.states_now(ids)
         live = st[st >= 0]
         distinct.append(int(np.unique(live).size))
-        line_bytes.append(float(per_state[np.where(st >= 0, st, len(per_state) - 1)].sum()))
+        row_idx = np.where(st >= 0, st, len(per_state) - 1)
+        line_bytes.append(float(per_state[row_idx].sum()))
+        for g, tab in dirty_tab.items():
+            dirty[g].append(float(tab[row_idx].sum()))
         keep = k >= warmup and len(recorded) < record_cpu
         if keep:
             raw = run.logits.cpu()
@@ -372,6 +397,7 @@ def _dense_trajectory(args, fsa, B, V, dtype, churn, starts, seed, steps, warmup
         parity &= bool(agree.item()) and torch.equal(run.batch._state.cpu(), pool_ref)
     res["distinct"] = distinct[warmup:]
     res["line_bytes"] = line_bytes[warmup:]
+    res["dirty_bytes"] = {g: v[warmup:] for g, v in dirty.items()}
     res["passes_agree"] = parity
     res["recorded"] = recorded
     res["committed"] = torch.cat(nxt_ref).cpu()  # every step's committed states, in order
@@ -747,10 +773,13 @@ def bench_schema(args) -> dict:
     walk_ms = [ev.elapsed_ms(2 * k, 2 * k + 1) for k in range(args.warmup, n_total)]
     ev.destroy()
     side = _memory_side(r, U, B, V, t_step)
+    side["written_bytes_per_mask_by_granularity"] = {
+        f"{g}B": round(statistics.fmean(v), 1) for g, v in r["dirty_bytes"].items()}
     traffic = _profiled_traffic("dense_fill_schema_b512_v151936.traffic.json", "dense_fill_kernel<2, true>")
     roof = _roofline(side["bytes_per_step_mean"], t_step * 1e-3, traffic=traffic,
                      scope="apply_mask + commit step (one event bracket)",
                      bytes_basis=side["basis"],
+                     written_bytes_per_mask_by_granularity=side["written_bytes_per_mask_by_granularity"],
                      algorithmic_bytes_per_step_mean=side["bytes_per_step_mean"],
                      kernel="dense_fill_kernel<2, true>",
                      mask_kernel=_roofline(statistics.fmean(r["line_bytes"]) + statistics.fmean(U) * V / 8,
@@ -760,10 +789,10 @@ def bench_schema(args) -> dict:
                      survey_formula={"bytes_per_step_mean": round(statistics.fmean(d_step), 1),
                                      "formula": "B*V*2e + U*V*4 + 16*B",
                                      "frac": round(statistics.fmean(d_step) / (t_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                                     "note": ("charges a read and a write of every logit; the mask "
-                                              "kernel reads none and writes only rejected ones, and "
-                                              "rows inside the name string keep most of the "
-                                              "vocabulary, so this figure exceeds the peak and is "
+                                     "note": ("charges a read of every logit besides its write; the "
+                                              "mask kernel reads no logit (FETCH_SIZE: the allow-bit "
+                                              "rows and states) and writes the segments holding "
+                                              "rejected ones, so this figure exceeds the peak and is "
                                               "not a measure of this kernel")})
     return {
         "metric": "µs/step apply_mask+commit, flat JSON-Schema DFA, B=512 V=151936 bf16",

@@ -59,7 +59,7 @@ class FsaTableC(C.Structure):
     _fields_ = [
         ("trans", vp), ("num_states", i32), ("num_symbols", i32), ("dead", i32),
         ("accept", vp), ("live", vp), ("tok_offsets", vp), ("tok_symbols", vp),
-        ("vocab", i64), ("eos_id", i32),
+        ("vocab", i64), ("eos_id", i32), ("trans16", vp), ("tok_records", vp),
     ]
 
 

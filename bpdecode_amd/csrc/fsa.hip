@@ -32,6 +32,10 @@ constexpr int kFsaAdvThreads = 256;
 constexpr int kFsaCommitThreads = 1024;
 constexpr int kFsaCommitPerThread = 4;
 constexpr size_t kFsaCommitLds = 112 * 1024;
+// 16-byte loads of the uint16 table per thread when staging: kFsaStage8 * 8 *
+// kFsaCommitThreads entries, at least the kFsaCommitLds / 2 a staged table holds.
+constexpr int kFsaStage8 = 7;
+static_assert(size_t(kFsaStage8) * 8 * kFsaCommitThreads * 2 >= kFsaCommitLds, "staging loads too few");
 constexpr uint16_t kReject16 = 0xFFFFu;
 
 struct FsaView {
@@ -43,11 +47,17 @@ struct FsaView {
   const uint8_t* sym;
   int64_t V;
   int32_t eos;
+  const uint16_t* trans16;  // optional: live-filtered uint16 table
+  const uint8_t* rec;       // optional: 16-byte token records
 };
 
+// Symbol i (< 16) of a load_syms record: one select between the two 64-bit
+// halves and a shift (a four-way word select with a loop-uniform index was
+// compiled to a scratch store and an indexed scratch load).
 __device__ __forceinline__ int packed_sym(const uint4& p, int i) {
-  const uint32_t w = i < 8 ? (i < 4 ? p.x : p.y) : (i < 12 ? p.z : p.w);
-  return int((w >> (8 * (i & 3))) & 0xFFu);
+  const uint64_t lo = (uint64_t(p.y) << 32) | p.x;
+  const uint64_t hi = (uint64_t(p.w) << 32) | p.z;
+  return int(((i < 8 ? lo : hi) >> (8 * (i & 7))) & 0xFFu);
 }
 
 // The token's first min(len, 16) symbol classes, byte i at bits 8 (i % 4)
@@ -189,13 +199,18 @@ __global__ __launch_bounds__(kFsaAdvThreads) void fsa_advance_kernel(
   next_out[b] = res;
 }
 
-// Commit of up to kFsaCommitThreads * kFsaCommitPerThread rows in one block:
-// each thread reads its rows' slot, state (or the queued value of its slot)
-// and token before the table is staged, so those loads overlap the staging;
-// the queued pool writes land after the walks have read the pool and before
+// Commit of up to kFsaCommitThreads * kFsaCommitPerThread rows in one block.
+// Every global load whose address is known is issued before the first wait:
+// each thread's rows' slot and token, then (InLds) its share of the uint16
+// table (trans16) as 16-byte loads held in registers; then the rows' states
+// and token records (the table goes to LDS while they are in flight).  So
+// the staging costs one memory round trip, and a token's symbols one load.
+// InLds: every walk step is one LDS read of the live-filtered table, whose
+// 0xFFFF entries (outside the table, `dead` or not live) reject; a walk of
+// at least one step that never meets one ends live.  Without the records,
+// the token's offsets and symbols are read as in the other kernels.  The
+// queued pool writes land after the walks have read the pool and before
 // the rows write back -- the order of the calls, as in the dense commit.
-// InLds: the [S, NS] table is copied to LDS as uint16 (entries outside
-// [0, S) read as kReject16) and every walk step is one LDS read.
 template <bool InLds>
 __global__ __launch_bounds__(kFsaCommitThreads) void fsa_advance_block_kernel(
     FsaView f, int32_t* __restrict__ states, const int64_t* __restrict__ slots,
@@ -206,44 +221,89 @@ __global__ __launch_bounds__(kFsaCommitThreads) void fsa_advance_block_kernel(
   __shared__ int64_t pslot[BPD_MAX_FUSED_PENDING];
   __shared__ int32_t pval[BPD_MAX_FUSED_PENDING];
   const int tid = threadIdx.x;
-  for (int32_t i = tid; i < num_pending; i += kFsaCommitThreads) {
-    pslot[i] = pending[i];
-    pval[i] = int32_t(pending[num_pending + i]);
-  }
-  int32_t st[kFsaCommitPerThread];
-  int64_t tk[kFsaCommitPerThread];
-  int64_t slot[kFsaCommitPerThread];
+  int64_t slot[kFsaCommitPerThread], tk[kFsaCommitPerThread];
 #pragma unroll
   for (int i = 0; i < kFsaCommitPerThread; ++i) {
     const int64_t b = int64_t(i) * kFsaCommitThreads + tid;
     slot[i] = -1;
-    st[i] = -1;
     tk[i] = 0;
     if (b < rows) {
       slot[i] = slots ? slots[b] : b;
-      st[i] = states[slot[i]];
       tk[i] = read_token(tokens, tok_dtype, b);
     }
   }
+  const int64_t n = int64_t(f.S) * f.NS;
+  const int64_t n8 = n >> 3;
+  int4 tv[InLds ? kFsaStage8 : 1];
+  uint16_t tail = kReject16;
   if (InLds) {
-    const int64_t n = int64_t(f.S) * f.NS;
-    for (int64_t j = tid; j < n; j += kFsaCommitThreads) {
-      const int32_t v = f.trans[j];
-      tr16[j] = (v >= 0 && v < f.S) ? uint16_t(v) : kReject16;
+    const int4* t8 = reinterpret_cast<const int4*>(f.trans16);
+#pragma unroll
+    for (int k = 0; k < kFsaStage8; ++k) {
+      const int64_t j = int64_t(k) * kFsaCommitThreads + tid;
+      tv[k] = j < n8 ? t8[j] : make_int4(0, 0, 0, 0);
+    }
+    if (tid < n - 8 * n8) tail = f.trans16[8 * n8 + tid];
+  }
+  for (int32_t i = tid; i < num_pending; i += kFsaCommitThreads) {
+    pslot[i] = pending[i];
+    pval[i] = int32_t(pending[num_pending + i]);
+  }
+  int32_t st[kFsaCommitPerThread], b0[kFsaCommitPerThread], len[kFsaCommitPerThread];
+  uint4 pk[kFsaCommitPerThread];
+#pragma unroll
+  for (int i = 0; i < kFsaCommitPerThread; ++i) {
+    st[i] = -1;
+    b0[i] = 0;
+    len[i] = 0;
+    pk[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (slot[i] < 0) continue;
+    st[i] = states[slot[i]];
+    int64_t t = tk[i];
+    if (t < 0) t += f.V;
+    tk[i] = t;
+    if (t >= 0 && t < f.V && t != f.eos) {
+      if (f.rec) {
+        pk[i] = reinterpret_cast<const uint4*>(f.rec)[t];
+      } else {
+        b0[i] = f.off[t];
+        len[i] = f.off[t + 1] - b0[i];
+      }
+    }
+  }
+  if (InLds) {
+    int4* l8 = reinterpret_cast<int4*>(tr16);
+#pragma unroll
+    for (int k = 0; k < kFsaStage8; ++k) {
+      const int64_t j = int64_t(k) * kFsaCommitThreads + tid;
+      if (j < n8) l8[j] = tv[k];
+    }
+    if (tid < n - 8 * n8) tr16[8 * n8 + tid] = tail;
+  }
+  // the symbols: from the record (bytes 0-14, length in byte 15; a longer
+  // token reads the rest through its offset) or from the offsets
+  const int inline_syms = f.rec ? 15 : 16;
+#pragma unroll
+  for (int i = 0; i < kFsaCommitPerThread; ++i) {
+    if (f.rec) {
+      len[i] = int32_t(pk[i].w >> 24);
+      if (len[i] > 15) {
+        b0[i] = f.off[tk[i]];
+        if (len[i] == 255) len[i] = f.off[tk[i] + 1] - b0[i];
+      }
+    } else {
+      pk[i] = load_syms(f.sym + b0[i], len[i]);
     }
   }
   __syncthreads();
-  int32_t nxt[kFsaCommitPerThread];
-#pragma unroll
-  for (int i = 0; i < kFsaCommitPerThread; ++i) {
+  // one row's walk (its symbols passed by value, so they stay in registers)
+  auto walk = [&](int i, const uint4 sy) __attribute__((always_inline)) -> int32_t {
     const int64_t b = int64_t(i) * kFsaCommitThreads + tid;
-    nxt[i] = -1;
-    if (b >= rows) continue;
+    if (b >= rows) return -1;
     int32_t s = st[i];
     for (int32_t k = 0; k < num_pending; ++k)
       if (pslot[k] == slot[i]) s = pval[k];
-    int64_t t = tk[i];
-    if (t < 0) t += f.V;
+    const int64_t t = tk[i];
     int32_t res = -1;
     if (t < 0 || t >= f.V) {
       if (err) atomicOr(err, BPD_FLAG_TOKEN_RANGE);
@@ -252,29 +312,40 @@ __global__ __launch_bounds__(kFsaCommitThreads) void fsa_advance_block_kernel(
     } else if (s >= 0) {
       if (t == f.eos) {
         res = f.accept[s] ? s : -1;
+      } else if (len[i] == 0) {
+        res = f.live[s] ? s : -1;
       } else {
-        const int32_t b0 = f.off[t], len = f.off[t + 1] - b0;
+        const uint8_t* rest = f.sym + b0[i];
         int32_t cur = s;
         bool ok = true;
-        for (int32_t j = 0; j < len && ok; ++j) {
-          const int k = f.sym[b0 + j];
+        for (int32_t j = 0; j < len[i] && ok; ++j) {
+          const int k = j < inline_syms ? packed_sym(sy, j) : int(rest[j]);
           if (k >= f.NS) {
             ok = false;
           } else if (InLds) {
             const uint16_t v = tr16[cur * f.NS + k];
-            ok = v != kReject16 && int32_t(v) != f.dead;
+            ok = v != kReject16;
             cur = v;
           } else {
             cur = f.trans[int64_t(cur) * f.NS + k];
             ok = cur != f.dead && cur >= 0 && cur < f.S;
           }
         }
-        res = ok && f.live[cur] ? cur : -1;
+        if (InLds)
+          res = ok ? cur : -1;  // every state the filtered table names is live
+        else
+          res = ok && f.live[cur] ? cur : -1;
       }
     }
-    nxt[i] = res;
     if (next_out) next_out[b] = res;
-  }
+    return res;
+  };
+  static_assert(kFsaCommitPerThread == 4, "one walk call per row below");
+  int32_t nxt[kFsaCommitPerThread];
+  nxt[0] = walk(0, pk[0]);
+  nxt[1] = walk(1, pk[1]);
+  nxt[2] = walk(2, pk[2]);
+  nxt[3] = walk(3, pk[3]);
   __syncthreads();
   for (int32_t i = tid; i < num_pending; i += kFsaCommitThreads) states[pslot[i]] = pval[i];
   if (!write_back) return;
@@ -326,7 +397,7 @@ int check_fsa(const BpdFsaTable* t) {
 
 FsaView view_of(const BpdFsaTable& t) {
   return FsaView{t.trans, t.num_states, t.num_symbols, t.dead, t.accept, t.live,
-                 t.tok_offsets, t.tok_symbols, t.vocab, t.eos_id};
+                 t.tok_offsets, t.tok_symbols, t.vocab, t.eos_id, t.trans16, t.tok_records};
 }
 
 size_t fsa_lds_bytes(const BpdFsaTable& t) {
@@ -411,10 +482,13 @@ extern "C" int bpd_fsa_advance(const BpdFsaTable* table, int32_t* states, const 
   hipStream_t s = as_stream(stream);
   const FsaView v = view_of(*table);
   if (rows <= int64_t(kFsaCommitThreads) * kFsaCommitPerThread) {
-    const size_t lds = size_t(table->num_states) * size_t(table->num_symbols) * 2;
+    const size_t lds = size_t(table->num_states) * size_t(table->num_symbols) * 2;  // uint16 table
     size_t room = 0;
     if (int rc = commit_lds_room(&room)) return rc;
-    if (table->num_states < 65535 && lds <= kFsaCommitLds && lds <= room)
+    const bool staged = table->trans16 && reinterpret_cast<uintptr_t>(table->trans16) % 16 == 0;
+    BPD_REQUIRE(!table->tok_records || reinterpret_cast<uintptr_t>(table->tok_records) % 16 == 0,
+                "token records must be 16-byte aligned");
+    if (staged && table->num_states < 65535 && lds <= kFsaCommitLds && lds <= room)
       fsa_advance_block_kernel<true><<<1, kFsaCommitThreads, lds, s>>>(
           v, states, slots, pending, int32_t(num_pending), tokens, token_dtype, rows, next_out,
           write_back, err);

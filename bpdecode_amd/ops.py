@@ -196,24 +196,57 @@ class FsaTensors:
         kept with it: symbols whose ``trans`` columns are equal are merged
         into one class (a walk cannot tell them apart), so the table the
         kernels read shrinks to [states, classes]; symbol ids at or above
-        ``num_symbols`` stay invalid (mapped past the last class)."""
+        ``num_symbols`` stay invalid (mapped past the last class).  With it,
+        for the fused commit: the merged table as uint16 with every entry
+        that cannot lead to acceptance (outside the table, ``dead``, or a
+        state off the live set) set to 0xFFFF, and per token a 16-byte record
+        of its first 15 classes and its length."""
         c = self.__dict__.get("_c_fsa")
         if c is None:
-            S, M = self.num_states, self.num_symbols
-            sym8 = _symbols_u8(self)
+            S, M, V = self.num_states, self.num_symbols, self.vocab_size
+            sym8 = _symbols_u8(self).cpu()
             table = self.trans.to("cpu", torch.int32).reshape(S, M)
             cols, cls = torch.unique(table.t().contiguous(), dim=0, return_inverse=True)
-            remap = torch.full((256,), cols.shape[0], dtype=torch.int32)
+            ncls = int(cols.shape[0])
+            remap = torch.full((256,), ncls, dtype=torch.int32)
             remap[:M] = cls.to(torch.int32)
-            trans = cols.t().contiguous().reshape(-1).to(self.device)
-            sym = remap.to(self.device)[sym8.long()].to(torch.uint8)
+            merged = cols.t().contiguous().reshape(-1)
+            sym_cls = remap[sym8.long()].to(torch.uint8)
+            trans = merged.to(self.device)
+            sym = sym_cls.to(self.device)
             offs = _i32(self.offsets)
             acc, live = self.accept.contiguous(), self.live.contiguous()
             eos = self.eos_id if self.eos_id is not None and 0 <= self.eos_id < self.vocab_size else -1
-            c = _lib.FsaTableC(ptr(trans), S, int(cols.shape[0]), self.dead, ptr(acc), ptr(live), ptr(offs),
-                               ptr(sym), self.vocab_size, eos)
+            t16 = rec = None
+            tab = merged.numpy()
+            live_np = live.cpu().numpy().astype(bool)
+            inside = (tab >= 0) & (tab < S)
+            src_live = np.repeat(live_np, ncls)
+            # rejecting at a non-live state mid-walk equals the final live
+            # check only when no non-live state steps to a live one (true of
+            # the reachability set; a caller's other live array keeps the
+            # int32 walk)
+            closed = not np.any(inside & ~src_live & live_np[np.where(inside, tab, 0)])
+            if S < 0xFFFF and closed:
+                ok_state = live_np.copy()
+                ok_state[self.dead] = False
+                keep = inside.copy()
+                keep[keep] = ok_state[tab[keep]]
+                t16 = torch.from_numpy(np.where(keep, tab, 0xFFFF).astype(np.uint16).view(np.int16)).to(self.device)
+            if V:
+                o = self.offsets.to("cpu", torch.int64).numpy()
+                lens = o[1:] - o[:-1]
+                cls_np = sym_cls.numpy()
+                r = np.zeros((V, 16), dtype=np.uint8)
+                for j in range(15):
+                    m = lens > j
+                    r[m, j] = cls_np[o[:-1][m] + j]
+                r[:, 15] = np.minimum(lens, 255)
+                rec = torch.from_numpy(r.reshape(-1)).to(self.device)
+            c = _lib.FsaTableC(ptr(trans), S, ncls, self.dead, ptr(acc), ptr(live), ptr(offs),
+                               ptr(sym), V, eos, ptr(t16), ptr(rec))
             self.__dict__["_c_fsa"] = c
-            self.__dict__["_c_fsa_keep"] = (sym, trans, offs, acc, live)
+            self.__dict__["_c_fsa_keep"] = (sym, trans, offs, acc, live, t16, rec)
         return c
 
     def ensure_allow_bits(self) -> torch.Tensor:

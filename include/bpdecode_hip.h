@@ -161,6 +161,14 @@ typedef struct BpdFsaTable {
   const uint8_t* tok_symbols; /* [tok_offsets[vocab]] */
   int64_t vocab;
   int32_t eos_id;             /* -1: none */
+  /* optional (NULL = none), read by bpd_fsa_advance: `trans` as uint16 with
+   * every entry outside [0, num_states) or naming a state that is not live
+   * set to 0xFFFF (a walk that reaches a non-live state can only end
+   * rejected); needs num_states < 65535 */
+  const uint16_t* trans16;    /* [num_states * num_symbols] */
+  /* optional (NULL = none), read by bpd_fsa_advance: per token 16 bytes,
+   * its first 15 symbol classes (zero padded) and min(length, 255) */
+  const uint8_t* tok_records; /* [vocab * 16] */
 } BpdFsaTable;
 
 /* bpd_fsa_apply_mask: logits[b, t] = neg_inf (checked conversion as in
