@@ -460,6 +460,7 @@ def bench_dense(args) -> dict:
         "two_bracket_us": round(statistics.fmean(two) * 1e3, 3),
         "api_us_per_step": round(statistics.fmean(r["api_ms"]) * 1e3, 3),
         "api_host_us_per_step": round(statistics.fmean(r["api_host_s"]) * 1e6, 2),
+        "api_host_us_per_step_median": round(statistics.median(r["api_host_s"]) * 1e6, 2),
         "row_vocab_entries_per_s": round(B * V / (t_step * 1e-3), 1),
         "distinct_live_states_mean": round(statistics.fmean(U), 2),
         "setup_s": round(setup_s, 3),

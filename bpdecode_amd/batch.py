@@ -168,10 +168,16 @@ class ConstraintBatch:
         self._recycled: list[int] = []  # evicted slots, reused last-in first-out
         self._fresh = 0  # slots [fresh, capacity) were never handed out
         self._version = 0
-        self._ids: list | None = None  # seq ids the cached slot tensor holds
+        self._ids: list | None = None  # seq ids the cached slot list holds
         self._ids_version = -1
         self._slot_vals: list[int] = []
+        # the slot list of _ids on the device: its address, the buffer that
+        # holds it (the upload buffer of a stream, or a tensor of its own)
+        # and, made on first use, a tensor view of it
+        self._slot_ptr = 0
+        self._slot_buf: torch.Tensor | None = None
         self._slot_tensor: torch.Tensor | None = None
+        self._ubufs: dict[int, torch.Tensor] = {}  # stream -> upload buffer (int64)
         # an upload staged by prepare(): (slots, queued-writes tensor, count)
         # and the queued writes it carries (still visible to state_of)
         self._staged: tuple | None = None
@@ -276,18 +282,49 @@ class ConstraintBatch:
             return False
         return self._ids == (seq_ids if type(seq_ids) is list else list(seq_ids))
 
-    def _remember(self, seq_ids: Sequence[Hashable], slot_vals: list[int], tensor: torch.Tensor) -> None:
+    def _upload(self, values: array.array) -> tuple[int, torch.Tensor]:
+        """(device address, buffer) holding ``values`` (int64) after one
+        staged copy on the current stream, into this batch's upload buffer
+        for that stream.  Reusing it is safe: the copy is ordered after every
+        launch already enqueued on the stream, the readers of what it held."""
+        stream = _lib.stream_of(self.device)
+        n = len(values)
+        buf = self._ubufs.get(stream)
+        if buf is None or buf.numel() < n:
+            buf = torch.empty(max(n, self.capacity + 2 * _lib.MAX_FUSED_PENDING), dtype=torch.int64,
+                              device=self.device)
+            self._ubufs[stream] = buf
+        addr, cnt = values.buffer_info()
+        ptr = buf.data_ptr()
+        if cnt:
+            check(lib().bpd_stage_int64(ptr, addr, cnt, stream))
+        return ptr, buf
+
+    def _remember(self, seq_ids: Sequence[Hashable], slot_vals, ptr: int, buf: torch.Tensor | None,
+                  tensor: torch.Tensor | None = None) -> None:
         self._ids = list(seq_ids)
         self._ids_version = self._version
         self._slot_vals = slot_vals
-        self._slot_tensor = tensor
+        self._slot_ptr, self._slot_buf, self._slot_tensor = ptr, buf, tensor
 
-    def _slots(self, seq_ids: Sequence[Hashable]) -> torch.Tensor:
-        """int64 slot per row on the device (uploaded when the ids or the
-        slot map changed)."""
+    def _slot_ptr_of(self, seq_ids: Sequence[Hashable]) -> int:
+        """Device address of the int64 slot list of ``seq_ids`` (uploaded
+        when the ids or the slot map changed)."""
         if not self._same_ids(seq_ids):
             vals = self._lookup(seq_ids)
-            self._remember(seq_ids, vals, index_tensor(vals, self.device))
+            if self.device.type == "cuda":
+                ptr, buf = self._upload(array.array("q", vals))
+                self._remember(seq_ids, vals, ptr, buf)
+            else:
+                t = torch.tensor(vals, dtype=torch.long)
+                self._remember(seq_ids, vals, t.data_ptr(), t, t)
+        return self._slot_ptr
+
+    def _slots(self, seq_ids: Sequence[Hashable]) -> torch.Tensor:
+        """int64 slot per row on the device, as a tensor."""
+        self._slot_ptr_of(seq_ids)
+        if self._slot_tensor is None:
+            self._slot_tensor = self._slot_buf[:len(self._slot_vals)]
         return self._slot_tensor
 
     def _lookup(self, seq_ids: Sequence[Hashable]) -> list | tuple:
@@ -298,12 +335,12 @@ class ConstraintBatch:
         return [self._slot_of[s] for s in seq_ids]
 
     def _slots_fused(self, seq_ids: Sequence[Hashable], fuse: bool):
-        """(slots, pending tensor or None, count) for a device launch.  With
-        ``fuse`` the queued pool writes travel in the slot upload (one pinned
-        copy) and the launch applies them; the caller then calls
-        :meth:`_launched`.  Otherwise they are flushed first.  An upload
-        staged by :meth:`prepare` for the same ids, with nothing queued since,
-        is used as it is."""
+        """(slot address, queued-writes address or None, count) for a
+        device launch.  With ``fuse`` the queued pool writes travel in the
+        slot upload (one pinned copy) and the launch applies them; the caller
+        then calls :meth:`_launched`.  Otherwise they are flushed first.  An
+        upload staged by :meth:`prepare` for the same ids, with nothing
+        queued since, is used as it is."""
         staged = self._staged
         if staged is not None:
             if fuse and not self._pending and self._same_ids(seq_ids):
@@ -311,22 +348,19 @@ class ConstraintBatch:
             self._unstage()
         n = len(self._pending)
         if n == 0:
-            return self._slots(seq_ids), None, 0
+            return self._slot_ptr_of(seq_ids), None, 0
         if not fuse or n > _lib.MAX_FUSED_PENDING or len(seq_ids) == 0:
             self._flush()
-            return self._slots(seq_ids), None, 0
-        if self._same_ids(seq_ids):
-            vals = self._slot_vals
-        else:
-            vals = self._lookup(seq_ids)
+            return self._slot_ptr_of(seq_ids), None, 0
+        vals = self._slot_vals if self._same_ids(seq_ids) else self._lookup(seq_ids)
         B = len(vals)
         # one upload of [slots | queued slots | queued values]
         arr = array.array("q", vals)
         arr.extend(self._pending.keys())
         arr.extend(self._pending.values())
-        dev = _stage(arr, self.device)
-        self._remember(seq_ids, vals, dev[:B])
-        self._staged = (dev[:B], dev[B:], n)
+        ptr, buf = self._upload(arr)
+        self._remember(seq_ids, vals, ptr, buf)
+        self._staged = (ptr, ptr + 8 * B, n)
         self._staged_pending = self._pending
         self._pending = {}
         return self._staged
@@ -360,8 +394,8 @@ class ConstraintBatch:
             ld = logits.stride(0) if B > 1 else self._V
             check(self._f_mask(
                 logits.data_ptr(), code, B, self._V, ld, self._bits_ptr, self._W, self._S,
-                self._pool_ptr, slots.data_ptr(), None if pend is None else pend.data_ptr(), n,
-                float(neg_inf), self._err_ptr, _lib.stream_of(self.device)))
+                self._pool_ptr, slots, pend, n, float(neg_inf), self._err_ptr,
+                _lib.stream_of(self.device)))
             if n:
                 self._launched()
             return logits
@@ -418,15 +452,14 @@ class ConstraintBatch:
             if code is not None:
                 slots, pend, n = self._slots_fused(seq_ids, B <= _COMMIT_FUSED_ROWS)
                 out = torch.empty(B, dtype=torch.int32, device=self.device)
-                pp = None if pend is None else pend.data_ptr()
                 if self._walk_table is None:
                     check(self._f_advance(
-                        self._tn_ptr, self._S, self._V, self._pool_ptr, slots.data_ptr(), pp, n,
+                        self._tn_ptr, self._S, self._V, self._pool_ptr, slots, pend, n,
                         tokens.data_ptr(), code, B, out.data_ptr(), 1, self._err_ptr,
                         _lib.stream_of(self.device)))
                 else:
                     check(self._f_advance(
-                        self._walk_table, self._pool_ptr, slots.data_ptr(), pp, n, tokens.data_ptr(),
+                        self._walk_table, self._pool_ptr, slots, pend, n, tokens.data_ptr(),
                         code, B, out.data_ptr(), 1, self._err_ptr, _lib.stream_of(self.device)))
                 if n:
                     self._launched()

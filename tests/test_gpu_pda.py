@@ -499,34 +499,49 @@ def test_json_bench_trajectory_64_steps(dev, json_case):
 @pytest.mark.timeout(900)
 def test_json_reference_flattening_full_vocab(dev):
     """The reference's own flattening of the recursive JSON grammar (no
-    epsilon reduction: it saturates the 8-config bound) at V = 151,936:
-    saturated config-sets go through the memoised kernel at full size.
-    Masks and raw config words against the C oracle, 8 steps."""
+    epsilon reduction: it saturates the 8-config bound) at V = 151,936, from
+    prefixes drawn as configured (nesting depth uniform over 0-8, 0-200
+    bytes).  That flattening rejects every prefix of depth >= 1 (its
+    saturation drops the config that continues), so the accepted rows are
+    depth-0 documents, every one saturated; eight rows hold the emptied set
+    a rejected prefix leaves.  Masks and raw config words against the C
+    oracle, 16 steps."""
     vocab = synth.serving_vocab(151_936, seed=1)
     comp = CompiledGrammar.build(parse_gbnf(synth.JSON_GBNF))
     g = build_pda_tensors(comp, vocab)  # the default: the reference's flattening
     t = OP.Table(g)
-    V, B = vocab.size, 48
-    _log("case json reference flattening V=151936 B=48 8 steps")
+    V, B, n_empty = vocab.size, 64, 8
+    _log("case json reference flattening V=151936 B=64 16 steps")
     rng = np.random.default_rng(21)
-    rows, saturated = [], 0
-    while len(rows) < B:
+    rows, emptied, deep_rejected = [], [], 0
+    while len(rows) < B - n_empty or len(emptied) < n_empty:
+        d = int(rng.integers(0, 9))
         c = g.init_config()
-        if g.feed(c, synth.json_prefix(rng, int(rng.integers(0, 4)), max_len=60)):
-            rows.append(c)
-    start = torch.stack(rows)
+        if g.feed(c, synth.json_prefix(rng, d, max_len=200)):
+            if len(rows) < B - n_empty:
+                rows.append(c)
+        else:
+            deep_rejected += d >= 1
+            if len(emptied) < n_empty and d >= 1:
+                emptied.append(c)
+    assert deep_rejected > 0 and all(int(c[0]) == 0 for c in emptied)
+    start = torch.stack(rows + emptied)
     gd = g.to(dev)
     pool = start.to(dev)
     mirror = start.numpy().copy()
     gen = torch.Generator(device=dev).manual_seed(22)
     threads = _oracle_threads()
-    for step in range(8):
+    saturated = 0
+    for step in range(16):
         saturated += int((mirror[:, 1] != 0).sum())
         bits = OP.compute_mask_threads(t, mirror, threads)
         got = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
         assert np.array_equal(got, bits), step
+        assert not bits[B - n_empty:].any(), step  # an emptied set allows nothing
+        allowed = _unpack_allowed(bits, V, dev)
         lg = torch.randn((B, V), generator=gen, device=dev)
-        want = lg.masked_fill(~_unpack_allowed(bits, V, dev), float("-inf"))
+        want = lg.masked_fill(~allowed, float("-inf"))
+        want[~allowed.any(dim=1)] = 0.0  # rows with nothing allowed sample anything (rejected)
         toks = torch.multinomial(torch.softmax(want, dim=-1), 1, generator=gen).view(-1).to(torch.int32)
         ok, _ = pda_step(pool, gd, toks)
         ok_o = OP.advance(t, mirror, toks.cpu().numpy())

@@ -132,30 +132,43 @@ def test_prior_unaligned_vocab(dev):
     assert torch.equal(w[:, V:].cpu(), wide[:, V:])
 
 
+@pytest.fixture(scope="module")
+def email_serving():
+    """B=128, V=151,936, k=4 over the email DFA, logits N(0, 3),
+    rows at random reachable states; the float64 oracle of every row,
+    computed once with the rows split over host threads (numpy releases the
+    interpreter lock in its array loops)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    vocab = synth.serving_vocab(151_936, seed=1)
+    fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
+    tn = fsa.tok_next.numpy()
+    st = synth.random_walk_states(fsa.tok_next, fsa.start, fsa.eos_id, 128, 40, seed=5).to(torch.int32)
+    x = synth.logits(128, tn.shape[1], std=3.0, dtype=torch.float32, seed=11)
+    xd = x.double().numpy()
+    live, acc, stn = fsa.live.numpy(), fsa.accept.numpy(), st.numpy()
+    with ThreadPoolExecutor(16) as ex:
+        rows = list(ex.map(lambda b: OS.prior_lookahead(xd[b:b + 1], tn, live, acc, fsa.eos_id,
+                                                         stn[b:b + 1], 4, 1.0), range(128)))
+    return fsa, st, x, np.concatenate(rows)
+
+
 @pytest.mark.parametrize("stats", ["list", "wave", "members", "classes"])
-def test_prior_email_serving(dev, stats, monkeypatch):
-    """B=128, V=151,936, k=4 over the email DFA: four rows against the
-    oracle, every row against the alpha-free identity (alpha = 0 leaves
+def test_prior_email_serving(dev, stats, monkeypatch, email_serving):
+    """B=128, V=151,936, k=4 over the email DFA: every row against the
+    float64 oracle and against the alpha-free identity (alpha = 0 leaves
     log_softmax on tokens whose k-1 lookahead is finite); class statistics
     with wave shifts over 8192-token chunks from the chunk member lists (and
     the member-list output pass) or from the class map, and over
     4096-token chunks from the member lists and from the class map."""
     monkeypatch.setenv("BPD_SOFT_STATS", stats)
-    vocab = synth.serving_vocab(151_936, seed=1)
-    fsa = FsaTensors.build(synth.EMAIL, vocab).densify()
-    tn = fsa.tok_next.numpy()
-    S, V = tn.shape
-    st = synth.random_walk_states(fsa.tok_next, fsa.start, fsa.eos_id, 128, 40, seed=5).to(torch.int32)
-    x = synth.logits(128, V, std=3.0, dtype=torch.float32, seed=11)
+    fsa, st, x, want = email_serving
     fd = fsa.to(dev)
     assert fd.ensure_soft_classes().chunk_cap in (256, 512, 1024)
     got = x.to(dev)
     ops.apply_soft_prior_(got, fd, st.to(dev), 4, 1.0)
     got = got.cpu().double().numpy()
-    rows = list(range(0, 128, 32))
-    want = OS.prior_lookahead(x[rows].double().numpy(), tn, fsa.live.numpy(), fsa.accept.numpy(),
-                              fsa.eos_id, st[rows].numpy(), 4, 1.0)
-    assert close(got[rows], want)
+    assert close(got, want)
     zero = x.to(dev)
     ops.apply_soft_prior_(zero, fd, st.to(dev), 4, 0.0)
     ls = torch.log_softmax(x.double(), dim=1).numpy()
