@@ -1812,8 +1812,32 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   int32_t* cfg = a.configs + row * kConfigWords;
   int32_t* x = bufs[0];
   int32_t* y = bufs[1];
-  if (threadIdx.x < kWave)
+  // the reads wave 0 needs after the table is staged -- the token, its
+  // offsets and first 64 bytes, the workspace stamps, the pool's set 0 --
+  // are issued before the staging loads, so their round trips overlap them
+  const int64_t t = read_token(a.tokens, a.tok_dtype, b);
+  const bool t_in = t >= 0 && t < a.vocab;
+  const bool walk_tok = t_in && t != a.eos;
+  const int32_t s = walk_tok ? a.tok_off[t] : 0, e = walk_tok ? a.tok_off[t + 1] : 0;
+  int32_t meta[4] = {0, 0, 0, 0};
+  uint32_t hdr = 0;
+  int32_t p0[kSetLoads];
+  const int32_t* pool = ws.pool ? ws.pool + b * kMemoSets * kConfigWords : nullptr;
+  if (threadIdx.x < kWave) {
     for (int k = lane; k < kConfigWords; k += kWave) x[k] = cfg[k];
+    if (pool) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) meta[q] = ws.meta[b * 4 + q];
+      hdr = ws.header[0];
+#pragma unroll
+      for (int q = 0; q < kSetLoads; ++q) {
+        const int k = lane + q * kWave;
+        p0[q] = k < kConfigWords ? pool[k] : 0;
+      }
+    }
+  }
+  // the token's first 64 bytes, one per lane
+  const int32_t bl = threadIdx.x < kWave && s + lane < e ? int32_t(a.tok_bytes[s + lane]) : 0;
   {
     const uint4* src = reinterpret_cast<const uint4*>(ws.table + b * (kMemoSets * 64));
     uint4 v[kMemoSets * 16 / kCommitThreads];
@@ -1825,9 +1849,8 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   const PdaTableView& g = a.g;
   __syncthreads();
   if (threadIdx.x >= kWave) return;
-  const int64_t t = read_token(a.tokens, a.tok_dtype, b);
   bool ok;
-  if (t < 0 || t >= a.vocab) {
+  if (!t_in) {
     if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
     ok = false;
   } else if (!config_ok(x, a.g.num_states, lane)) {
@@ -1836,11 +1859,8 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   } else if (t == a.eos) {
     ok = is_complete(g, ConstFlatView{x});
   } else {
-    const int32_t s = a.tok_off[t], e = a.tok_off[t + 1];
     ok = true;
     if (s < e) {
-      // the token's first 64 bytes, one per lane
-      const int32_t bl = s + lane < e ? int32_t(a.tok_bytes[s + lane]) : 0;
       auto byte_at = [&](int32_t i) -> int {
         return i - s < kWave ? __shfl(bl, int(i - s)) : int(a.tok_bytes[i]);
       };
@@ -1852,10 +1872,21 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
       int cur = -1, prev = -1;  // -1: no usable table, step every byte from the row's set
       bool exact = false;
       int32_t i = s;
-      const int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
-      if (ws.pool && ws.meta[b * 4] == 1 && ws.meta[b * 4 + 1] == int32_t(uint32_t(tag)) &&
-          ws.meta[b * 4 + 2] == int32_t(uint32_t(tag >> 32)) &&
-          uint32_t(ws.meta[b * 4 + 3]) == ws.header[0] && coop_same(x, pool, lane)) {
+      bool same0 = false;
+      if (pool && meta[0] == 1 && meta[1] == int32_t(uint32_t(tag)) && meta[2] == int32_t(uint32_t(tag >> 32)) &&
+          uint32_t(meta[3]) == hdr) {
+        // set 0 of the pool against the row's set (coop_same with the pool's
+        // words already in registers)
+        int32_t* p0l = y;
+#pragma unroll
+        for (int q = 0; q < kSetLoads; ++q) {
+          const int k = lane + q * kWave;
+          if (k < kConfigWords) p0l[k] = p0[q];
+        }
+        wave_sync();
+        same0 = coop_same(x, p0l, lane);
+      }
+      if (same0) {
         const uint8_t* T = reinterpret_cast<const uint8_t*>(trow);
         cur = 0;
         for (; i < e; ++i) {
