@@ -208,12 +208,14 @@ struct MemoWs {
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Entries of each of a row's two queue buffers: the whole vocab up to 4096
-// tokens, a quarter of it above (a row that pauses more tokens in one pass
-// starts again in tile mode).  The bench rows pause at most 2,692 of 151,936
-// tokens in their first pass.
+// tokens, a quarter of it above, at most kQueueMax (a row that pauses more
+// tokens in one pass starts again in tile mode).  The bench rows pause at
+// most 2,692 of 151,936 tokens in their first pass; at kQueueMax the
+// buffers take 256 KB of a row's workspace instead of 608 KB at V/4.
+constexpr int64_t kQueueMax = 16384;
 int32_t queue_cap(int64_t vocab) {
   const int64_t v = vocab > 0 ? vocab : 0;
-  int64_t cap = v <= 4096 ? v : (v + 3) / 4;
+  int64_t cap = v <= 4096 ? v : std::min<int64_t>((v + 3) / 4, kQueueMax);
   // BPD_PDA_QUEUE_CAP lowers it (tests of the full-queue path; read by the
   // workspace size and the launch alike)
   if (const char* e = std::getenv("BPD_PDA_QUEUE_CAP")) {

@@ -72,7 +72,11 @@ def test_toy_every_state(dev, pattern, dtype, nondense_path):
 
 
 def test_flat_schema_serving_scale(dev, monkeypatch):
-    _log("case fsa walk flat-schema DFA V=151936 B=256 bf16")
+    """The flat JSON-Schema DFA at serving scale (826 states, V = 151,936,
+    B = 256, bf16) on the walking kernels (no allow-bit table): one mask,
+    packed bits and commit against the oracle, then eight mask + commit
+    steps through ConstraintBatch."""
+    _log("case fsa walk flat-schema DFA V=151936 B=256 bf16, 9 steps")
     monkeypatch.setattr(ops, "ALLOW_BITS_LIMIT", 0)  # the walking kernels
     vocab = synth.serving_vocab(151_936, seed=1)
     comp = CompiledGrammar.build(json_schema_to_grammar(synth.FLAT_SCHEMA))
@@ -103,6 +107,32 @@ def test_flat_schema_serving_scale(dev, monkeypatch):
                              generator=torch.Generator().manual_seed(2)).view(-1)
     nxt = ops.advance_state(fd, starts.to(dev), toks.to(dev))
     assert nxt.cpu().tolist() == OD.advance(tn, st, toks.numpy()).tolist()
+    # eight more steps through ConstraintBatch on the walking kernels: the
+    # mask against ATen's masked_fill_ over the oracle-checked table, the
+    # commit against the oracle's advance
+    batch = ConstraintBatch(fd, capacity=256, device=dev)
+    assert not batch._fast
+    ids = list(range(256))
+    for i in ids:
+        batch.add(i)
+    batch._state[:256] = nxt
+    st = nxt.cpu().numpy()
+    gen = torch.Generator(device=dev).manual_seed(3)
+    for step in range(8):
+        lg = torch.randn((256, vocab.size), generator=gen, device=dev).mul_(3.0).to(torch.bfloat16)
+        s_ = torch.from_numpy(st).to(dev).long()
+        rejected = (tn_dev.index_select(0, s_.clamp(min=0)) == -1) | (s_ < 0)[:, None]
+        want = lg.clone().masked_fill_(rejected, float("-inf"))
+        got = lg.clone()
+        batch.apply_mask(ids, got)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        finite = torch.isfinite(want.float()).any(dim=1)
+        probs = torch.softmax(torch.where(finite[:, None], want.float(), torch.zeros_like(want.float())), dim=-1)
+        toks = torch.multinomial(probs, 1, generator=gen).view(-1)
+        nxt = batch.commit(ids, toks)
+        st = OD.advance(tn, st, toks.cpu().numpy())
+        assert nxt.cpu().numpy().tolist() == st.tolist(), step
+    batch.check_errors()
 
 
 def test_batch_churn_and_range_flags(dev, nondense_path):
@@ -235,3 +265,64 @@ def test_flat_schema_auto_mode_churn_64_steps(dev):
     batch.check_errors()
     pool = batch._state.cpu().numpy()
     assert all(pool[batch._slot_of[i]] == s for i, s in state.items())
+
+
+@pytest.mark.parametrize("rows", [3000, 5000])
+def test_fused_walking_commit_large_batches(dev, rows):
+    """bpd_fsa_advance at 3,000 rows (one fused launch: four rows per
+    thread, queued writes applied) and 5,000 rows (the gather and scatter
+    launches, no queued writes) against the oracle's advance."""
+    _log(f"case fsa commit rows={rows}")
+    vocab = synth.serving_vocab(8192, seed=3)
+    f = FsaTensors.build(synth.EMAIL, vocab, dense=False)
+    tn = oracle_table(f)
+    S, V = tn.shape
+    fd = f.to(dev)
+    rng = np.random.default_rng(rows)
+    st = rng.integers(-2, S, size=rows).astype(np.int32)
+    toks = rng.integers(-V, V, size=rows).astype(np.int64)
+    pool = torch.from_numpy(st.copy()).to(dev)
+    slots = torch.from_numpy(rng.permutation(rows).astype(np.int64)).to(dev)
+    want_st = st[slots.cpu().numpy()]
+    pending = None
+    if rows <= 4096:  # queued writes: 40 slots get a new value first
+        qs = rng.choice(rows, size=40, replace=False).astype(np.int64)
+        qv = rng.integers(0, S, size=40).astype(np.int64)
+        pending = torch.from_numpy(np.concatenate([qs, qv])).to(dev)
+        pool_after = st.copy()
+        pool_after[qs] = qv
+        want_st = pool_after[slots.cpu().numpy()]
+    nxt = ops.fsa_advance(fd, pool, torch.from_numpy(toks).to(dev), slots=slots, write_back=True,
+                          pending=pending)
+    want = OD.advance(tn, want_st, toks)
+    assert nxt.cpu().numpy().tolist() == want.tolist()
+    expect_pool = (pool_after if pending is not None else st).copy()
+    expect_pool[slots.cpu().numpy()] = want
+    assert np.array_equal(pool.cpu().numpy(), expect_pool)
+
+
+def test_walking_commit_with_a_live_array_not_closed(dev):
+    """A caller's live array that is not closed under successors (a state
+    marked non-live although it steps to a live one): the bundle keeps no
+    filtered uint16 table, and the commit walks the int32 table with the
+    final live check of mask_cpu.cpp:53-71 -- against the oracle's table
+    built with the same live array."""
+    _log("case fsa commit, live array not closed")
+    f = FsaTensors.build("ab|c|a+1", TOY_VOCAB, dense=False)
+    S = f.num_states
+    tr = f.trans.reshape(S, f.num_symbols)
+    live = f.live.clone()
+    src = next(s for s in range(S) if s != f.dead and live[s] and any(
+        0 <= int(v) < S and bool(live[int(v)]) for v in tr[s]))
+    live[src] = 0
+    g = FsaTensors(f.trans, f.accept, live, f.num_symbols, f.dead, f.offsets, f.symbols, f.eos_id,
+                   f.start, f.accepting)
+    gd = g.to(dev)
+    assert not gd.c_fsa_table().trans16
+    tn = OD.build_token_transitions(g.trans.numpy(), g.accept.numpy(), live.numpy(), g.num_symbols,
+                                    g.offsets.numpy(), g.symbols.numpy(), g.eos_id)
+    V = g.vocab_size
+    st = np.array([s for s in range(S) for _ in range(V)], dtype=np.int32)
+    toks = np.array([t for _ in range(S) for t in range(V)], dtype=np.int64)
+    nxt = ops.advance_state(gd, torch.from_numpy(st).to(dev), torch.from_numpy(toks).to(dev))
+    assert nxt.cpu().numpy().tolist() == tn[st, toks].tolist()
