@@ -178,8 +178,9 @@ class ConstraintBatch:
         self._slot_buf: torch.Tensor | None = None
         self._slot_tensor: torch.Tensor | None = None
         self._ubufs: dict[int, torch.Tensor] = {}  # stream -> upload buffer (int64)
-        # an upload staged by prepare(): (slots, queued-writes tensor, count)
-        # and the queued writes it carries (still visible to state_of)
+        # an upload staged by prepare(): (slot list address, queued-writes
+        # address, count) and the queued writes it carries (still visible to
+        # state_of)
         self._staged: tuple | None = None
         self._staged_pending: dict[int, int] = {}
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device) if self.device.type == "cuda" else None
