@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
 // by the direct-walk kernel (pda_mask_kernel filtered to flagged rows).
 constexpr int kMemoThreads = 1024;
 constexpr int kMemoSets = 128;
-constexpr int kMemoReq = 256;
+constexpr int kMemoReq = 128;
 constexpr int kMemoTok = 4;
 constexpr int kMemoMaxVocab = 262144;  // verdict bitmap of a row in LDS
 constexpr uint8_t kTUnknown = 0xFE;
@@ -189,6 +189,57 @@ constexpr uint8_t kTExact = 0x80;
 // the depth of the list's common stack starts
 constexpr int kListBase = 17;
 constexpr int kMemoIds = 125;
+// List states of the row-wide walk.  A set that is in a frame list is walked
+// through the lists' byte table (BpdPdaFrames::trans) without interning the
+// sets it reaches: the walk state is kListState | anchor << 13 | sat << 12 |
+// list, where `anchor` is the pool set whose common stack the list sits on
+// (every list reached from it sits on the same stack) and `sat` the
+// saturation flag.  Only a boundary byte (trans -2: the step needs the
+// stack) makes a set with words: the boundary table LT, keyed by
+// (anchor, sat, list, byte), holds the pool set it leads to.
+constexpr int kListState = 1 << 20;
+constexpr int kLT = 512;                 // boundary entries of a row (LDS hash table)
+constexpr uint32_t kLTEmpty = 0xFFFFFFFFu;
+constexpr int kReqLT = 1 << 30;          // request list: boundary entry `slot` (else set << 8 | byte)
+// Direct-mapped LDS cache of the lists' byte table (global, 1 KB per list):
+// word = list << 21 | byte << 13 | code, code 0x1FFF empties (-1), 0x1FFE
+// boundary (-2), else sat << 11 | list reached (list ids < 2048); an empty
+// slot (all ones) names list 2047, which no table has.  One 32-bit word per
+// entry, so a reader sees a whole entry whichever thread wrote it last.
+constexpr int kLC = 1024;
+static_assert(BPD_PDA_MAX_FRAME_LISTS < 2047, "list ids of the byte-table cache are 11 bits");
+
+__device__ __forceinline__ int list_code(const BpdPdaFrames& f, uint32_t* lcache, int l, int byte) {
+  const uint32_t tag = (uint32_t(l) << 21) | (uint32_t(byte) << 13);
+  const int slot = int((uint32_t(l) * 37u + uint32_t(byte) * 11u) & uint32_t(kLC - 1));
+  const uint32_t w = lcache[slot];
+  if ((w & ~0x1FFFu) == tag) {
+    const uint32_t c = w & 0x1FFFu;
+    return c == 0x1FFFu ? -1 : c == 0x1FFEu ? -2 : int((c & 0x7FFu) | ((c & 0x800u) != 0u ? BPD_PDA_FRAME_SAT : 0));
+  }
+  const int code = f.trans[l * 256 + byte];
+  const uint32_t c = code == -1 ? 0x1FFFu
+                     : code < 0 ? 0x1FFEu
+                                : (uint32_t(code & 0x7FF) | ((code & BPD_PDA_FRAME_SAT) != 0 ? 0x800u : 0u));
+  lcache[slot] = tag | c;
+  return code;
+}
+
+__device__ __forceinline__ bool walking(int cur) { return cur < 256 || cur >= kListState; }
+__device__ __forceinline__ int list_state(int anchor, int sl) {
+  // sl: the anchor's frame-list word (list | saturation flag | base << kListBase)
+  return kListState | (anchor << 13) | ((sl & BPD_PDA_FRAME_SAT) != 0 ? 1 << 12 : 0) | (sl & 0xFFF);
+}
+// key of a boundary entry: anchor << 21 | sat << 20 | list << 8 | byte
+__device__ __forceinline__ uint32_t lt_key_of(int cur, int byte) {
+  return (uint32_t(cur - kListState) << 8) | uint32_t(byte);
+}
+__device__ __forceinline__ uint32_t lt_hash(uint32_t key) {
+  key ^= key >> 15;
+  key *= 0x2C1B3C6Du;
+  key ^= key >> 12;
+  return key;
+}
 
 struct MemoWs {
   uint32_t* header;   // [64]: word 0 = generation of the last mask launch on this workspace,
@@ -203,6 +254,9 @@ struct MemoWs {
   int2* tmeta;        // [vocab] (token id, length) of the token at walk position k
   uint2* queue;       // [rows, 2, qcap] paused tokens of the row-wide walk (two buffers)
   int32_t qcap;       // entries per queue buffer (queue_cap)
+  uint2* lt;          // [rows, kLT]: the row's boundary table after the mask (key, entry;
+                      // entry | kTExact where the step's raw words are the set's)
+  int32_t* slist;     // [rows, kMemoSets]: frame-list word of each interned set (-1: none)
 };
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
@@ -229,7 +283,8 @@ size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
   return 256 + sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
-         v * sizeof(int2) + r * 2 * size_t(queue_cap(vocab)) * sizeof(uint2);
+         v * sizeof(int2) + r * 2 * size_t(queue_cap(vocab)) * sizeof(uint2) + r * kLT * sizeof(uint2) +
+         r * kMemoSets * sizeof(int32_t);
 }
 
 MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
@@ -250,6 +305,10 @@ MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   p += size_t(vocab) * sizeof(int2);
   w.queue = reinterpret_cast<uint2*>(p);
   w.qcap = queue_cap(vocab);
+  p += r * 2 * size_t(w.qcap) * sizeof(uint2);
+  w.lt = reinterpret_cast<uint2*>(p);
+  p += r * kLT * sizeof(uint2);
+  w.slist = reinterpret_cast<int32_t*>(p);
   return w;
 }
 
@@ -864,7 +923,13 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   // frame list of a new set: l | BPD_PDA_FRAME_SAT (the set's saturation
   // flag) | base << kListBase (the depth of its common stack), -1 none
   __shared__ int32_t cand_list[kMemoReq];
-  __shared__ int32_t set_list[kMemoSets];  // the same for the interned sets, without the flag
+  __shared__ int32_t set_list[kMemoSets];  // the same for the interned sets
+  __shared__ int32_t set_ls[kMemoSets];    // list state a walk takes at the set, -1 none
+  __shared__ uint32_t lt_key[kLT];         // boundary table: keys (kLTEmpty: free slot)
+  __shared__ uint8_t lt_res[kLT];          // ... and entries (pool id, kTDead, kTOverflow, kTUnknown)
+  __shared__ uint32_t lt_req[kLT / 32];    // requested boundary entries
+  __shared__ uint32_t lt_exact[kLT / 32];  // entries whose step gives the set's raw words
+  __shared__ uint32_t lcache[kLC];         // entries of the lists' byte table met so far
   __shared__ uint8_t cand_comp[kMemoReq];  // composed from a list's key: raw words unknown
   __shared__ uint32_t fslots[BPD_PDA_FRAME_SLOTS];  // the frame lists' slot table
   __shared__ int32_t cand_id[kMemoReq];
@@ -904,11 +969,39 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     req[i] = 0;
     texact[i] = 0;
   }
+  for (int i = tid; i < kLT; i += kMemoThreads) {
+    lt_key[i] = kLTEmpty;
+    lt_res[i] = kTUnknown;
+    if (i < kLT / 32) {
+      lt_req[i] = 0u;
+      lt_exact[i] = 0u;
+    }
+  }
+  for (int i = tid; i < kLC; i += kMemoThreads) lcache[i] = 0xFFFFFFFFu;
   if (tid == 0) {
     pool_count = 1;
     overflowed = 0;
   }
   __syncthreads();
+  if (tid >= kWave && tid < 2 * kWave) {
+    // wave 1: the row's frame list and the entries of T row 0 it fills (the
+    // dead entries it writes are ones wave 0 writes too: a byte no top's
+    // edge contains empties the list)
+    const int lane = tid - kWave;
+    const bool dead = (a.broken != nullptr && a.broken[row] != 0) || !config_ok(row_cfg, a.g.num_states, lane);
+    int base0 = 0;
+    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, lane, &base0);
+    if (lane == 0) {
+      row_list = l0;
+      const int sl0 = l0 >= 0 ? (l0 | (row_cfg[1] != 0 ? BPD_PDA_FRAME_SAT : 0) | (base0 << kListBase)) : -1;
+      set_list[0] = sl0;
+      set_ls[0] = sl0 >= 0 ? list_state(0, sl0) : -1;
+    }
+    if (l0 >= 0) {
+      wave_sync();
+      frame_fill_row(a.frames, l0, row_cfg[1] != 0, 0, T, lane);
+    }
+  }
   if (tid < kWave) {
     bool dead = a.broken != nullptr && a.broken[row] != 0;
     if (!config_ok(row_cfg, a.g.num_states, tid)) {
@@ -930,16 +1023,6 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     wave_sync();
     coop_set_intervals(g, set_tops[0], set_n[0], set_bnd[0], set_hit[0], T, tid);
-    int base0 = 0;
-    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, tid, &base0);
-    if (tid == 0) {
-      row_list = l0;
-      set_list[0] = l0 >= 0 ? (l0 | (base0 << kListBase)) : -1;
-    }
-    if (l0 >= 0) {
-      wave_sync();
-      frame_fill_row(a.frames, l0, row_cfg[1] != 0, 0, T, tid);
-    }
   }
   for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
   __syncthreads();
@@ -948,22 +1031,27 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 
   const int64_t V = a.vocab;
 
-  // Resolve the requested transitions: compact the request bits, claim one
-  // request per elementary interval, compute each claimed transition (one
-  // wave each), intern the new sets and fill T; sets `overflowed` when the
-  // pool is full.  Called by every thread, between barriers.
+  // Resolve the requested transitions: compact the request bits (T entries,
+  // then boundary entries), claim one request per elementary interval,
+  // compute each claimed transition (one wave each), intern the new sets and
+  // fill T and LT; sets `overflowed` when the pool is full.  A request beyond
+  // the first kMemoReq stays unresolved and its token asks again after the
+  // next walk.  Called by every thread, between barriers.
   auto resolve = [&]() {
     if (tid == 0) nreq = 0;
     __syncthreads();
-    for (int w = tid; w < kMemoSets * 8; w += kMemoThreads) {
-      uint32_t bits = req[w];
+    for (int w = tid; w < kMemoSets * 8 + kLT / 32; w += kMemoThreads) {
+      const bool lt = w >= kMemoSets * 8;
+      uint32_t* word = lt ? &lt_req[w - kMemoSets * 8] : &req[w];
+      uint32_t bits = *word;
       if (bits) {
-        req[w] = 0;
+        *word = 0;
         int at = atomicAdd(&nreq, __popc(bits));
         while (bits) {
           const int bit = __ffs(bits) - 1;
           bits &= bits - 1;
-          if (at < kMemoReq) req_list[at] = ((w >> 3) << 8) | ((w & 7) * 32 + bit);
+          if (at < kMemoReq)
+            req_list[at] = lt ? (kReqLT | ((w - kMemoSets * 8) * 32 + bit)) : (((w >> 3) << 8) | ((w & 7) * 32 + bit));
           ++at;
         }
       }
@@ -978,8 +1066,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       bool cheap = true;
       if (tid < n) {
         entry = uint32_t(req_list[tid]);
-        const int sl = set_list[entry >> 8];
-        cheap = sl >= 0 && a.frames.trans[(sl & (BPD_PDA_FRAME_SAT - 1)) * 256 + int(entry & 255u)] != -2;
+        if (entry >= uint32_t(kReqLT)) {
+          cheap = false;  // a boundary entry: always stepped
+        } else {
+          const int sl = set_list[entry >> 8];
+          cheap = sl >= 0 && a.frames.trans[(sl & (BPD_PDA_FRAME_SAT - 1)) * 256 + int(entry & 255u)] != -2;
+        }
       }
       if (tid == 0) {
         n_stepped = 0;
@@ -993,7 +1085,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (tid < n) req_list[slot] = int32_t(entry);
       __syncthreads();
     }
-    if (tid < n) {
+    if (tid < n && req_list[tid] >= kReqLT) {
+      cand_lo[tid] = 0;
+      cand_hi[tid] = 0;
+      cand_res[tid] = 0;  // a boundary entry has its own slot: always computed
+    } else if (tid < n) {
       // every byte of the request's elementary interval [lo, hi] shares
       // its result: the first request of an interval computes it and
       // fills the whole interval
@@ -1023,9 +1119,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         while (r < n && cand_res[r] < -3) r += kMemoThreads / kWave;
         return r;
       };
+      // the pool set a request starts from (a boundary entry: its anchor)
+      auto req_set = [&](int r) -> int {
+        const int e = req_list[r];
+        return e >= kReqLT ? int(lt_key[e & (kLT - 1)] >> 21) : e >> 8;
+      };
       int32_t words[kSetLoads];
       auto load_src = [&](int r) {
-        const int set = r < n ? req_list[r] >> 8 : 0;
+        const int set = r < n ? req_set(r) : 0;
         const int32_t* ps = pool + set * kConfigWords;
 #pragma unroll
         for (int q = 0; q < kSetLoads; ++q) {
@@ -1036,7 +1137,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       int r = next_req(wave);
       load_src(r);
       while (r < n) {
-        const int set = req_list[r] >> 8, byte = req_list[r] & 255;
+        const int e = req_list[r];
+        const bool lt = e >= kReqLT;
+        const uint32_t lk = lt ? lt_key[e & (kLT - 1)] : 0u;
+        const int set = lt ? int(lk >> 21) : e >> 8, byte = lt ? int(lk & 255u) : e & 255;
         if (set != 0) {
 #pragma unroll
           for (int q = 0; q < kSetLoads; ++q) {
@@ -1052,7 +1156,16 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         // key instead of stepped
         const int32_t* src = set != 0 ? wsrc : row_cfg;
         const int sl = set_list[set];
-        const int code = sl >= 0 ? a.frames.trans[(sl & (BPD_PDA_FRAME_SAT - 1)) * 256 + byte] : -3;
+        int code = -3;
+        if (lt) {
+          // a boundary entry steps the list state's set: the anchor's
+          // common stack under the list's key
+          compose_list_set(src, wsrc, a.frames.keys + int64_t((lk >> 8) & 0xFFFu) * BPD_PDA_FRAME_KEY_WORDS,
+                           sl >> kListBase, int((lk >> 20) & 1u), lane);
+          src = wsrc;
+        } else if (sl >= 0) {
+          code = a.frames.trans[(sl & (BPD_PDA_FRAME_SAT - 1)) * 256 + byte];
+        }
         bool ok;
         if (code >= 0) {
           const int sat = src[1] != 0 || (code & BPD_PDA_FRAME_SAT) != 0 ? 1 : 0;
@@ -1142,7 +1255,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       if (id < max_sets) {
         pool_hash[id] = cand_hash[tid];
         set_n[id] = cand_n[tid];
-        set_list[id] = cand_list[tid] >= 0 ? (cand_list[tid] & ~BPD_PDA_FRAME_SAT) : -1;
+        const int cl = cand_list[tid];
+        set_list[id] = cl;
+        set_ls[id] = cl >= 0 ? list_state(id, cl) : -1;
         for (int i = 0; i < kMaxConfigs; ++i) set_tops[id][i] = cand_tops[tid][i];
         cand_id[tid] = id;
       } else {
@@ -1157,7 +1272,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       for (int r = wave; r < n; r += kMemoThreads / kWave) {
         const int res = cand_res[r];
         if (res == -4) continue;  // a duplicate of another request's interval
-        const int set = req_list[r] >> 8;
+        const int rq = req_list[r];
         const int id = res == -2 ? cand_id[cand_lead[r]] : res;
         uint8_t e;
         if (id == -1 || id == -5) {
@@ -1168,6 +1283,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         } else {
           e = uint8_t(id);
         }
+        if (rq >= kReqLT) {
+          // a boundary entry: its slot of LT (exact as below; never composed)
+          if (lane == 0) {
+            const int slot = rq & (kLT - 1);
+            lt_res[slot] = e;
+            if ((res >= 0 && cand_exact[r]) || (res == -2 && cand_lead[r] == r && id >= 0))
+              atomicOr(&lt_exact[slot >> 5], 1u << (slot & 31));
+          }
+          continue;
+        }
+        const int set = rq >> 8;
         const int lo = cand_lo[r], hi = cand_hi[r];
         for (int c = lo + lane; c <= hi; c += kWave) T[set * 256 + c] = e;
         // the interval's step gives the set's raw words: a new set (its
@@ -1211,10 +1337,18 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     __syncthreads();
   };
 
-  // Empty the pool back to the row's own set (set 0) and T to "unknown".
+  // Empty the pool back to the row's own set (set 0), T to "unknown" and LT.
   auto reset_pool = [&]() {
     for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
     for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) texact[i] = 0u;
+    for (int i = tid; i < kLT; i += kMemoThreads) {
+      lt_key[i] = kLTEmpty;
+      lt_res[i] = kTUnknown;
+      if (i < kLT / 32) {
+        lt_req[i] = 0u;
+        lt_exact[i] = 0u;
+      }
+    }
     for (int k = tid; k < kConfigWords; k += kMemoThreads) pool[k] = row_cfg[k];
     if (tid < kMaxConfigs) {
       const int n0 = row_cfg[0];
@@ -1268,25 +1402,76 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           row_fail = 1;  // the buffer is full: the row starts again in tile mode
       }
     };
-    // one step of a token from set cur by `byte`: false when the entry is
-    // missing (its interval requested, cur unchanged)
+    // one step of a token by `byte` from its state after the T loop stopped:
+    // a pool set's special entry (a missing entry of a set in a frame list
+    // turns the state into the set's list state without taking the byte), or
+    // a list state (the lists' byte table; a boundary byte takes the entry of
+    // LT, inserted when missing).  False when the entry is missing (its
+    // interval or LT entry requested, the state unchanged).
     auto step = [&](int& cur, int& pos, int byte) -> bool {
-      const uint8_t nx = T[cur * 256 + byte];
-      if (nx == kTUnknown) {
-        if (((set_hit[cur][byte >> 5] >> (byte & 31)) & 1u) == 0u) {
-          cur = kRejected;  // no byte edge contains it: the step empties the set
-          return true;
+      if (cur < kWalkEnd) {
+        const uint8_t nx = T[cur * 256 + byte];
+        if (nx == kTUnknown) {
+          const int ls = set_ls[cur];
+          if (ls >= 0) {
+            cur = ls;
+            return true;
+          }
+          if (((set_hit[cur][byte >> 5] >> (byte & 31)) & 1u) == 0u) {
+            cur = kRejected;  // no byte edge contains it: the step empties the set
+            return true;
+          }
+          const int lo = interval_start(set_bnd[cur], byte);
+          const int w = cur * 8 + (lo >> 5);
+          const uint32_t bit = 1u << (lo & 31);
+          if ((req[w] & bit) == 0u) atomicOr(&req[w], bit);
+          return false;
         }
-        const int lo = interval_start(set_bnd[cur], byte);
-        const int w = cur * 8 + (lo >> 5);
-        const uint32_t bit = 1u << (lo & 31);
-        if ((req[w] & bit) == 0u) atomicOr(&req[w], bit);
+        if (nx == kTDead || nx == kTOverflow) {
+          cur = kRejected;
+        } else {
+          cur = nx;
+          ++pos;
+        }
+        return true;
+      }
+      const int code = list_code(a.frames, lcache, cur & 0xFFF, byte);
+      if (code >= 0) {
+        const int sat = (cur & (1 << 12)) | ((code & BPD_PDA_FRAME_SAT) != 0 ? 1 << 12 : 0);
+        cur = (cur & ~0x1FFF) | sat | (code & 0xFFF);
+        ++pos;
+        return true;
+      }
+      if (code == -1) {
+        cur = kRejected;  // the list (and so the set) empties
+        return true;
+      }
+      const uint32_t key = lt_key_of(cur, byte);
+      const uint32_t h = lt_hash(key);
+      int slot = -1;
+      for (int p = 0; p < kLT && slot < 0; ++p) {
+        const int s = int((h + uint32_t(p)) & uint32_t(kLT - 1));
+        uint32_t k = lt_key[s];
+        if (k == kLTEmpty) {
+          k = atomicCAS(&lt_key[s], kLTEmpty, key);
+          if (k == kLTEmpty) k = key;
+        }
+        if (k == key) slot = s;
+      }
+      if (slot < 0) {
+        row_fail = 1;  // LT is full: the row starts again in tile mode
         return false;
       }
-      if (nx == kTDead || nx == kTOverflow) {
+      const uint8_t r = lt_res[slot];
+      if (r == kTUnknown) {
+        const uint32_t bit = 1u << (slot & 31);
+        if ((lt_req[slot >> 5] & bit) == 0u) atomicOr(&lt_req[slot >> 5], bit);
+        return false;
+      }
+      if (r == kTDead || r == kTOverflow) {
         cur = kRejected;
       } else {
-        cur = nx;
+        cur = r;
         ++pos;
       }
       return true;
@@ -1296,50 +1481,63 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     // record in registers: that loop has no memory wait other than the table
     // read, so queue stores still in flight do not stall it; the bytes after
     // them are read from tok_bytes in a second loop.
-    // Each loop takes only entries that are interned sets and stops at the
-    // first other one (missing, dead or overflow: entries >= kTOverflow);
-    // step() then settles that entry once, outside the loop, so the loop
-    // body has no branch besides its exit.  A special entry never advances
-    // the token, so the walk ends there (paused or rejected).
+    // Each T loop takes only entries that are interned sets and stops at the
+    // first other one (missing, dead or overflow: entries >= kTOverflow) or
+    // at a list state; step() then settles that entry or takes the list
+    // state's byte, outside the loop, so the loop body has no branch besides
+    // its exit.  Every step() either ends the walk, takes a byte or (turning
+    // a pool set into its list state) is followed by one that does.
     auto walk = [&](int& cur, int& pos, int len, uint4 pk, int32_t t) -> bool {
       const int n16 = len < 16 ? len : 16;
-      while (cur < kWalkEnd && pos < n16) {
-        const uint8_t nx = T[cur * 256 + packed_byte(pk, pos)];
-        if (nx >= kTOverflow) break;
-        cur = nx;
-        ++pos;
-      }
-      if (cur < kWalkEnd && pos < n16 && !step(cur, pos, packed_byte(pk, pos))) return true;
-      if (cur < kWalkEnd && pos < len) {
-        const uint8_t* tb = a.tok_bytes + a.tok_off[t];
-        while (cur < kWalkEnd && pos < len) {
-          const uint8_t nx = T[cur * 256 + tb[pos]];
+      while (pos < n16 && walking(cur)) {
+        while (cur < kWalkEnd && pos < n16) {
+          const uint8_t nx = T[cur * 256 + packed_byte(pk, pos)];
           if (nx >= kTOverflow) break;
           cur = nx;
           ++pos;
         }
-        if (cur < kWalkEnd && pos < len && !step(cur, pos, int(tb[pos]))) return true;
+        if (pos < n16 && walking(cur) && !step(cur, pos, packed_byte(pk, pos))) return true;
       }
-      if (cur < kWalkEnd) cur = kAllowed;
+      if (pos < len && walking(cur)) {
+        const uint8_t* tb = a.tok_bytes + a.tok_off[t];
+        while (pos < len && walking(cur)) {
+          while (cur < kWalkEnd && pos < len) {
+            const uint8_t nx = T[cur * 256 + tb[pos]];
+            if (nx >= kTOverflow) break;
+            cur = nx;
+            ++pos;
+          }
+          if (pos < len && walking(cur) && !step(cur, pos, int(tb[pos]))) return true;
+        }
+      }
+      if (walking(cur)) cur = kAllowed;
       return false;
     };
-    // the tail of a token's walk: queue it if paused, else record an accept
+    // the tail of a token's walk: queue it if paused, else record an accept.
+    // A queue entry holds the walk position k (< 2^18) and 14 bits of the
+    // state in x, the byte position and the state's other bits in y.
     auto settle = [&](bool paused, int cur, int pos, int len, int32_t k, int32_t t, uint2* q) {
       if (paused && len > 0xFFFF) {
         row_fail = 1;
         paused = false;
       }
-      enqueue(paused, make_uint2(uint32_t(k) | (uint32_t(cur) << 24), uint32_t(pos) | (uint32_t(len) << 16)), q);
+      enqueue(paused,
+              make_uint2(uint32_t(k) | (uint32_t(cur & 0x3FFF) << 18), uint32_t(pos) | (uint32_t(cur >> 14) << 16)),
+              q);
       if (cur == kAllowed) atomicOr(&vbits[t >> 5], 1u << (t & 31));
     };
 
     if (!dead_row) {
-      // every interval of set 0 first, so the first pass already steps past byte 0
+      // every interval of set 0 first, so the first pass already steps past
+      // byte 0; of a set in a frame list only the boundary intervals (the
+      // others are walked as its list state or were filled from the list)
       if (tid < 8) {
         uint32_t m = (set_bnd[0][tid] | (tid == 0 ? 1u : 0u)) & set_hit[0][tid];
-        for (uint32_t x = m; x != 0u; x &= x - 1u) {
-          const int bit = __ffs(x) - 1;
-          if (T[tid * 32 + bit] != kTUnknown) m &= ~(1u << bit);  // filled from the frame list
+        if (row_list >= 0) {
+          for (uint32_t x = m; x != 0u; x &= x - 1u) {
+            const int c = tid * 32 + __ffs(x) - 1;
+            if (T[c] != kTUnknown || a.frames.trans[row_list * 256 + c] != -2) m &= ~(1u << (c & 31));
+          }
         }
         req[tid] = m;
       }
@@ -1528,24 +1726,24 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
           const int i = i0 + j * kMemoThreads + tid;
-          e[j] = i < qn ? qin[i] : make_uint2(0xFFFFFFFFu, 0u);
+          e[j] = i < qn ? qin[i] : make_uint2(0u, 0u);
         }
-        int32_t tq[kMemoTok];
+        int2 tq[kMemoTok];  // (token id, length)
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
-          const bool valid = e[j].x != 0xFFFFFFFFu;
-          pk[j] = valid ? ws.recs[e[j].x & 0xFFFFFFu] : make_uint4(0u, 0u, 0u, 0u);
-          tq[j] = valid ? ws.tmeta[e[j].x & 0xFFFFFFu].x : -1;
+          const bool valid = i0 + j * kMemoThreads + tid < qn;
+          pk[j] = valid ? ws.recs[e[j].x & 0x3FFFFu] : make_uint4(0u, 0u, 0u, 0u);
+          tq[j] = valid ? ws.tmeta[e[j].x & 0x3FFFFu] : make_int2(-1, 0);
         }
 #pragma unroll
         for (int j = 0; j < kMemoTok; ++j) {
-          const bool valid = e[j].x != 0xFFFFFFFFu;
-          const int32_t k = int32_t(e[j].x & 0xFFFFFFu);
-          int cur = valid ? int(e[j].x >> 24) : kNone;
+          const bool valid = i0 + j * kMemoThreads + tid < qn;
+          const int32_t k = int32_t(e[j].x & 0x3FFFFu);
+          int cur = valid ? int((e[j].x >> 18) | ((e[j].y >> 16) << 14)) : kNone;
           int pos = int(e[j].y & 0xFFFFu);
-          const int len = int(e[j].y >> 16);
-          const bool paused = walk(cur, pos, len, pk[j], tq[j]);
-          settle(paused, cur, pos, len, k, tq[j], qout);
+          const int len = tq[j].y;
+          const bool paused = walk(cur, pos, len, pk[j], tq[j].x);
+          settle(paused, cur, pos, len, k, tq[j].x, qout);
         }
       }
       __syncthreads();
@@ -1658,6 +1856,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     for (int j = 0; j < 4; ++j)
       if (((nib >> j) & 1u) != 0u && ((v >> (8 * j)) & 0xFFu) < kTOverflow) m |= uint32_t(kTExact) << (8 * j);
     tout[i] = v | m;
+  }
+  // ... the boundary table and the sets' frame-list words (the commit walks
+  // list states the same way)
+  for (int i = tid; i < kLT; i += kMemoThreads) {
+    uint32_t r = lt_res[i];
+    if (r < kTOverflow && ((lt_exact[i >> 5] >> (i & 31)) & 1u) != 0u) r |= kTExact;
+    ws.lt[b * kLT + i] = make_uint2(lt_key[i], r);
+  }
+  {
+    const int pc = pool_count < max_sets ? pool_count : max_sets;
+    for (int i = tid; i < kMemoSets; i += kMemoThreads) ws.slist[b * kMemoSets + i] = i < pc ? set_list[i] : -1;
   }
   if (tid == 0) {
     ws.overflow[b] = overflowed;
@@ -1808,6 +2017,8 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
                                                                          uint64_t tag) {
   __shared__ int32_t bufs[2][kConfigWords];
   __shared__ uint4 trow[kMemoSets * 16];  // the row's table (256 bytes per set)
+  __shared__ uint2 lrow[kLT];             // the row's boundary table
+  __shared__ int32_t srow[kMemoSets];     // frame-list word of each interned set
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t b = blockIdx.x;
   const int64_t row = a.slots ? a.slots[b] : b;
@@ -1845,8 +2056,15 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
     uint4 v[kMemoSets * 16 / kCommitThreads];
 #pragma unroll
     for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) v[q] = src[q * kCommitThreads + threadIdx.x];
+    uint2 lv[kLT / kCommitThreads];
+#pragma unroll
+    for (int q = 0; q < kLT / kCommitThreads; ++q) lv[q] = ws.lt[b * kLT + q * kCommitThreads + threadIdx.x];
+    const int32_t sv = threadIdx.x < kMemoSets ? ws.slist[b * kMemoSets + threadIdx.x] : -1;
 #pragma unroll
     for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) trow[q * kCommitThreads + threadIdx.x] = v[q];
+#pragma unroll
+    for (int q = 0; q < kLT / kCommitThreads; ++q) lrow[q * kCommitThreads + threadIdx.x] = lv[q];
+    if (threadIdx.x < kMemoSets) srow[threadIdx.x] = sv;
   }
   const PdaTableView& g = a.g;
   __syncthreads();
@@ -1866,11 +2084,15 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
       auto byte_at = [&](int32_t i) -> int {
         return i - s < kWave ? __shfl(bl, int(i - s)) : int(a.tok_bytes[i]);
       };
-      // walk the mask's table while it has the entries.  A step's raw words
-      // depend only on the meaningful words of the set it starts from, so
-      // when the last byte's entry is flagged exact the interned set is the
-      // written config-set; otherwise the rest (at least the last byte) is
-      // stepped with advance_byte from the interned set reached
+      // walk the mask's tables while they have the entries, as the mask's
+      // walk does: T for interned sets; for a set in a frame list whose T
+      // entry is missing, its list state through the lists' byte table and
+      // LT at boundary bytes.  A step's raw words depend only on the
+      // meaningful words of the set it starts from, so when the last byte's
+      // entry is flagged exact the interned set is the written config-set;
+      // otherwise the rest (at least the last byte) is stepped with
+      // advance_byte from the set reached (a list state's set rebuilt from
+      // its anchor's common stack and the list's key)
       int cur = -1, prev = -1;  // -1: no usable table, step every byte from the row's set
       bool exact = false;
       int32_t i = s;
@@ -1892,27 +2114,75 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
         const uint8_t* T = reinterpret_cast<const uint8_t*>(trow);
         cur = 0;
         for (; i < e; ++i) {
-          const uint8_t nx = T[cur * 256 + byte_at(i)];
-          if (nx == kTDead) {
+          const int byte = byte_at(i);
+          if (cur < kListState) {
+            const uint8_t nx = T[cur * 256 + byte];
+            if (nx == kTDead) {
+              cur = -2;
+              break;
+            }
+            if (nx < kTOverflow) {
+              prev = cur;
+              cur = nx & (kTExact - 1);
+              exact = (nx & kTExact) != 0;
+              continue;
+            }
+            const int sl = a.frames.num_lists > 0 ? srow[cur] : -1;
+            if (sl < 0) break;  // not resolved by the mask: step from here
+            cur = list_state(cur, sl);
+          }
+          const int code = a.frames.trans[(cur & 0xFFF) * 256 + byte];
+          if (code == -1) {
             cur = -2;
             break;
           }
-          if (nx >= kTOverflow) break;  // not resolved by the mask: step from here
+          if (code >= 0) {
+            prev = cur;
+            cur = (cur & ~0xFFF) | ((code & BPD_PDA_FRAME_SAT) != 0 ? 1 << 12 : 0) | (code & 0xFFF);
+            exact = false;
+            continue;
+          }
+          // a boundary byte: the mask's LT entry, if it has one
+          const uint32_t key = lt_key_of(cur, byte);
+          const uint32_t h = lt_hash(key);
+          int r = -1;
+          for (int p = 0; p < kLT; ++p) {
+            const uint2 v = lrow[(h + uint32_t(p)) & uint32_t(kLT - 1)];
+            if (v.x == key) {
+              r = int(v.y);
+              break;
+            }
+            if (v.x == kLTEmpty) break;
+          }
+          if (r == kTDead) {
+            cur = -2;
+            break;
+          }
+          if (r < 0 || r >= kTOverflow) break;  // step from the list state's set
           prev = cur;
-          cur = nx & (kTExact - 1);
-          exact = (nx & kTExact) != 0;
+          cur = r & (kTExact - 1);
+          exact = (r & kTExact) != 0;
         }
       }
       if (cur == -2) {
         ok = false;
-      } else if (cur >= 0 && i == e && exact) {
+      } else if (cur >= 0 && cur < kListState && i == e && exact) {
         for (int k = lane; k < kConfigWords; k += kWave) cfg[k] = pool[cur * kConfigWords + k];
       } else {
         if (cur >= 0 && i == e) {
           cur = prev;  // every byte had its entry: step the last one again
           i = e - 1;
         }
-        if (cur > 0) {
+        if (cur >= kListState) {
+          // the list state's set: its anchor's words under the list's key
+          const int anchor = (cur >> 13) & (kMemoSets - 1);
+          if (anchor > 0) {
+            for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[anchor * kConfigWords + k];
+            wave_sync();
+          }
+          compose_list_set(x, x, a.frames.keys + int64_t(cur & 0xFFF) * BPD_PDA_FRAME_KEY_WORDS,
+                           srow[anchor] >> kListBase, (cur >> 12) & 1, lane);
+        } else if (cur > 0) {
           for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[cur * kConfigWords + k];
           wave_sync();
         }
