@@ -472,18 +472,44 @@ __device__ inline bool coop_append(int32_t* dst, const int32_t* src, int i, int 
   return true;
 }
 
-__device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
+// Lane i's value of v for a wave-uniform i with every lane active: a scalar
+// read of the register (no LDS round trip, unlike a shuffle).
+__device__ __forceinline__ int lane_value(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
+
+// Closure of c in place.  Lane l < c[0] holds config l's depth (d_l) and
+// top state (top_l) on entry; the edge range and accept flag of every top are
+// loaded at once, and a config that an append adds gets its own in lane n as
+// it is added (the loads complete while earlier configs are visited), so a
+// visit waits for no table read before its edges.
+__device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane, int d_l, int top_l) {
   // one visit per config in index order, as close() in pda_core.hpp; the
   // top state's edges are loaded lane-parallel and the eps / call edges taken
   // in edge order from the ballot
-  for (int i = 0; i < c[0]; ++i) {
-    const int d = c[2 + i];
+  int n = c[0];
+  int eb_l = 0, ee_l = 0, acc_l = 0;
+  if (lane < n && d_l > 0) {
+    eb_l = g.edge_offsets[top_l];
+    ee_l = g.edge_offsets[top_l + 1];
+    acc_l = g.accept[top_l];
+  }
+  for (int i = 0; i < n; ++i) {
+    const int d = lane_value(d_l, i);
     if (d <= 0) continue;
-    const int top = c[kF + i * kMaxDepth + d - 1];
-    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
-    if (g.accept[top] && d > 1) {
-      if (!coop_holds(c, c, i, d - 1, 0, 0, 0, lane)) coop_append(c, c, i, d - 1, 0, 0, 0, lane);
-    }
+    const int eb = lane_value(eb_l, i), ee = lane_value(ee_l, i);
+    // config i's first `keep` frames and x0, x1 (nx of them) unless present;
+    // the new config's top is `ntop`
+    auto add = [&](int keep, int x0, int x1, int nx, int ntop) {
+      if (coop_holds(c, c, i, keep, x0, x1, nx, lane) || !coop_append(c, c, i, keep, x0, x1, nx, lane)) return;
+      if (lane == n) {
+        d_l = keep + nx;
+        top_l = ntop;
+        eb_l = g.edge_offsets[ntop];
+        ee_l = g.edge_offsets[ntop + 1];
+        acc_l = g.accept[ntop];
+      }
+      ++n;
+    };
+    if (lane_value(acc_l, i) != 0 && d > 1) add(d - 1, 0, 0, 0, c[kF + i * kMaxDepth + d - 2]);
     for (int base = eb; base < ee; base += kWave) {
       const int e = base + lane;
       int kind = -1, x0 = 0, x1 = 0;
@@ -496,11 +522,11 @@ __device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
       while (m) {
         const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
         m &= m - 1;
-        const int k = __shfl(kind, l), y0 = __shfl(x0, l), y1 = __shfl(x1, l);
+        const int k = lane_value(kind, l), y0 = lane_value(x0, l), y1 = lane_value(x1, l);
         if (k == BPD_PDA_EDGE_EPS) {
-          if (!coop_holds(c, c, i, d - 1, y0, 0, 1, lane)) coop_append(c, c, i, d - 1, y0, 0, 1, lane);
+          add(d - 1, y0, 0, 1, y0);
         } else if (d + 1 <= kMaxDepth) {
-          if (!coop_holds(c, c, i, d - 1, y0, y1, 2, lane)) coop_append(c, c, i, d - 1, y0, y1, 2, lane);
+          add(d - 1, y0, y1, 2, y1);
         } else {
           wave_sync();
           if (lane == 0) c[1] = 1;
@@ -509,14 +535,14 @@ __device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
       }
     }
   }
-  // prune_dead: order-preserving compaction, vacated words not cleared
+  // prune_dead: order-preserving compaction, vacated words not cleared (the
+  // live flags of every top read at once)
+  const uint64_t live = __ballot(lane < n && d_l > 0 && g.live[top_l] != 0);
   int out = 0;
-  const int n = c[0];
   for (int i = 0; i < n; ++i) {
-    const int d = c[2 + i];
-    if (d <= 0) continue;
-    if (!g.live[c[kF + i * kMaxDepth + d - 1]]) continue;
+    if (((live >> i) & 1u) == 0u) continue;
     if (out != i) {
+      const int d = lane_value(d_l, i);
       if (lane < d) c[kF + out * kMaxDepth + lane] = c[kF + i * kMaxDepth + lane];
       wave_sync();
       if (lane == 0) c[2 + out] = d;
@@ -530,17 +556,29 @@ __device__ bool coop_close(const PdaTableView& g, int32_t* c, int lane) {
   return out > 0;
 }
 
-// next = close(byte step of src) with next freshly zeroed (as FlatView::reset_all)
+// next = close(byte step of src) with next freshly zeroed (as
+// FlatView::reset_all).  The depth, top and edge range of every config of
+// src are read at once (lane l: config l); the configs the step appends to
+// next hand their depth and top to coop_close the same way.
 __device__ bool coop_advance_byte(const PdaTableView& g, const int32_t* src, int32_t* next, int byte,
                                   int lane) {
   for (int k = lane; k < kConfigWords; k += kWave) next[k] = 0;
-  wave_sync();
   const int n = src[0];
+  int sd = 0, seb = 0, see = 0;
+  if (lane < n) {
+    sd = src[2 + lane];
+    if (sd > 0) {
+      const int top = src[kF + lane * kMaxDepth + sd - 1];
+      seb = g.edge_offsets[top];
+      see = g.edge_offsets[top + 1];
+    }
+  }
+  wave_sync();
+  int nd = 0, ntop = -1, nn = 0;  // lane l: depth and top of config l of next
   for (int i = 0; i < n; ++i) {
-    const int d = src[2 + i];
+    const int d = lane_value(sd, i);
     if (d <= 0) continue;
-    const int top = src[kF + i * kMaxDepth + d - 1];
-    const int eb = g.edge_offsets[top], ee = g.edge_offsets[top + 1];
+    const int eb = lane_value(seb, i), ee = lane_value(see, i);
     for (int base = eb; base < ee; base += kWave) {
       const int e = base + lane;
       bool match = false;
@@ -553,15 +591,21 @@ __device__ bool coop_advance_byte(const PdaTableView& g, const int32_t* src, int
       while (m) {
         const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
         m &= m - 1;
-        const int y = __shfl(x, l);
-        if (!coop_holds(next, src, i, d - 1, y, 0, 1, lane)) coop_append(next, src, i, d - 1, y, 0, 1, lane);
+        const int y = lane_value(x, l);
+        if (!coop_holds(next, src, i, d - 1, y, 0, 1, lane) && coop_append(next, src, i, d - 1, y, 0, 1, lane)) {
+          if (lane == nn) {
+            nd = d;
+            ntop = y;
+          }
+          ++nn;
+        }
       }
     }
   }
   wave_sync();
   if (lane == 0) next[1] = (next[1] || src[1]) ? 1 : 0;
   wave_sync();
-  return coop_close(g, next, lane);
+  return coop_close(g, next, lane, nd, ntop);
 }
 
 // Is word w of a FlatView set with n configs and depths dep() meaningful?
@@ -802,27 +846,31 @@ __device__ void frame_fill_row(const BpdPdaFrames& f, int l, bool sat, int id, u
 // The meaningful words of the set of list `key` over the common stack that
 // config 0 of `src` holds in its first `base` frames, written to `dst`
 // (words past each depth set to 0; dst may be src).  One wave.
+static_assert(BPD_PDA_FRAME_KEY_WORDS <= kWave, "a frame-list key is read one word per lane");
 __device__ void compose_list_set(const int32_t* src, int32_t* dst, const int32_t* key, int base, int sat,
                                  int lane) {
+  // the key in one load (lane l: word l), read back by lane exchanges
+  const int32_t kw = lane < BPD_PDA_FRAME_KEY_WORDS ? key[lane] : 0;
   const int32_t pw = lane < base ? src[kF + lane] : 0;
-  const int n = key[0];
-  int32_t len[kMaxConfigs];
-#pragma unroll
-  for (int i = 0; i < kMaxConfigs; ++i) len[i] = i < n ? key[1 + i] : 0;
+  const int n = lane_value(kw, 0);
   wave_sync();
   for (int w = lane; w < kMaxConfigs * kMaxDepth; w += kWave) {
     const int i = w / kMaxDepth, k = w % kMaxDepth;
     const int32_t p = __shfl(pw, k < base ? k : 0);
+    const int len = __shfl(kw, 1 + i);
+    const int f = k - base < 0 ? 0 : (k - base < BPD_PDA_FRAME_SUFFIX ? k - base : BPD_PDA_FRAME_SUFFIX - 1);
+    const int32_t sfx = __shfl(kw, 1 + kMaxConfigs + i * BPD_PDA_FRAME_SUFFIX + f);
     int32_t v = 0;
     if (i < n) {
       if (k < base)
         v = p;
-      else if (k < base + len[i])
-        v = key[1 + kMaxConfigs + i * BPD_PDA_FRAME_SUFFIX + (k - base)];
+      else if (k < base + len)
+        v = sfx;
     }
     dst[kF + w] = v;
   }
-  if (lane < kMaxConfigs) dst[2 + lane] = lane < n ? base + len[lane] : 0;
+  const int len_l = __shfl(kw, 1 + (lane & (kMaxConfigs - 1)));
+  if (lane < kMaxConfigs) dst[2 + lane] = lane < n ? base + len_l : 0;
   if (lane == 0) {
     dst[0] = n;
     dst[1] = sat;
@@ -899,9 +947,12 @@ __device__ PdaTableView stage_tables(const PdaTableView& src, int32_t* tab, int 
 // verdicts of a token in the memoised walk, past every set id
 constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 
+// InLds: the grammar tables are staged in LDS (the dynamic array `tab`).  A
+// compile-time choice, so that every table read of the walk and of the
+// resolution rounds is an LDS read rather than a flat one.
+template <bool InLds>
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
-                                                                     int table_in_lds, uint64_t tag,
-                                                                     uint32_t gen, int row_mode,
+                                                                     uint64_t tag, uint32_t gen, int row_mode,
                                                                      uint64_t pkey) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
@@ -939,6 +990,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t work[kMemoThreads / kWave][2][kConfigWords];  // per-wave src / dst
   __shared__ int pool_count, nreq, row_flags, overflowed, qcount, row_fail, loop_n, row_list;
   __shared__ int n_stepped, n_cheap;
+  __shared__ int walk_lists;  // the row-wide walk takes list states (not in tile mode)
   __shared__ uint32_t h0_sh;
   __shared__ uint8_t loop0[256];  // T[0][c] == 0: byte c keeps set 0 (row-wide walk)
   // first pass of the row-wide walk: pass index i -> walk position
@@ -959,7 +1011,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   }
 
   for (int k = tid; k < kConfigWords; k += kMemoThreads) row_cfg[k] = a.configs[row * kConfigWords + k];
-  const PdaTableView g = table_in_lds ? stage_tables(a.g, tab, tid, kMemoThreads) : a.g;
+  const PdaTableView g = InLds ? stage_tables(a.g, tab, tid, kMemoThreads) : a.g;
   for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
   for (int i = tid; i < BPD_PDA_FRAME_SLOTS; i += kMemoThreads)
     fslots[i] = a.frames.num_lists > 0 ? a.frames.slots[i] : BPD_PDA_FRAME_EMPTY;
@@ -981,6 +1033,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   if (tid == 0) {
     pool_count = 1;
     overflowed = 0;
+    walk_lists = row_mode != 0 ? 1 : 0;
   }
   __syncthreads();
   if (tid >= kWave && tid < 2 * kWave) {
@@ -1319,9 +1372,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           const int k = lane + q * kWave;
           words[q] = k < kConfigWords ? src[k] : 0;
         }
-        coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]],
-                           T + cand_id[r] * 256, lane);
+        // a set in a frame list needs no intervals while lists are walked
+        // (its missing entries turn the walk into its list state)
         const int cl = cand_list[r];
+        if (cl < 0 || !walk_lists)
+          coop_set_intervals(g, cand_tops[r], cand_n[r], set_bnd[cand_id[r]], set_hit[cand_id[r]],
+                             T + cand_id[r] * 256, lane);
         if (cl >= 0) {
           wave_sync();
           frame_fill_row(a.frames, cl & (BPD_PDA_FRAME_SAT - 1), (cl & BPD_PDA_FRAME_SAT) != 0, cand_id[r],
@@ -1754,6 +1810,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     if (overflowed || row_fail) {
       // start again in tile mode from an empty pool, bitmap and request set
+      if (tid == 0) walk_lists = 0;
       for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
       for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) req[i] = 0u;
       reset_pool();
@@ -2409,10 +2466,15 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     // stage the grammar tables in LDS when they fit beside the static arrays
     const size_t tab_bytes = staged_table_bytes(g);
     size_t room = 0;
-    if (int rc = lds_room(reinterpret_cast<const void*>(&pda_memo_mask_kernel), 0, &room)) return rc;
-    const bool in_lds = tab_bytes <= room;
-    pda_memo_mask_kernel<<<unsigned(rows), kMemoThreads, in_lds ? tab_bytes : 0, as_stream(stream)>>>(
-        a, ws, max_sets, in_lds ? 1 : 0, memo_tag(g, toks, rows), next_generation(), row_mode, pkey);
+    if (int rc = lds_room(reinterpret_cast<const void*>(&pda_memo_mask_kernel<true>), 0, &room)) return rc;
+    const uint64_t tag = memo_tag(g, toks, rows);
+    const uint32_t gen = next_generation();
+    if (tab_bytes <= room)
+      pda_memo_mask_kernel<true><<<unsigned(rows), kMemoThreads, tab_bytes, as_stream(stream)>>>(
+          a, ws, max_sets, tag, gen, row_mode, pkey);
+    else
+      pda_memo_mask_kernel<false><<<unsigned(rows), kMemoThreads, 0, as_stream(stream)>>>(a, ws, max_sets, tag, gen,
+                                                                                        row_mode, pkey);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
     // rows that overflow are rare: four waves per row keep short a launch
