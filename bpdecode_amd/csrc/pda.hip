@@ -907,10 +907,36 @@ size_t staged_table_bytes(const BpdPdaTable* g) {
   return (size_t(g->num_states) + 1) * 4 + size_t(g->num_edges) * 20 + (size_t(g->num_states) * 2 + 3) / 4 * 4;
 }
 
+// Entry tid of each grammar table, read into registers before the workgroup
+// fills its LDS arrays so that these loads are in flight meanwhile.
+struct TableSlice {
+  int32_t eo, ek, elo, ehi, ed, ec;
+  uint8_t acc, lv;
+};
+
+__device__ TableSlice table_slice(const PdaTableView& src, int tid) {
+  TableSlice t{0, 0, 0, 0, 0, 0, 0, 0};
+  if (tid <= src.num_states) t.eo = src.edge_offsets[tid];
+  if (tid < src.num_edges) {
+    t.ek = src.edge_kind[tid];
+    t.elo = src.edge_lo[tid];
+    t.ehi = src.edge_hi[tid];
+    t.ed = src.edge_dst[tid];
+    t.ec = src.edge_callee[tid];
+  }
+  if (tid < src.num_states) {
+    t.acc = src.accept[tid];
+    t.lv = src.live[tid];
+  }
+  return t;
+}
+
 // Copy of the grammar tables in LDS at `tab` (staged_table_bytes long) made
-// by the workgroup's `nthreads` threads, and a view of it; the caller
-// synchronises before the view is read.
-__device__ PdaTableView stage_tables(const PdaTableView& src, int32_t* tab, int tid, int nthreads) {
+// by the workgroup's `nthreads` threads (entry tid of each table from the
+// thread's slice, the entries past nthreads read here), and a view of it;
+// the caller synchronises before the view is read.
+__device__ PdaTableView stage_tables(const PdaTableView& src, int32_t* tab, const TableSlice& t, int tid,
+                                     int nthreads) {
   const int N = src.num_states, E = src.num_edges;
   int32_t* eo = tab;
   int32_t* ek = eo + N + 1;
@@ -920,15 +946,27 @@ __device__ PdaTableView stage_tables(const PdaTableView& src, int32_t* tab, int 
   int32_t* ec = ed + E;
   uint8_t* acc = reinterpret_cast<uint8_t*>(ec + E);
   uint8_t* lv = acc + N;
-  for (int i = tid; i <= N; i += nthreads) eo[i] = src.edge_offsets[i];
-  for (int i = tid; i < E; i += nthreads) {
+  if (tid <= N) eo[tid] = t.eo;
+  for (int i = tid + nthreads; i <= N; i += nthreads) eo[i] = src.edge_offsets[i];
+  if (tid < E) {
+    ek[tid] = t.ek;
+    elo[tid] = t.elo;
+    ehi[tid] = t.ehi;
+    ed[tid] = t.ed;
+    ec[tid] = t.ec;
+  }
+  for (int i = tid + nthreads; i < E; i += nthreads) {
     ek[i] = src.edge_kind[i];
     elo[i] = src.edge_lo[i];
     ehi[i] = src.edge_hi[i];
     ed[i] = src.edge_dst[i];
     ec[i] = src.edge_callee[i];
   }
-  for (int i = tid; i < N; i += nthreads) {
+  if (tid < N) {
+    acc[tid] = t.acc;
+    lv[tid] = t.lv;
+  }
+  for (int i = tid + nthreads; i < N; i += nthreads) {
     acc[i] = src.accept[i];
     lv[i] = src.live[i];
   }
@@ -1010,11 +1048,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     ws.header[3] = uint32_t(pkey >> 32);
   }
 
-  for (int k = tid; k < kConfigWords; k += kMemoThreads) row_cfg[k] = a.configs[row * kConfigWords + k];
-  const PdaTableView g = InLds ? stage_tables(a.g, tab, tid, kMemoThreads) : a.g;
+  // the prologue's global reads (the row's set, the frame lists' slot
+  // table, the first slice of the grammar tables) are issued first and
+  // stored after the LDS fills below, which run while they are in flight
+  static_assert(kConfigWords <= kMemoThreads && BPD_PDA_FRAME_SLOTS % kMemoThreads == 0, "prologue slices");
+  const int32_t cfg_w = tid < kConfigWords ? a.configs[row * kConfigWords + tid] : 0;
+  uint32_t fsv[BPD_PDA_FRAME_SLOTS / kMemoThreads];
+#pragma unroll
+  for (int q = 0; q < BPD_PDA_FRAME_SLOTS / kMemoThreads; ++q)
+    fsv[q] = a.frames.num_lists > 0 ? a.frames.slots[q * kMemoThreads + tid] : BPD_PDA_FRAME_EMPTY;
+  const TableSlice tsl = InLds ? table_slice(a.g, tid) : TableSlice{0, 0, 0, 0, 0, 0, 0, 0};
   for (int i = tid; i < kMemoSets * 256 / 4; i += kMemoThreads) T32[i] = 0xFEFEFEFEu;
-  for (int i = tid; i < BPD_PDA_FRAME_SLOTS; i += kMemoThreads)
-    fslots[i] = a.frames.num_lists > 0 ? a.frames.slots[i] : BPD_PDA_FRAME_EMPTY;
   const int32_t vwords = (a.vocab + 31) / 32;
   for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = 0u;
   for (int i = tid; i < kMemoSets * 8; i += kMemoThreads) {
@@ -1030,6 +1074,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
   }
   for (int i = tid; i < kLC; i += kMemoThreads) lcache[i] = 0xFFFFFFFFu;
+  if (tid < kConfigWords) row_cfg[tid] = cfg_w;
+#pragma unroll
+  for (int q = 0; q < BPD_PDA_FRAME_SLOTS / kMemoThreads; ++q) fslots[q * kMemoThreads + tid] = fsv[q];
+  const PdaTableView g = InLds ? stage_tables(a.g, tab, tsl, tid, kMemoThreads) : a.g;
   if (tid == 0) {
     pool_count = 1;
     overflowed = 0;
