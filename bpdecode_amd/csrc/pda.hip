@@ -883,7 +883,7 @@ __device__ void compose_list_set(const int32_t* src, int32_t* dst, const int32_t
 // once per device and kernel slot.
 int lds_room(const void* kernel, int slot, size_t* room) {
   constexpr int kDevices = 64;
-  static std::atomic<long long> cache[kDevices][1];  // room + 1; 0: not queried yet
+  static std::atomic<long long> cache[kDevices][2];  // room + 1; 0: not queried yet
   int dev = 0;
   BPD_HIP(hipGetDevice(&dev));
   if (dev >= 0 && dev < kDevices) {
@@ -2118,8 +2118,12 @@ __global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a)
 // commits the row.
 constexpr int kCommitThreads = 256;
 
+// InLds: the grammar tables are staged in LDS (the dynamic array `ctab`), so
+// the closure of the commit's byte steps reads them from LDS.
+template <bool InLds>
 __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(AdvanceArgs a, MemoWs ws,
                                                                          uint64_t tag) {
+  extern __shared__ __align__(16) int32_t ctab[];
   __shared__ int32_t bufs[2][kConfigWords];
   __shared__ uint4 trow[kMemoSets * 16];  // the row's table (256 bytes per set)
   __shared__ uint2 lrow[kLT];             // the row's boundary table
@@ -2156,6 +2160,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   }
   // the token's first 64 bytes, one per lane
   const int32_t bl = threadIdx.x < kWave && s + lane < e ? int32_t(a.tok_bytes[s + lane]) : 0;
+  const TableSlice tsl = InLds ? table_slice(a.g, int(threadIdx.x)) : TableSlice{0, 0, 0, 0, 0, 0, 0, 0};
   {
     const uint4* src = reinterpret_cast<const uint4*>(ws.table + b * (kMemoSets * 64));
     uint4 v[kMemoSets * 16 / kCommitThreads];
@@ -2171,7 +2176,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
     for (int q = 0; q < kLT / kCommitThreads; ++q) lrow[q * kCommitThreads + threadIdx.x] = lv[q];
     if (threadIdx.x < kMemoSets) srow[threadIdx.x] = sv;
   }
-  const PdaTableView& g = a.g;
+  const PdaTableView g = InLds ? stage_tables(a.g, ctab, tsl, int(threadIdx.x), kCommitThreads) : a.g;
   __syncthreads();
   if (threadIdx.x >= kWave) return;
   bool ok;
@@ -2588,7 +2593,16 @@ extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, 
     const size_t need = memo_ws_bytes(rows, toks->vocab_size);
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
     const MemoWs ws = memo_ws(workspace, rows, toks->vocab_size);
-    pda_memo_advance_kernel<<<unsigned(rows), kCommitThreads, 0, as_stream(stream)>>>(a, ws, memo_tag(g, toks, rows));
+    // the grammar tables in LDS when they fit beside the static arrays
+    const size_t tab_bytes = staged_table_bytes(g);
+    size_t room = 0;
+    if (int rc = lds_room(reinterpret_cast<const void*>(&pda_memo_advance_kernel<true>), 1, &room)) return rc;
+    if (tab_bytes <= room)
+      pda_memo_advance_kernel<true><<<unsigned(rows), kCommitThreads, tab_bytes, as_stream(stream)>>>(
+          a, ws, memo_tag(g, toks, rows));
+    else
+      pda_memo_advance_kernel<false><<<unsigned(rows), kCommitThreads, 0, as_stream(stream)>>>(
+          a, ws, memo_tag(g, toks, rows));
     BPD_LAUNCHED();
     return BPD_OK;
   }
