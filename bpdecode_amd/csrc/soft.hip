@@ -1288,8 +1288,10 @@ __global__ __launch_bounds__(kRoundThreads) void prior_rounds_kernel(
     }
   } else {
     // [P] piece (max, sum) pairs, 8-byte aligned after the pairs
-    const uintptr_t pc_at = reinterpret_cast<uintptr_t>(pr + (PairsInLds ? NP : 0));
-    float2* pc = reinterpret_cast<float2*>((pc_at + 7) & ~uintptr_t(7));
+    // (offsets from the LDS base rather than an integer address, so that the
+    // accesses stay LDS ones)
+    const size_t pc_at = size_t(reinterpret_cast<char*>(pr + (PairsInLds ? NP : 0)) - reinterpret_cast<char*>(lds));
+    float2* pc = reinterpret_cast<float2*>(reinterpret_cast<char*>(lds) + ((pc_at + 7) & ~size_t(7)));
     for (int32_t p = tid; p < P; p += kRoundThreads)
       pc[p] = make_float2(ws.mid[(b * P + p) * 2], ws.mid[(b * P + p) * 2 + 1]);
     __syncthreads();
