@@ -991,7 +991,7 @@ constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 template <bool InLds>
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
                                                                      uint64_t tag, uint32_t gen, int row_mode,
-                                                                     uint64_t pkey) {
+                                                                     uint64_t pkey, int lt_cap) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
@@ -1018,6 +1018,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ uint8_t lt_res[kLT];          // ... and entries (pool id, kTDead, kTOverflow, kTUnknown)
   __shared__ uint32_t lt_req[kLT / 32];    // requested boundary entries
   __shared__ uint32_t lt_exact[kLT / 32];  // entries whose step gives the set's raw words
+  __shared__ int lt_used;                  // entries inserted in LT
   __shared__ uint32_t lcache[kLC];         // entries of the lists' byte table met so far
   __shared__ uint8_t cand_comp[kMemoReq];  // composed from a list's key: raw words unknown
   __shared__ uint32_t fslots[BPD_PDA_FRAME_SLOTS];  // the frame lists' slot table
@@ -1082,6 +1083,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     pool_count = 1;
     overflowed = 0;
     walk_lists = row_mode != 0 ? 1 : 0;
+    lt_used = 0;
   }
   __syncthreads();
   if (tid >= kWave && tid < 2 * kWave) {
@@ -1472,6 +1474,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       pool_count = 1;
       pool_hash[0] = h0_sh;
       overflowed = 0;
+      lt_used = 0;
     }
     __syncthreads();
   };
@@ -1558,7 +1561,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         uint32_t k = lt_key[s];
         if (k == kLTEmpty) {
           k = atomicCAS(&lt_key[s], kLTEmpty, key);
-          if (k == kLTEmpty) k = key;
+          if (k == kLTEmpty) {
+            k = key;
+            if (atomicAdd(&lt_used, 1) >= lt_cap) row_fail = 1;  // beyond the cap (tests)
+          }
         }
         if (k == key) slot = s;
       }
@@ -2522,12 +2528,19 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     if (int rc = lds_room(reinterpret_cast<const void*>(&pda_memo_mask_kernel<true>), 0, &room)) return rc;
     const uint64_t tag = memo_tag(g, toks, rows);
     const uint32_t gen = next_generation();
+    // BPD_PDA_LT_CAP lowers the entries the boundary table takes (tests of a
+    // full table: the row starts again in tile mode)
+    int lt_cap = kLT;
+    if (const char* e = std::getenv("BPD_PDA_LT_CAP")) {
+      const int v = std::atoi(e);
+      if (v >= 1 && v < kLT) lt_cap = v;
+    }
     if (tab_bytes <= room)
       pda_memo_mask_kernel<true><<<unsigned(rows), kMemoThreads, tab_bytes, as_stream(stream)>>>(
-          a, ws, max_sets, tag, gen, row_mode, pkey);
+          a, ws, max_sets, tag, gen, row_mode, pkey, lt_cap);
     else
-      pda_memo_mask_kernel<false><<<unsigned(rows), kMemoThreads, 0, as_stream(stream)>>>(a, ws, max_sets, tag, gen,
-                                                                                        row_mode, pkey);
+      pda_memo_mask_kernel<false><<<unsigned(rows), kMemoThreads, 0, as_stream(stream)>>>(
+          a, ws, max_sets, tag, gen, row_mode, pkey, lt_cap);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
     // rows that overflow are rare: four waves per row keep short a launch

@@ -231,6 +231,36 @@ def test_json_full_queue_rows_match_oracle(dev, json_case, monkeypatch, cap):
     assert np.array_equal(cb._configs.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("cap", ["1", "3"])
+def test_json_full_boundary_table_rows_match_oracle(dev, json_case, monkeypatch, cap):
+    """With the boundary table lowered to one or three entries, rows whose
+    list states meet more boundary bytes start again in tile mode; masks and
+    the commits that read the kept tables stay the oracle's."""
+    vocab, g, t = json_case
+    _log(f"case json V=151936 B=16 boundary-table cap {cap}")
+    monkeypatch.setenv("BPD_PDA_LT_CAP", cap)
+    cfgs = _json_configs(g, 16, seed=29)
+    gd = g.to(dev)
+    pool = cfgs.to(dev)
+    bits = pda_compute_mask(gd, pool).cpu().numpy().view(np.uint32)
+    assert np.array_equal(bits, OP.compute_mask(t, cfgs.numpy()))
+    cb = CFGConstraintBatch(gd, capacity=16, device=dev)
+    for i in range(16):
+        cb.add(i)
+    cb._configs.copy_(pool)
+    x = synth.logits(16, vocab.size, 3.0, torch.float32, seed=8).to(dev)
+    cb.apply_mask(list(range(16)), x)
+    ref = synth.logits(16, vocab.size, 3.0, torch.float32, seed=8).numpy().copy()
+    OP.apply_mask(t, cfgs.numpy().copy(), ref)
+    assert np.array_equal(x.cpu().numpy(), ref)
+    toks = torch.argmax(x, dim=1).to(torch.int32)
+    cb.commit(list(range(16)), toks)
+    want = cfgs.numpy().copy()
+    ok = OP.advance(t, want, toks.cpu().numpy())
+    assert ok.all()
+    assert np.array_equal(cb._configs.cpu().numpy(), want)
+
+
 def test_json_row_walk_equals_tile_walk(dev, json_case, monkeypatch):
     """The row-wide walk (default) and the tile-by-tile walk of the memoised
     kernel give the oracle's bits on 48 rows (string, number, after-value and
