@@ -476,6 +476,20 @@ __device__ inline bool coop_append(int32_t* dst, const int32_t* src, int i, int 
 // read of the register (no LDS round trip, unlike a shuffle).
 __device__ __forceinline__ int lane_value(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
 
+// Sum of v over the wave, in every lane (every lane active): DPP exchanges
+// within each row of 16 lanes (lane ^ 1, lane ^ 2, then the half-row and row
+// mirrors), then the four row sums by scalar lane reads -- no LDS round
+// trip, where a shuffle reduction takes six.
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+  uint32_t s = v;
+  s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x140, 0xF, 0xF, false));  // row_mirror
+  return uint32_t(__builtin_amdgcn_readlane(int(s), 0)) + uint32_t(__builtin_amdgcn_readlane(int(s), 16)) +
+         uint32_t(__builtin_amdgcn_readlane(int(s), 32)) + uint32_t(__builtin_amdgcn_readlane(int(s), 48));
+}
+
 // Closure of c in place.  Lane l < c[0] holds config l's depth (d_l) and
 // top state (top_l) on entry; the edge range and accept flag of every top are
 // loaded at once, and a config that an append adds gets its own in lane n as
@@ -632,7 +646,7 @@ __device__ uint32_t coop_hash(const int32_t* c, int lane) {
   uint32_t h = 0;
   for (int w = lane; w < kConfigWords; w += kWave)
     if (meaningful_word(c, n, w)) h += mix32(uint32_t(w) * 0x9E3779B1u ^ uint32_t(c[w]));
-  for (int o = 32; o > 0; o >>= 1) h += __shfl_xor(h, o);
+  h = wave_sum(h);
   return h;
 }
 
@@ -800,7 +814,7 @@ __device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const uint
         term = frame_mix((uint32_t((i << 8) | k) * 0x9E3779B1u) ^ uint32_t(want));
       }
     }
-    for (int o = 1; o < kWave; o <<= 1) term += __shfl_xor(term, o);
+    term = wave_sum(term);
     const uint32_t h = frame_mix(term);
     const uint32_t fp = (h >> 10) & 0xFFFFFu;
     uint32_t at = h;
