@@ -826,7 +826,7 @@ __device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const uint
       while (m != 0u) {
         const int k = __ffsll(static_cast<unsigned long long>(m)) - 1;
         m &= m - 1;
-        const int id = int(__shfl(e, k) & 0xFFFu);
+        const int id = int(uint32_t(lane_value(int(e), k)) & 0xFFFu);
         if (id < f.num_lists) {
           const bool diff = lane < BPD_PDA_FRAME_KEY_WORDS && f.keys[id * BPD_PDA_FRAME_KEY_WORDS + lane] != want;
           if (__ballot(diff) == 0u) {
@@ -1514,7 +1514,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       const int leader = __ffsll(static_cast<unsigned long long>(m)) - 1;
       int base = 0;
       if (lane == leader) base = atomicAdd(&qcount, __popcll(m));
-      base = __shfl(base, leader);
+      base = lane_value(base, leader);
       if (p) {
         const int idx = base + __popcll(m & ((uint64_t(1) << lane) - 1u));
         if (idx < Q)
