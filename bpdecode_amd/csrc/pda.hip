@@ -868,10 +868,16 @@ __device__ void compose_list_set(const int32_t* src, int32_t* dst, const int32_t
   const int32_t pw = lane < base ? src[kF + lane] : 0;
   const int n = lane_value(kw, 0);
   wave_sync();
+  // a lane's frame index k = lane % 32 is the same in every pass, so its
+  // common-stack frame is exchanged once; the two configs of a pass (lanes
+  // below and above 32) read their suffix lengths by scalar lane reads
+  static_assert(kWave == 2 * kMaxDepth, "two configs per pass of the wave");
+  const int32_t p = __shfl(pw, (lane & (kMaxDepth - 1)) < base ? (lane & (kMaxDepth - 1)) : 0);
   for (int w = lane; w < kMaxConfigs * kMaxDepth; w += kWave) {
     const int i = w / kMaxDepth, k = w % kMaxDepth;
-    const int32_t p = __shfl(pw, k < base ? k : 0);
-    const int len = __shfl(kw, 1 + i);
+    const int i0 = (w - lane) / kMaxDepth;  // the pass's first config (wave-uniform)
+    const int len0 = lane_value(kw, 1 + i0), len1 = lane_value(kw, 2 + i0);
+    const int len = lane < kMaxDepth ? len0 : len1;
     const int f = k - base < 0 ? 0 : (k - base < BPD_PDA_FRAME_SUFFIX ? k - base : BPD_PDA_FRAME_SUFFIX - 1);
     const int32_t sfx = __shfl(kw, 1 + kMaxConfigs + i * BPD_PDA_FRAME_SUFFIX + f);
     int32_t v = 0;
