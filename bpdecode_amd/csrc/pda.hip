@@ -10,10 +10,14 @@
 // rejected with one bit test.  Verdicts of the 64 lanes are written as one
 // coalesced store (logits) or packed into two words with a ballot (bits).
 //
-// Commit kernel: one thread per row with two int32 config-sets in LDS; the
-// walk starts from the row's set in global memory and every byte step writes
-// a freshly cleared set, so the 266 words written back on acceptance are
-// exactly those the reference produces.
+// Commit kernel without a workspace: one thread per row with two int32
+// config-sets in LDS; the walk starts from the row's set in global memory and
+// every byte step writes a freshly cleared set, so the 266 words written back
+// on acceptance are exactly those the reference produces.  With the mask's
+// workspace the commit walks the mask's tables first (pda_memo_advance_kernel).
+//
+// Memoised mask kernel (pda_memo_mask_kernel, the default with a workspace):
+// see the section below.
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
@@ -166,13 +170,16 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
 // workgroup therefore interns the sets it meets (pool, global workspace) and
 // fills a transition table T[set][byte] in LDS on demand: threads walk their
 // tokens through T; a missing entry pauses the token and is requested; the
-// requests of a round are computed in parallel (one thread each, the set
-// being built in a workspace slot), de-duplicated against the pool and among
-// themselves, and entered in T; then the walks resume.  Every entry is
-// computed by the same advance_byte as the direct walk, so verdicts are
-// identical.  A row that needs more than kMemoSets distinct sets marks the
-// missing entries "overflow", leaves those tokens untouched and is finished
-// by the direct-walk kernel (pda_mask_kernel filtered to flagged rows).
+// requests of a round are computed in parallel (one wave each, the set
+// being built in LDS), de-duplicated against the pool and among themselves,
+// and entered in T; then the walks resume.  A set that is in a stack-relative
+// frame list is walked through the lists' byte table instead (list states,
+// below), and only its boundary bytes are requested, through the boundary
+// table LT.  Every entry is computed by the same advance_byte as the direct
+// walk, so verdicts are identical.  A row that needs more than kMemoSets
+// distinct sets marks the missing entries "overflow", leaves those tokens
+// untouched and is finished by the direct-walk kernel (pda_mask_kernel
+// filtered to flagged rows).
 constexpr int kMemoThreads = 1024;
 constexpr int kMemoSets = 128;
 constexpr int kMemoReq = 128;
