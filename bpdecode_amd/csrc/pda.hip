@@ -1111,6 +1111,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     overflowed = 0;
     walk_lists = row_mode != 0 ? 1 : 0;
     lt_used = 0;
+    nreq = 0;
   }
   __syncthreads();
   if (tid >= kWave && tid < 2 * kWave) {
@@ -1167,9 +1168,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   // fill T and LT; sets `overflowed` when the pool is full.  A request beyond
   // the first kMemoReq stays unresolved and its token asks again after the
   // next walk.  Called by every thread, between barriers.
+  // (nreq is 0 on entry: set so in the prologue and at the end of each call)
   auto resolve = [&]() {
-    if (tid == 0) nreq = 0;
-    __syncthreads();
     for (int w = tid; w < kMemoSets * 8 + kLT / 32; w += kMemoThreads) {
       const bool lt = w >= kMemoSets * 8;
       uint32_t* word = lt ? &lt_req[w - kMemoSets * 8] : &req[w];
@@ -1188,10 +1188,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     __syncthreads();
     const int n = nreq < kMemoReq ? nreq : kMemoReq;
-    {
+    if (n > kMemoThreads / kWave) {
       // the requests a wave steps (no frame-list composition) first: waves
       // take requests r = wave, wave + 16, ..., so each wave gets at most
-      // one more of them than another
+      // one more of them than another (with one request per wave at most
+      // there is nothing to order)
       uint32_t entry = 0u;
       bool cheap = true;
       if (tid < n) {
@@ -1467,6 +1468,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
       }
     }
+    if (tid == 0) nreq = 0;  // every thread read it before the claim's barrier
     __syncthreads();
   };
 
