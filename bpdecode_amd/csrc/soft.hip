@@ -385,14 +385,40 @@ __device__ inline Lse lse_merge_fast(Lse a, Lse b) {
   return Lse{m, a.s * exp_shift(a.m, m) + b.s * exp_shift(b.m, m)};
 }
 
+// Wave reductions with every lane active, the result in every lane: DPP
+// exchanges within each row of 16 lanes (lane ^ 1, lane ^ 2, the half-row
+// mirror, the row mirror), then the four row results by scalar lane reads --
+// no LDS round trip, where a shuffle butterfly takes six.
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
 __device__ inline Lse wave_lse(Lse a) {
-  for (int o = 32; o > 0; o >>= 1) {
-    Lse b;
-    b.m = __shfl_xor(a.m, o);
-    b.s = __shfl_xor(a.s, o);
-    a = lse_merge_fast(a, b);
-  }
-  return a;
+  a = lse_merge_fast(a, Lse{dpp_f<0xB1>(a.m), dpp_f<0xB1>(a.s)});
+  a = lse_merge_fast(a, Lse{dpp_f<0x4E>(a.m), dpp_f<0x4E>(a.s)});
+  a = lse_merge_fast(a, Lse{dpp_f<0x141>(a.m), dpp_f<0x141>(a.s)});
+  a = lse_merge_fast(a, Lse{dpp_f<0x140>(a.m), dpp_f<0x140>(a.s)});
+  const Lse r0 = lse_merge_fast(Lse{lane_f(a.m, 0), lane_f(a.s, 0)}, Lse{lane_f(a.m, 16), lane_f(a.s, 16)});
+  const Lse r1 = lse_merge_fast(Lse{lane_f(a.m, 32), lane_f(a.s, 32)}, Lse{lane_f(a.m, 48), lane_f(a.s, 48)});
+  return lse_merge_fast(r0, r1);
 }
 
 // Block-wide merge of one Lse per thread; the result is valid in every thread.
@@ -695,7 +721,7 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_wave_kernel(
   float m = -INFINITY;
 #pragma unroll
   for (int u = 0; u < kWideLoads; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = wave_max_f(m);
   // the wave's own class sums: only this wave writes them, and LDS
   // operations of one wave complete in order, so a wave fence orders the
   // zeroing above before the atomics
@@ -721,7 +747,7 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_wave_kernel(
       one(x[u].w, k[u].y >> 16);
     }
   }
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  sum = wave_sum_f(sum);
   if (lane == 0) {
     wm[w] = m;
     wl[w] = sum;
@@ -838,14 +864,14 @@ __global__ __launch_bounds__(kPriorThreads) void prior_stats_list_kernel(
   float m = -INFINITY;
 #pragma unroll
   for (int u = 0; u < kWideLoads; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = wave_max_f(m);
   float sum = 0.0f;
   if (m != -INFINITY) {
 #pragma unroll
     for (int u = 0; u < kWideLoads; ++u)
       sum += (exp_shift(x[u].x, m) + exp_shift(x[u].y, m)) + (exp_shift(x[u].z, m) + exp_shift(x[u].w, m));
   }
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  sum = wave_sum_f(sum);
 #pragma unroll
   for (int u = 0; u < kWideLoads; ++u) xs[u * kPriorThreads + threadIdx.x] = x[u];
   if (lane == 0) {
