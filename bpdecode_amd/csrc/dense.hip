@@ -163,6 +163,23 @@ __device__ __forceinline__ int32_t advance_one(const int32_t* __restrict__ tok_n
   return tok_next[int64_t(s) * vocab + t];
 }
 
+// advance_one with the token id already read (raw: negative ids index from
+// the end)
+__device__ __forceinline__ int32_t advance_tok(const int32_t* __restrict__ tok_next, int32_t num_states,
+                                               int64_t vocab, int32_t s, int64_t t, int32_t* __restrict__ err) {
+  if (t < 0) t += vocab;
+  if (t < 0 || t >= vocab) {
+    if (err) atomicOr(err, BPD_FLAG_TOKEN_RANGE);
+    return -1;
+  }
+  if (s >= num_states) {
+    if (err) atomicOr(err, BPD_FLAG_STATE_RANGE);
+    return -1;
+  }
+  if (s < 0) return -1;
+  return tok_next[int64_t(s) * vocab + t];
+}
+
 constexpr int kAdvThreads = 1024;
 constexpr int kAdvPerThread = 4;
 
@@ -179,24 +196,34 @@ __global__ __launch_bounds__(kAdvThreads) void dense_advance_block_kernel(
     int32_t* __restrict__ err) {
   __shared__ int64_t pslot[BPD_MAX_FUSED_PENDING];
   __shared__ int32_t pval[BPD_MAX_FUSED_PENDING];
+  // every load that does not need the queued writes is issued before they
+  // are staged: each row's slot and token, then the slot's state (one chain
+  // of two dependent loads beside the staging instead of after it)
+  int64_t slot[kAdvPerThread], tk[kAdvPerThread];
+#pragma unroll
+  for (int i = 0; i < kAdvPerThread; ++i) {
+    const int64_t b = int64_t(i) * kAdvThreads + threadIdx.x;
+    slot[i] = b < rows ? (slots ? slots[b] : b) : -1;
+    tk[i] = b < rows ? read_token(tokens, tok_dtype, b) : 0;
+  }
+  int32_t st[kAdvPerThread];
+#pragma unroll
+  for (int i = 0; i < kAdvPerThread; ++i) st[i] = slot[i] >= 0 ? states[slot[i]] : 0;
   for (int32_t i = threadIdx.x; i < num_pending; i += kAdvThreads) {
     pslot[i] = pending[i];
     pval[i] = int32_t(pending[num_pending + i]);
   }
   __syncthreads();
   int32_t nxt[kAdvPerThread];
-  int64_t slot[kAdvPerThread];
 #pragma unroll
   for (int i = 0; i < kAdvPerThread; ++i) {
     const int64_t b = int64_t(i) * kAdvThreads + threadIdx.x;
     nxt[i] = -1;
-    slot[i] = -1;
     if (b < rows) {
-      slot[i] = slots ? slots[b] : b;
-      int32_t s = states[slot[i]];
+      int32_t s = st[i];
       for (int32_t k = 0; k < num_pending; ++k)
         if (pslot[k] == slot[i]) s = pval[k];
-      nxt[i] = advance_one(tok_next, num_states, vocab, s, tokens, tok_dtype, b, err);
+      nxt[i] = advance_tok(tok_next, num_states, vocab, s, tk[i], err);
       if (next_out) next_out[b] = nxt[i];
     }
   }
