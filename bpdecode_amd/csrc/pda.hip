@@ -1188,6 +1188,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     __syncthreads();
     const int n = nreq < kMemoReq ? nreq : kMemoReq;
+    // with at most one request per wave, request r is computed by wave r and
+    // its result stays in that wave's LDS buffer until the round ends (no
+    // copy to the workspace's candidate slots)
+    const bool in_work = n <= kMemoThreads / kWave;
+    auto cand_words = [&](int r) -> const int32_t* { return in_work ? work[r][1] : cand + r * kConfigWords; };
     if (n > kMemoThreads / kWave) {
       // the requests a wave steps (no frame-list composition) first: waves
       // take requests r = wave, wave + 16, ..., so each wave gets at most
@@ -1343,7 +1348,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
             cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0) | (lbase << kListBase)) : -1;
             cand_comp[r] = code >= 0 ? 1 : 0;
           }
-          if (found == -2) {
+          if (found == -2 && !in_work) {
             int32_t* out = cand + r * kConfigWords;
             for (int k = lane; k < kConfigWords; k += kWave) out[k] = wdst[k];
           }
@@ -1366,7 +1371,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       for (int r = wave; r < n; r += kMemoThreads / kWave) {
         if (cand_res[r] != -2) continue;
         const uint32_t h = cand_hash[r];
-        const int32_t* mine = cand + r * kConfigWords;
+        const int32_t* mine = cand_words(r);
         int lead = r;
         for (int j0 = 0; j0 < r && lead == r; j0 += kWave) {
           const int j = j0 + lane;
@@ -1374,7 +1379,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           while (m != 0u && lead == r) {
             const int k = j0 + __ffsll(static_cast<unsigned long long>(m)) - 1;
             m &= m - 1;
-            if (coop_same(mine, cand + k * kConfigWords, lane)) lead = k;
+            if (coop_same(mine, cand_words(k), lane)) lead = k;
           }
         }
         if (lane == 0) cand_lead[r] = lead;
@@ -1442,7 +1447,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (cand_res[r] != -2 || cand_lead[r] != r || cand_id[r] < 0) continue;
         // the set's words are loaded first and stored last, so the load
         // waits behind the interval and frame-list work
-        const int32_t* src = cand + r * kConfigWords;
+        const int32_t* src = cand_words(r);
         int32_t* dst = pool + cand_id[r] * kConfigWords;
         int32_t words[kSetLoads];
 #pragma unroll
