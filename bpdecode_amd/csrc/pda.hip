@@ -183,7 +183,9 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
 constexpr int kMemoThreads = 1024;
 constexpr int kMemoSets = 128;
 constexpr int kMemoReq = 128;
-constexpr int kMemoTok = 4;
+// tokens a thread walks per tile (1: the walk's registers then fit without
+// spilling in the walk loops; 2 and 4 measured 154 and 163 us per mask)
+constexpr int kMemoTok = 1;
 constexpr int kMemoMaxVocab = 262144;  // verdict bitmap of a row in LDS
 constexpr uint8_t kTUnknown = 0xFE;
 constexpr uint8_t kTDead = 0xFF;
@@ -1770,7 +1772,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     const int rn = run_n, rtop = run_top;
     if (!overflowed) {
       // the records of the next tile are loaded while this one is walked;
-      // queue entries are stored after all four walks of a tile
+      // queue entries are stored after all kMemoTok walks of a tile
       constexpr int64_t kTile = int64_t(kMemoThreads) * kMemoTok;
       int2 nm[kMemoTok];
       uint4 npk[kMemoTok];
