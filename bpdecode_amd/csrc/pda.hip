@@ -1782,6 +1782,17 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       // the live runs, the last run whose prefix is <= i is found by binary
       // lifting, the four searches of a thread interleaved (one LDS wait per
       // step); the total after the last run stops every step at it.
+      // mode 2: the seed entries (walk positions) are read a tile ahead of
+      // the records they index, so a tile's record loads never wait for its
+      // seed loads
+      int32_t seed_next[kMemoTok];
+      auto load_seeds = [&](int64_t base) {
+#pragma unroll
+        for (int j = 0; j < kMemoTok; ++j) {
+          const int64_t i = base + int64_t(j) * kMemoThreads + tid;
+          seed_next[j] = mode == 2 && i < P ? a.frames.seeds[pass_base + i] : -1;
+        }
+      };
       auto prefetch = [&](int64_t base) {
         int32_t ii[kMemoTok], lo[kMemoTok];
 #pragma unroll
@@ -1805,7 +1816,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           if (k >= 0 && mode == 1) {
             k = grp_start[lo[j]] + (k - grp_pre[lo[j]]);
           } else if (k >= 0 && mode == 2) {
-            k = a.frames.seeds[pass_base + k];
+            k = seed_next[j];
             k = k >= 0 && k < V ? k : -1;
           }
           nk[j] = k;
@@ -1813,7 +1824,9 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           npk[j] = k >= 0 ? ws.recs[k] : make_uint4(0u, 0u, 0u, 0u);
         }
       };
+      load_seeds(0);
       prefetch(0);
+      load_seeds(kTile);
       for (int64_t tile = 0; tile < P; tile += kTile) {
         int32_t tt[kMemoTok], pos[kMemoTok], len[kMemoTok], kk[kMemoTok];
         int cur[kMemoTok];
@@ -1838,6 +1851,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           }
         }
         prefetch(tile + kTile);
+        load_seeds(tile + 2 * kTile);
         // the leading bytes that keep set 0 (a string loop's body) are
         // checked together, with independent table reads, and the walk
         // starts at the first other byte
