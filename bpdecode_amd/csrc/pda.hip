@@ -1645,15 +1645,24 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (pos < n16 && walking(cur) && !step(cur, pos, packed_byte(pk, pos))) return true;
       }
       if (pos < len && walking(cur)) {
+        // the bytes past the record, 16 at a time, each group read with
+        // independent loads and packed like a record
         const uint8_t* tb = a.tok_bytes + a.tok_off[t];
         while (pos < len && walking(cur)) {
-          while (cur < kWalkEnd && pos < len) {
-            const uint8_t nx = T[cur * 256 + tb[pos]];
-            if (nx >= kTOverflow) break;
-            cur = nx;
-            ++pos;
+          uint32_t w4[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int i = 0; i < 16; ++i) w4[i >> 2] |= (pos + i < len ? uint32_t(tb[pos + i]) : 0u) << (8 * (i & 3));
+          const uint4 ck = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          const int p0 = pos, pe = len < pos + 16 ? len : pos + 16;
+          while (pos < pe && walking(cur)) {
+            while (cur < kWalkEnd && pos < pe) {
+              const uint8_t nx = T[cur * 256 + packed_byte(ck, pos - p0)];
+              if (nx >= kTOverflow) break;
+              cur = nx;
+              ++pos;
+            }
+            if (pos < pe && walking(cur) && !step(cur, pos, packed_byte(ck, pos - p0))) return true;
           }
-          if (pos < len && walking(cur) && !step(cur, pos, int(tb[pos]))) return true;
         }
       }
       if (walking(cur)) cur = kAllowed;
