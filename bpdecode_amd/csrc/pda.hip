@@ -21,6 +21,8 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #include "bpd_common.hpp"
@@ -54,6 +56,13 @@ struct MaskArgs {
   const int32_t* order;      // memo walk order (null: id order)
   const int32_t* runs;       // first-byte runs of order (null: none)
   BpdPdaFrames frames;       // num_lists 0: no frame lists
+  // the launch after a memoised mask (only_rows set): the workspace header
+  // (the pack key is stamped there, the deferred slots read), the deferred
+  // rows' verdict bits (null: none), the mask launch's generation and pack key
+  uint32_t* header;
+  const uint32_t* defer_bits;
+  uint32_t gen;
+  uint64_t pkey;
 };
 
 // Structural check of a row's config-set before any table lookup with its
@@ -78,14 +87,13 @@ __device__ bool config_ok(const int32_t* c, int32_t num_states, int lane) {
   return __ballot(!ok) == 0;
 }
 
-__global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
+// Chunk `blockIdx.x` of row b's verdicts by one wave.
+__device__ void mask_row_chunk(const MaskArgs& a, int64_t b) {
   __shared__ int32_t row_cfg[kConfigWords];
   __shared__ uint32_t lane_sets[2 * kLaneWords * kWave];
   __shared__ uint32_t first_ok[8];
 
-  const int64_t b = blockIdx.y;
   const int lane = threadIdx.x;
-  if (a.only_rows && a.only_rows[b] == 0) return;
   const int64_t row = a.slots ? a.slots[b] : b;
   for (int k = lane; k < kConfigWords; k += kWave) row_cfg[k] = a.configs[row * kConfigWords + k];
   __syncthreads();
@@ -160,6 +168,7 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
       }
     }
   }
+  __syncthreads();  // the LDS arrays are reused by the next row of the block
 }
 
 // ------------------------------------------------------- memoised mask --
@@ -251,7 +260,11 @@ __device__ __forceinline__ uint32_t lt_hash(uint32_t key) {
 
 struct MemoWs {
   uint32_t* header;   // [64]: word 0 = generation of the last mask launch on this workspace,
-                      // words 2-3 = pack key of the token records it walked (0: none)
+                      // words 2-3 = pack key of the token records it walked (0: none),
+                      // word kFinishWord = running count of rows that reached their logits,
+                      // word kFinishWord + 1 = its value when the last mask launch began,
+                      // words kDeferWord + 2k.. (64 bits) = generation << 32 | row of
+                      // deferred write slot k
   int32_t* pool;      // [rows, kMemoSets, kConfigWords]
   int32_t* cand;      // [rows, kMemoReq, kConfigWords]
   int32_t* overflow;  // [rows]
@@ -265,9 +278,23 @@ struct MemoWs {
   uint2* lt;          // [rows, kLT]: the row's boundary table after the mask (key, entry;
                       // entry | kTExact where the step's raw words are the set's)
   int32_t* slist;     // [rows, kMemoSets]: frame-list word of each interned set (-1: none)
+  uint32_t* defer;    // [kDefer, kMemoMaxVocab / 32]: verdict bits of the deferred rows
 };
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// The last kDefer rows of a logits launch to finish their walk leave the
+// logits write to the launch after it (pda_mask_kernel), which spreads each
+// row over kDeferBlocks one-wave blocks: one block writes a row at the store
+// rate of one CU, and these rows end after every other row has written its
+// own.  The slots carry the launch's generation and the finish count runs
+// on (the launch after a mask copies it as the next launch's base), so no
+// launch has to clear them.
+constexpr int kDefer = 8;
+constexpr int kDeferBlocks = 64;
+constexpr int kFinishWord = 8;
+constexpr int kDeferWord = 16;
+static_assert(kDeferWord + 2 * kDefer <= 64, "deferred slots in the workspace header");
 
 // Entries of each of a row's two queue buffers: the whole vocab up to 4096
 // tokens, a quarter of it above, at most kQueueMax (a row that pauses more
@@ -292,7 +319,7 @@ size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
   return 256 + sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
          v * sizeof(int2) + r * 2 * size_t(queue_cap(vocab)) * sizeof(uint2) + r * kLT * sizeof(uint2) +
-         r * kMemoSets * sizeof(int32_t);
+         align256(r * kMemoSets * sizeof(int32_t)) + size_t(kDefer) * (kMemoMaxVocab / 32) * sizeof(uint32_t);
 }
 
 MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
@@ -317,6 +344,8 @@ MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   w.lt = reinterpret_cast<uint2*>(p);
   p += r * kLT * sizeof(uint2);
   w.slist = reinterpret_cast<int32_t*>(p);
+  p += align256(r * kMemoSets * sizeof(int32_t));
+  w.defer = reinterpret_cast<uint32_t*>(p);
   return w;
 }
 
@@ -364,22 +393,9 @@ uint64_t pack_key(const BpdTokenBytes* toks, int64_t rows) {
   return h ? h : 1;
 }
 
-// Token records in walk order (k -> t = order[k], or t = k): recs[k] = the
-// first 16 bytes of t (little-endian words, zero padded), meta[k] = (t,
-// length of t), so the walks read them coalesced.  Nothing to do when the
-// workspace header carries this launch's pack key: the last mask launch on
-// the workspace walked records of the same tables at the same place, and
-// nothing but a pack writes there.
-__global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restrict__ off,
-                                                          const uint8_t* __restrict__ bytes,
-                                                          const int32_t* __restrict__ order,
-                                                          int32_t vocab, uint4* __restrict__ recs,
-                                                          int2* __restrict__ meta,
-                                                          const uint32_t* __restrict__ header,
-                                                          uint64_t key) {
-  if (key != 0 && header[2] == uint32_t(key) && header[3] == uint32_t(key >> 32)) return;
-  const int32_t k = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x);
-  if (k >= vocab) return;
+// Record k of the token records below.
+__device__ __forceinline__ void pack_record(const int32_t* off, const uint8_t* bytes, const int32_t* order, int32_t k,
+                                            uint4* recs, int2* meta) {
   const int32_t t = order ? order[k] : k;
   const int32_t s = off[t];
   const int32_t len = off[t + 1] - s;
@@ -388,6 +404,25 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restr
   for (int i = 0; i < n; ++i) w[i >> 2] |= uint32_t(bytes[s + i]) << ((i & 3) * 8);
   recs[k] = make_uint4(w[0], w[1], w[2], w[3]);
   meta[k] = make_int2(t, len);
+}
+
+// Token records in walk order (k -> t = order[k], or t = k): recs[k] = the
+// first 16 bytes of t (little-endian words, zero padded), meta[k] = (t,
+// length of t), so the walks read them coalesced.  Nothing to do when the
+// workspace header carries this launch's pack key: the last mask launch on
+// the workspace walked records of the same tables at the same place, and
+// nothing but a pack writes there (the key is stamped by the launch after
+// the mask, once every record is written).
+__global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restrict__ off,
+                                                          const uint8_t* __restrict__ bytes,
+                                                          const int32_t* __restrict__ order,
+                                                          int32_t vocab, uint4* __restrict__ recs,
+                                                          int2* __restrict__ meta,
+                                                          const uint32_t* __restrict__ header,
+                                                          uint64_t key) {
+  if (key != 0 && header[2] == uint32_t(key) && header[3] == uint32_t(key >> 32)) return;
+  for (int32_t k = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x); k < vocab; k += int32_t(gridDim.x) * 256)
+    pack_record(off, bytes, order, k, recs, meta);
 }
 
 __device__ inline int packed_byte(const uint4& p, int i) {
@@ -1013,31 +1048,31 @@ __device__ PdaTableView stage_tables(const PdaTableView& src, int32_t* tab, cons
 // verdicts of a token in the memoised walk, past every set id
 constexpr int kWalkEnd = 256, kAllowed = 256, kRejected = 257, kNone = 258;
 
-// The fill value into the rejected columns of a logits row of E-byte
-// elements (allowed columns: set bits of vb, V columns), by the kMemoThreads
-// threads of a block: one column per lane, 64 consecutive columns per wave
-// and step, eight steps per batch with the batch's verdict words read first,
-// so a step is one masked, coalesced store.  Measured on one row of 151,936
-// fp32 columns whose 2.5 % allowed columns are spread over every 256-column
-// group: 9.1 us, where a group of four columns per lane with per-column
-// stores in mixed groups takes 17.2 us; a row whose destination is not
-// in L2 is bound by the stores a wave keeps in flight, so the batch issues
-// them back to back.
-template <int E>
-__device__ __forceinline__ void write_rejected(uint8_t* rowp, const uint32_t* vb, int V, uint32_t fill,
+// The fill value into the rejected columns [lo, hi) of a logits row of
+// E-byte elements (allowed columns: set bits of vb, indexed by column; lo a
+// multiple of 64), by the T threads of a block: one column per lane, 64
+// consecutive columns per wave and step, eight steps per batch with the
+// batch's verdict words read first, so a step is one masked, coalesced store.
+// Measured on one row of 151,936 fp32 columns whose 2.5 % allowed columns
+// are spread over every 256-column group, by 1024 threads: 9.1 us, where a
+// group of four columns per lane with per-column stores in mixed groups
+// takes 17.2 us; a row whose destination is not in L2 is bound by the
+// stores a wave keeps in flight, so the batch issues them back to back.
+template <int E, int T>
+__device__ __forceinline__ void write_rejected(uint8_t* rowp, const uint32_t* vb, int lo, int hi, uint32_t fill,
                                                int tid) {
   const int lane = tid & (kWave - 1);
   constexpr int kBatch = 8;
-  for (int c0 = tid - lane; c0 < V; c0 += kBatch * kMemoThreads) {
+  for (int c0 = lo + tid - lane; c0 < hi; c0 += kBatch * T) {
     uint32_t w[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int c = c0 + u * kMemoThreads + lane;
-      w[u] = c < V ? vb[c >> 5] : 0xFFFFFFFFu;
+      const int c = c0 + u * T + lane;
+      w[u] = c < hi ? vb[c >> 5] : 0xFFFFFFFFu;
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int c = c0 + u * kMemoThreads + lane;
+      const int c = c0 + u * T + lane;
       if (((w[u] >> (c & 31)) & 1u) == 0u) {
         if (E == 2)
           *reinterpret_cast<uint16_t*>(rowp + c * 2) = uint16_t(fill & 0xFFFFu);
@@ -1054,7 +1089,7 @@ __device__ __forceinline__ void write_rejected(uint8_t* rowp, const uint32_t* vb
 template <bool InLds>
 __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a, MemoWs ws, int max_sets,
                                                                      uint64_t tag, uint32_t gen, int row_mode,
-                                                                     uint64_t pkey, int lt_cap) {
+                                                                     uint64_t pkey, int lt_cap, int pack_here) {
   extern __shared__ __align__(16) int32_t tab[];  // grammar tables when they fit
   __shared__ int32_t set_tops[kMemoSets][kMaxConfigs];  // top state per config, -1 if empty
   __shared__ int32_t set_n[kMemoSets];
@@ -1106,11 +1141,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   const int64_t row = a.slots ? a.slots[b] : b;
   int32_t* pool = ws.pool + b * kMemoSets * kConfigWords;
   int32_t* cand = ws.cand + b * kMemoReq * kConfigWords;
-  if (b == 0 && tid == 0) {
-    // the records this launch walks (the pack before it has finished)
-    ws.header[2] = uint32_t(pkey);
-    ws.header[3] = uint32_t(pkey >> 32);
-  }
+  // the pack key of the records in the workspace (stamped only by the launch
+  // after a mask, so no block of this launch sees another's stamp)
+  const uint32_t hdr_key0 = ws.header[2], hdr_key1 = ws.header[3];
+  // the finish count when this launch began (copied by the launch after the
+  // last mask; a workspace of unknown content only loses the deferral)
+  const uint32_t finish_base = ws.header[kFinishWord + 1];
 
   // the prologue's global reads (the row's set, the frame lists' slot
   // table, the first slice of the grammar tables) are issued first and
@@ -1557,6 +1593,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   // tile.  A row whose sets overflow the pool, that pauses a token of 65536
   // bytes or more, or that pauses more tokens in one pass than a queue
   // buffer holds, starts again in tile mode.
+  // with no pack launched before this one and records of other tables (or
+  // none) in the workspace, every block packs all of them itself before it
+  // walks any: blocks write identical values, so a block reads its own
+  // writes or equal ones
+  if (pack_here && (hdr_key0 != uint32_t(pkey) || hdr_key1 != uint32_t(pkey >> 32))) {
+    for (int32_t k = tid; k < a.vocab; k += kMemoThreads) pack_record(a.tok_off, a.tok_bytes, a.order, k, ws.recs, ws.tmeta);
+    __syncthreads();
+  }
   bool tiles = row_mode == 0;
   if (!tiles) {
     const int64_t Q = ws.qcap;
@@ -2085,12 +2129,85 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     for (int w = tid; w < vwords && w < a.words; w += kMemoThreads) a.bits[b * a.words + w] = vbits[w];
     return;
   }
-  // logits: the rejected columns get the fill value
+  // logits: the rejected columns get the fill value, here or -- for the
+  // last kDefer rows of the launch to get here -- by the deferred-write
+  // kernel from the row's verdict bits
+  __shared__ int defer_slot;
+  if (tid == 0) {
+    // this row's place among the launch's rows to get here: the running
+    // count less its value when the launch began (one atomic add, no retry
+    // loop: rows that finish together would serialise on a compare-and-swap)
+    const uint32_t order = atomicAdd(&ws.header[kFinishWord], 1u) - finish_base;
+    const int64_t first = a.rows > kDefer ? a.rows - kDefer : 0;
+    defer_slot = int64_t(order) >= first && int64_t(order) - first < kDefer ? int(int64_t(order) - first) : -1;
+  }
+  __syncthreads();
+  if (defer_slot >= 0) {
+    uint32_t* dst = ws.defer + int64_t(defer_slot) * (kMemoMaxVocab / 32);
+    for (int i = tid; i < vwords; i += kMemoThreads) dst[i] = vbits[i];
+    if (tid == 0)
+      *reinterpret_cast<unsigned long long*>(ws.header + kDeferWord + 2 * defer_slot) =
+          (static_cast<unsigned long long>(gen) << 32) | static_cast<unsigned long long>(b);
+    return;
+  }
   uint8_t* rowp = a.logits + b * a.ld_bytes;
   if (a.elem == 2)
-    write_rejected<2>(rowp, vbits, int(V), a.fill, tid);
+    write_rejected<2, kMemoThreads>(rowp, vbits, 0, int(V), a.fill, tid);
   else
-    write_rejected<4>(rowp, vbits, int(V), a.fill, tid);
+    write_rejected<4, kMemoThreads>(rowp, vbits, 0, int(V), a.fill, tid);
+}
+
+// Rows of a launch with only_rows set that a block of this kernel checks:
+// the flags of the block's rows are one load, so a launch whose rows are
+// mostly unflagged is short.
+constexpr int kOnlyRowsPerBlock = 16;
+
+// The direct mask: grid (chunks, rows), block (x, b) takes chunk x of row b.
+// After a memoised mask (only_rows set): grid (chunks, F + D) with F =
+// ceil(rows / kOnlyRowsPerBlock): block (x, y < F) takes chunk x of each
+// flagged row among rows [16 y, 16 y + 16), one after another; the blocks
+// y >= F, kDeferBlocks per slot in x-major order, write the logits of the
+// deferred slots' rows, each block a 64-column-aligned piece; block (0, 0)
+// stamps the pack key of the records the mask walked and the finish count
+// the next mask launch starts from.
+__global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
+  if (!a.only_rows) {
+    mask_row_chunk(a, blockIdx.y);
+    return;
+  }
+  const int64_t flag_rows = (a.rows + kOnlyRowsPerBlock - 1) / kOnlyRowsPerBlock;
+  if (int64_t(blockIdx.y) >= flag_rows) {
+    const int64_t e = (int64_t(blockIdx.y) - flag_rows) * gridDim.x + blockIdx.x;
+    const int k = int(e / kDeferBlocks), piece = int(e % kDeferBlocks);
+    if (!a.defer_bits || !a.logits || k >= kDefer) return;
+    const unsigned long long v = *reinterpret_cast<const unsigned long long*>(a.header + kDeferWord + 2 * k);
+    if (uint32_t(v >> 32) != a.gen) return;
+    const int64_t b = int64_t(uint32_t(v));
+    const int V = a.vocab;
+    const int per = (V + kDeferBlocks * kWave - 1) / (kDeferBlocks * kWave) * kWave;
+    const int lo = piece * per, hi = lo + per < V ? lo + per : V;
+    if (lo >= hi || b >= a.rows) return;
+    uint8_t* rowp = a.logits + b * a.ld_bytes;
+    const uint32_t* vb = a.defer_bits + int64_t(k) * (kMemoMaxVocab / 32);
+    if (a.elem == 2)
+      write_rejected<2, kWave>(rowp, vb, lo, hi, a.fill, int(threadIdx.x));
+    else
+      write_rejected<4, kWave>(rowp, vb, lo, hi, a.fill, int(threadIdx.x));
+    return;
+  }
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && a.header) {
+    a.header[2] = uint32_t(a.pkey);
+    a.header[3] = uint32_t(a.pkey >> 32);
+    a.header[kFinishWord + 1] = a.header[kFinishWord];
+  }
+  const int64_t b0 = int64_t(blockIdx.y) * kOnlyRowsPerBlock;
+  const int64_t bl = b0 + threadIdx.x;
+  uint64_t m = __ballot(threadIdx.x < kOnlyRowsPerBlock && bl < a.rows && a.only_rows[bl] != 0);
+  while (m != 0u) {
+    const int i = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    m &= m - 1;
+    mask_row_chunk(a, b0 + i);
+  }
 }
 
 struct AdvanceArgs {
@@ -2517,6 +2634,18 @@ extern "C" int bpd_pda_init(const BpdPdaTable* g, int32_t* config_out) {
   return BPD_OK;
 }
 
+// Whether this process launched the pack of key `key` into `workspace`
+// before (and records that it has now).
+static bool packed_before(const void* workspace, uint64_t key) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, uint64_t> last;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = last.find(workspace);
+  if (it != last.end() && it->second == key) return true;
+  last[workspace] = key;
+  return false;
+}
+
 static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, const int32_t* configs,
                            const int64_t* slots, const uint8_t* broken, int64_t rows,
                            void* logits, int dtype, int64_t ld, double neg_inf, uint32_t* bits,
@@ -2565,9 +2694,18 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     BPD_REQUIRE(workspace_bytes >= need, "workspace too small (%zu < %zu bytes)", workspace_bytes, need);
     const MemoWs ws = memo_ws(workspace, rows, toks->vocab_size);
     const uint64_t pkey = pack_key(toks, rows);
-    pack_tokens_kernel<<<unsigned((toks->vocab_size + 255) / 256), 256, 0, as_stream(stream)>>>(
-        toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta, ws.header, pkey);
-    BPD_LAUNCHED();
+    // the records are packed by a launch of their own the first time this
+    // process masks with this key on this workspace; after that the mask
+    // checks the workspace's stamp itself and, should another key be there
+    // (the memory was reused), every block packs the records before walking
+    const bool pack_launch = !packed_before(workspace, pkey);
+    if (pack_launch) {
+      // at most one block per CU
+      const int64_t pack_blocks = std::min<int64_t>((int64_t(toks->vocab_size) + 255) / 256, 256);
+      pack_tokens_kernel<<<unsigned(pack_blocks), 256, 0, as_stream(stream)>>>(
+          toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta, ws.header, pkey);
+      BPD_LAUNCHED();
+    }
     // BPD_PDA_MEMO_SETS lowers the interned-set limit (tests of the overflow path)
     int max_sets = kMemoIds;
     if (const char* e = std::getenv("BPD_PDA_MEMO_SETS")) {
@@ -2592,12 +2730,16 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
     }
     if (tab_bytes <= room)
       pda_memo_mask_kernel<true><<<unsigned(rows), kMemoThreads, tab_bytes, as_stream(stream)>>>(
-          a, ws, max_sets, tag, gen, row_mode, pkey, lt_cap);
+          a, ws, max_sets, tag, gen, row_mode, pkey, lt_cap, pack_launch ? 0 : 1);
     else
       pda_memo_mask_kernel<false><<<unsigned(rows), kMemoThreads, 0, as_stream(stream)>>>(
-          a, ws, max_sets, tag, gen, row_mode, pkey, lt_cap);
+          a, ws, max_sets, tag, gen, row_mode, pkey, lt_cap, pack_launch ? 0 : 1);
     BPD_LAUNCHED();
     a.only_rows = ws.overflow;  // rows that ran out of interned sets
+    a.header = ws.header;
+    a.defer_bits = a.logits ? ws.defer : nullptr;
+    a.gen = gen;
+    a.pkey = pkey;
     // rows that overflow are rare: four waves per row keep short a launch
     // whose blocks mostly read their flag and exit
     if (chunks > 4) {
@@ -2607,7 +2749,12 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
       a.chunk_tokens = int32_t(per);
     }
   }
-  pda_mask_kernel<<<dim3(unsigned(chunks), unsigned(rows)), dim3(kWave), 0, as_stream(stream)>>>(a);
+  int64_t grid_rows = rows;
+  if (a.only_rows) {
+    grid_rows = (rows + kOnlyRowsPerBlock - 1) / kOnlyRowsPerBlock;
+    if (a.defer_bits) grid_rows += (int64_t(kDefer) * kDeferBlocks + chunks - 1) / chunks;
+  }
+  pda_mask_kernel<<<dim3(unsigned(chunks), unsigned(grid_rows)), dim3(kWave), 0, as_stream(stream)>>>(a);
   BPD_LAUNCHED();
   return BPD_OK;
 }

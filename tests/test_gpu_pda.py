@@ -713,3 +713,44 @@ def test_token_records_of_two_vocabularies_one_workspace(dev):
                                          ptr(ws), need, stream))
         assert np.array_equal(out.cpu().numpy().view(np.uint32), want), i
 
+
+
+def test_token_records_repacked_when_workspace_overwritten(dev, json_case):
+    """Masks through the C ABI on one workspace that is overwritten between
+    calls (0xAB in every byte, the pack stamp included): the first call packs
+    the token records in a launch of its own; the next finds this workspace
+    and key already packed by this process, so the mask checks the stamp
+    itself, finds garbage and packs the records in every block before
+    walking; the third takes them as they are.  Bits and fp32 logits at
+    B=16, V=151,936 (the last eight rows to finish leave their logits to the
+    launch after the mask), each call against the oracle."""
+    from bpdecode_amd._lib import DTYPE_F32, check, lib, ptr
+
+    vocab, g, t = json_case
+    gd = g.to(dev)
+    B, V = 16, g.vocab_size
+    cfgs = _json_configs(g, B, seed=97)
+    pool = cfgs.to(dev)
+    want_bits = OP.compute_mask(t, cfgs.numpy())
+    need = int(lib().bpd_pda_workspace_bytes(B, V))
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for mode in ("bits", "logits"):
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+        for call in ("packs", "overwritten", "packed"):
+            _log(f"case repack {mode} {call}")
+            if call == "overwritten":
+                ws.fill_(0xAB)
+                torch.cuda.synchronize(dev)
+            if mode == "bits":
+                out = torch.empty((B, (V + 31) // 32), dtype=torch.int32, device=dev)
+                check(lib().bpd_pda_compute_mask(gd.c_table(), gd.c_tokens(), ptr(pool), None, B, ptr(out),
+                                                 ptr(ws), need, stream))
+                assert np.array_equal(out.cpu().numpy().view(np.uint32), want_bits), call
+            else:
+                lg = synth.logits(B, V, 3.0, torch.float32, seed=5)
+                got = lg.to(dev)
+                check(lib().bpd_pda_apply_mask(gd.c_table(), gd.c_tokens(), ptr(pool), None, None, B, ptr(got),
+                                               DTYPE_F32, V, float("-inf"), ptr(ws), need, stream))
+                ref = lg.numpy().copy()
+                OP.apply_mask(t, cfgs.numpy(), ref)
+                assert np.array_equal(got.cpu().numpy(), ref), call
