@@ -1764,15 +1764,26 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       // every interval of set 0 first, so the first pass already steps past
       // byte 0; of a set in a frame list only the boundary intervals (the
       // others are walked as its list state or were filled from the list)
-      if (tid < 8) {
-        uint32_t m = (set_bnd[0][tid] | (tid == 0 ? 1u : 0u)) & set_hit[0][tid];
-        if (row_list >= 0) {
-          for (uint32_t x = m; x != 0u; x &= x - 1u) {
-            const int c = tid * 32 + __ffs(x) - 1;
-            if (T[c] != kTUnknown || a.frames.trans[row_list * 256 + c] != -2) m &= ~(1u << (c & 31));
-          }
+      // (wave 0: lane l takes bytes l, 64 + l, 128 + l, 192 + l, the list's
+      // codes for them read at once; four ballots are the eight request
+      // words, each stored by the thread that collects it)
+      if (tid < kWave) {
+        int code[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) code[q] = row_list >= 0 ? a.frames.trans[row_list * 256 + q * kWave + tid] : -2;
+        uint64_t m[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = q * kWave + tid;
+          const bool start = c == 0 || ((set_bnd[0][c >> 5] >> (c & 31)) & 1u) != 0u;
+          bool want = start && ((set_hit[0][c >> 5] >> (c & 31)) & 1u) != 0u;
+          if (row_list >= 0) want = want && T[c] == kTUnknown && code[q] == -2;
+          m[q] = __ballot(want);
         }
-        req[tid] = m;
+        if (tid < 8) {
+          const uint64_t mq = tid < 2 ? m[0] : (tid < 4 ? m[1] : (tid < 6 ? m[2] : m[3]));
+          req[tid] = uint32_t(mq >> (32 * (tid & 1)));
+        }
       }
       resolve();
     }
@@ -2180,19 +2191,41 @@ __global__ __launch_bounds__(kWave) void pda_mask_kernel(MaskArgs a) {
     const int64_t e = (int64_t(blockIdx.y) - flag_rows) * gridDim.x + blockIdx.x;
     const int k = int(e / kDeferBlocks), piece = int(e % kDeferBlocks);
     if (!a.defer_bits || !a.logits || k >= kDefer) return;
-    const unsigned long long v = *reinterpret_cast<const unsigned long long*>(a.header + kDeferWord + 2 * k);
-    if (uint32_t(v >> 32) != a.gen) return;
-    const int64_t b = int64_t(uint32_t(v));
     const int V = a.vocab;
     const int per = (V + kDeferBlocks * kWave - 1) / (kDeferBlocks * kWave) * kWave;
     const int lo = piece * per, hi = lo + per < V ? lo + per : V;
-    if (lo >= hi || b >= a.rows) return;
-    uint8_t* rowp = a.logits + b * a.ld_bytes;
+    if (lo >= hi) return;
+    // the slot's verdict words of the piece's first eight steps are read
+    // beside the slot word (the slot's bits exist whether or not it is set)
     const uint32_t* vb = a.defer_bits + int64_t(k) * (kMemoMaxVocab / 32);
-    if (a.elem == 2)
-      write_rejected<2, kWave>(rowp, vb, lo, hi, a.fill, int(threadIdx.x));
-    else
-      write_rejected<4, kWave>(rowp, vb, lo, hi, a.fill, int(threadIdx.x));
+    const int lane = int(threadIdx.x);
+    uint32_t w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = lo + u * kWave + lane;
+      w[u] = c < hi ? vb[c >> 5] : 0xFFFFFFFFu;
+    }
+    const unsigned long long v = *reinterpret_cast<const unsigned long long*>(a.header + kDeferWord + 2 * k);
+    if (uint32_t(v >> 32) != a.gen) return;
+    const int64_t b = int64_t(uint32_t(v));
+    if (b >= a.rows) return;
+    uint8_t* rowp = a.logits + b * a.ld_bytes;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = lo + u * kWave + lane;
+      if (((w[u] >> (c & 31)) & 1u) == 0u) {
+        if (a.elem == 2)
+          *reinterpret_cast<uint16_t*>(rowp + c * 2) = uint16_t(a.fill & 0xFFFFu);
+        else
+          *reinterpret_cast<uint32_t*>(rowp + c * 4) = a.fill;
+      }
+    }
+    if (lo + 8 * kWave < hi) {
+      if (a.elem == 2)
+        write_rejected<2, kWave>(rowp, vb, lo + 8 * kWave, hi, a.fill, lane);
+      else
+        write_rejected<4, kWave>(rowp, vb, lo + 8 * kWave, hi, a.fill, lane);
+    }
     return;
   }
   if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && a.header) {
