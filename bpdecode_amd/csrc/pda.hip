@@ -2330,6 +2330,7 @@ __global__ __launch_bounds__(kCommitRows) void pda_advance_kernel(AdvanceArgs a)
 // token's bytes is then a chain of LDS reads, not of global ones); wave 0
 // commits the row.
 constexpr int kCommitThreads = 256;
+static_assert(kCommitThreads == 256, "a thread per byte stages the list's codes");
 
 // InLds: the grammar tables are staged in LDS (the dynamic array `ctab`), so
 // the closure of the commit's byte steps reads them from LDS.
@@ -2341,6 +2342,9 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   __shared__ uint4 trow[kMemoSets * 16];  // the row's table (256 bytes per set)
   __shared__ uint2 lrow[kLT];             // the row's boundary table
   __shared__ int32_t srow[kMemoSets];     // frame-list word of each interned set
+  __shared__ int32_t ltrans[256];         // byte codes of the frame list of the row's set (if any)
+  __shared__ int32_t lkey[BPD_PDA_FRAME_KEY_WORDS];  // and its key
+  __shared__ int row_l0;                  // that list (-1: none)
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t b = blockIdx.x;
   const int64_t row = a.slots ? a.slots[b] : b;
@@ -2383,15 +2387,27 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
 #pragma unroll
     for (int q = 0; q < kLT / kCommitThreads; ++q) lv[q] = ws.lt[b * kLT + q * kCommitThreads + threadIdx.x];
     const int32_t sv = threadIdx.x < kMemoSets ? ws.slist[b * kMemoSets + threadIdx.x] : -1;
+    // the list of the row's set (set 0 of the pool), its byte codes and key:
+    // the walk's list steps and the composed set mostly use that list
+    const int32_t sl0 = a.frames.num_lists > 0 ? ws.slist[b * kMemoSets] : -1;
+    const int l0 = sl0 >= 0 && (sl0 & (BPD_PDA_FRAME_SAT - 1)) < a.frames.num_lists ? (sl0 & (BPD_PDA_FRAME_SAT - 1)) : -1;
+    const int32_t ltv = l0 >= 0 ? a.frames.trans[int64_t(l0) * 256 + threadIdx.x] : -1;
+    const int32_t lkv = l0 >= 0 && threadIdx.x < BPD_PDA_FRAME_KEY_WORDS
+                            ? a.frames.keys[int64_t(l0) * BPD_PDA_FRAME_KEY_WORDS + threadIdx.x]
+                            : 0;
 #pragma unroll
     for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) trow[q * kCommitThreads + threadIdx.x] = v[q];
 #pragma unroll
     for (int q = 0; q < kLT / kCommitThreads; ++q) lrow[q * kCommitThreads + threadIdx.x] = lv[q];
     if (threadIdx.x < kMemoSets) srow[threadIdx.x] = sv;
+    ltrans[threadIdx.x] = ltv;
+    if (threadIdx.x < BPD_PDA_FRAME_KEY_WORDS) lkey[threadIdx.x] = lkv;
+    if (threadIdx.x == 0) row_l0 = l0;
   }
   const PdaTableView g = InLds ? stage_tables(a.g, ctab, tsl, int(threadIdx.x), kCommitThreads) : a.g;
   __syncthreads();
   if (threadIdx.x >= kWave) return;
+  const int own = row_l0;  // the list whose codes and key are staged
   bool ok;
   if (!t_in) {
     if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
@@ -2454,7 +2470,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
             if (sl < 0) break;  // not resolved by the mask: step from here
             cur = list_state(cur, sl);
           }
-          const int code = a.frames.trans[(cur & 0xFFF) * 256 + byte];
+          const int code = (cur & 0xFFF) == own ? ltrans[byte] : a.frames.trans[(cur & 0xFFF) * 256 + byte];
           if (code == -1) {
             cur = -2;
             break;
@@ -2503,7 +2519,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
             for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[anchor * kConfigWords + k];
             wave_sync();
           }
-          compose_list_set(x, x, a.frames.keys + int64_t(cur & 0xFFF) * BPD_PDA_FRAME_KEY_WORDS,
+          compose_list_set(x, x, (cur & 0xFFF) == own ? lkey : a.frames.keys + int64_t(cur & 0xFFF) * BPD_PDA_FRAME_KEY_WORDS,
                            srow[anchor] >> kListBase, (cur >> 12) & 1, lane);
         } else if (cur > 0) {
           for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[cur * kConfigWords + k];
@@ -2521,7 +2537,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
             int l = l0, sat = x[1] != 0 ? 1 : 0, code = 0;
             int32_t j = i;
             for (; j < e - 1; ++j) {
-              code = a.frames.trans[l * 256 + byte_at(j)];
+              code = l == own ? ltrans[byte_at(j)] : a.frames.trans[l * 256 + byte_at(j)];
               if (code < 0) break;
               l = code & (BPD_PDA_FRAME_SAT - 1);
               sat |= (code & BPD_PDA_FRAME_SAT) != 0 ? 1 : 0;
@@ -2529,7 +2545,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
             if (j < e - 1 && code == -1) {
               ok = false;  // the list (and so the set) empties at byte j
             } else if (j > i) {
-              compose_list_set(x, x, a.frames.keys + int64_t(l) * BPD_PDA_FRAME_KEY_WORDS, base, sat, lane);
+              compose_list_set(x, x, l == own ? lkey : a.frames.keys + int64_t(l) * BPD_PDA_FRAME_KEY_WORDS, base, sat, lane);
               i = j;
             }
           }
