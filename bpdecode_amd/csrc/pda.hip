@@ -226,19 +226,27 @@ constexpr int kReqLT = 1 << 30;          // request list: boundary entry `slot` 
 constexpr int kLC = 1024;
 static_assert(BPD_PDA_MAX_FRAME_LISTS < 2047, "list ids of the byte-table cache are 11 bits");
 
+// (the bytes of one list take distinct slots: 11 is odd)
+__device__ __forceinline__ int lc_slot(int l, int byte) {
+  return int((uint32_t(l) * 37u + uint32_t(byte) * 11u) & uint32_t(kLC - 1));
+}
+__device__ __forceinline__ uint32_t lc_entry(int l, int byte, int code) {
+  const uint32_t c = code == -1 ? 0x1FFFu
+                     : code < 0 ? 0x1FFEu
+                                : (uint32_t(code & 0x7FF) | ((code & BPD_PDA_FRAME_SAT) != 0 ? 0x800u : 0u));
+  return (uint32_t(l) << 21) | (uint32_t(byte) << 13) | c;
+}
+
 __device__ __forceinline__ int list_code(const BpdPdaFrames& f, uint32_t* lcache, int l, int byte) {
   const uint32_t tag = (uint32_t(l) << 21) | (uint32_t(byte) << 13);
-  const int slot = int((uint32_t(l) * 37u + uint32_t(byte) * 11u) & uint32_t(kLC - 1));
+  const int slot = lc_slot(l, byte);
   const uint32_t w = lcache[slot];
   if ((w & ~0x1FFFu) == tag) {
     const uint32_t c = w & 0x1FFFu;
     return c == 0x1FFFu ? -1 : c == 0x1FFEu ? -2 : int((c & 0x7FFu) | ((c & 0x800u) != 0u ? BPD_PDA_FRAME_SAT : 0));
   }
   const int code = f.trans[l * 256 + byte];
-  const uint32_t c = code == -1 ? 0x1FFFu
-                     : code < 0 ? 0x1FFEu
-                                : (uint32_t(code & 0x7FF) | ((code & BPD_PDA_FRAME_SAT) != 0 ? 0x800u : 0u));
-  lcache[slot] = tag | c;
+  lcache[slot] = lc_entry(l, byte, code);
   return code;
 }
 
@@ -1783,6 +1791,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (tid < 8) {
           const uint64_t mq = tid < 2 ? m[0] : (tid < 4 ? m[1] : (tid < 6 ? m[2] : m[3]));
           req[tid] = uint32_t(mq >> (32 * (tid & 1)));
+        }
+        // the same codes fill the list's entries of the byte-table cache
+        // (read by the walks after the round's barriers)
+        if (row_list >= 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) lcache[lc_slot(row_list, q * kWave + tid)] = lc_entry(row_list, q * kWave + tid, code[q]);
         }
       }
       resolve();
