@@ -276,11 +276,12 @@ struct MemoWs {
   int32_t* pool;      // [rows, kMemoSets, kConfigWords]
   int32_t* cand;      // [rows, kMemoReq, kConfigWords]
   int32_t* overflow;  // [rows]
-  int32_t* meta;      // [rows, 4]: valid, tag low, tag high, generation
+  int32_t* meta;      // [rows, 4]: interned sets (0: dead row), tag low, tag high, generation
   uint32_t* table;    // [rows, kMemoSets * 64]: the row's transition table after the mask
                       // (ids flagged kTExact where the step's raw words are the set's)
   uint4* recs;        // [vocab] first 16 bytes of the token at walk position k, zero padded
   int2* tmeta;        // [vocab] (token id, length) of the token at walk position k
+  uint4* trecs;       // [vocab] (length, first 12 bytes) of token t, by token id
   uint2* queue;       // [rows, 2, qcap] paused tokens of the row-wide walk (two buffers)
   int32_t qcap;       // entries per queue buffer (queue_cap)
   uint2* lt;          // [rows, kLT]: the row's boundary table after the mask (key, entry;
@@ -326,7 +327,8 @@ size_t memo_ws_bytes(int64_t rows, int64_t vocab) {
   const size_t r = size_t(rows > 0 ? rows : 0), v = size_t(vocab > 0 ? vocab : 0);
   const size_t sets = r * (kMemoSets + kMemoReq) * kConfigWords * sizeof(int32_t);
   return 256 + sets + align256(r * 4) + align256(r * 16) + r * kMemoSets * 256 + v * sizeof(uint4) +
-         v * sizeof(int2) + r * 2 * size_t(queue_cap(vocab)) * sizeof(uint2) + r * kLT * sizeof(uint2) +
+         v * sizeof(int2) + v * sizeof(uint4) + r * 2 * size_t(queue_cap(vocab)) * sizeof(uint2) +
+         r * kLT * sizeof(uint2) +
          align256(r * kMemoSets * sizeof(int32_t)) + size_t(kDefer) * (kMemoMaxVocab / 32) * sizeof(uint32_t);
 }
 
@@ -346,6 +348,8 @@ MemoWs memo_ws(void* base, int64_t rows, int64_t vocab) {
   p += size_t(vocab) * sizeof(uint4);
   w.tmeta = reinterpret_cast<int2*>(p);
   p += size_t(vocab) * sizeof(int2);
+  w.trecs = reinterpret_cast<uint4*>(p);
+  p += size_t(vocab) * sizeof(uint4);
   w.queue = reinterpret_cast<uint2*>(p);
   w.qcap = queue_cap(vocab);
   p += r * 2 * size_t(w.qcap) * sizeof(uint2);
@@ -401,9 +405,9 @@ uint64_t pack_key(const BpdTokenBytes* toks, int64_t rows) {
   return h ? h : 1;
 }
 
-// Record k of the token records below.
+// Record k of the token records below, and token t's record by id.
 __device__ __forceinline__ void pack_record(const int32_t* off, const uint8_t* bytes, const int32_t* order, int32_t k,
-                                            uint4* recs, int2* meta) {
+                                            uint4* recs, int2* meta, uint4* trecs) {
   const int32_t t = order ? order[k] : k;
   const int32_t s = off[t];
   const int32_t len = off[t + 1] - s;
@@ -412,11 +416,14 @@ __device__ __forceinline__ void pack_record(const int32_t* off, const uint8_t* b
   for (int i = 0; i < n; ++i) w[i >> 2] |= uint32_t(bytes[s + i]) << ((i & 3) * 8);
   recs[k] = make_uint4(w[0], w[1], w[2], w[3]);
   meta[k] = make_int2(t, len);
+  trecs[t] = make_uint4(uint32_t(len), w[0], w[1], w[2]);
 }
 
 // Token records in walk order (k -> t = order[k], or t = k): recs[k] = the
 // first 16 bytes of t (little-endian words, zero padded), meta[k] = (t,
-// length of t), so the walks read them coalesced.  Nothing to do when the
+// length of t), so the walks read them coalesced; trecs[t] = (length of t,
+// its first 12 bytes), so the commit has a short token's bytes one read
+// after the token id.  Nothing to do when the
 // workspace header carries this launch's pack key: the last mask launch on
 // the workspace walked records of the same tables at the same place, and
 // nothing but a pack writes there (the key is stamped by the launch after
@@ -425,12 +432,12 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(const int32_t* __restr
                                                           const uint8_t* __restrict__ bytes,
                                                           const int32_t* __restrict__ order,
                                                           int32_t vocab, uint4* __restrict__ recs,
-                                                          int2* __restrict__ meta,
+                                                          int2* __restrict__ meta, uint4* __restrict__ trecs,
                                                           const uint32_t* __restrict__ header,
                                                           uint64_t key) {
   if (key != 0 && header[2] == uint32_t(key) && header[3] == uint32_t(key >> 32)) return;
   for (int32_t k = int32_t(blockIdx.x) * 256 + int32_t(threadIdx.x); k < vocab; k += int32_t(gridDim.x) * 256)
-    pack_record(off, bytes, order, k, recs, meta);
+    pack_record(off, bytes, order, k, recs, meta, trecs);
 }
 
 __device__ inline int packed_byte(const uint4& p, int i) {
@@ -1606,7 +1613,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   // walks any: blocks write identical values, so a block reads its own
   // writes or equal ones
   if (pack_here && (hdr_key0 != uint32_t(pkey) || hdr_key1 != uint32_t(pkey >> 32))) {
-    for (int32_t k = tid; k < a.vocab; k += kMemoThreads) pack_record(a.tok_off, a.tok_bytes, a.order, k, ws.recs, ws.tmeta);
+    for (int32_t k = tid; k < a.vocab; k += kMemoThreads) pack_record(a.tok_off, a.tok_bytes, a.order, k, ws.recs, ws.tmeta, ws.trecs);
     __syncthreads();
   }
   bool tiles = row_mode == 0;
@@ -2143,7 +2150,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   }
   if (tid == 0) {
     ws.overflow[b] = overflowed;
-    ws.meta[b * 4 + 0] = dead_row ? 0 : 1;
+    ws.meta[b * 4 + 0] = dead_row ? 0 : (pool_count < max_sets ? pool_count : max_sets);
     ws.meta[b * 4 + 1] = int32_t(uint32_t(tag));
     ws.meta[b * 4 + 2] = int32_t(uint32_t(tag >> 32));
     ws.meta[b * 4 + 3] = int32_t(gen);
@@ -2350,11 +2357,10 @@ static_assert(kCommitThreads == 256, "a thread per byte stages the list's codes"
 // the closure of the commit's byte steps reads them from LDS.
 template <bool InLds>
 __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(AdvanceArgs a, MemoWs ws,
-                                                                         uint64_t tag) {
+                                                                         uint64_t tag, uint64_t pkey) {
   extern __shared__ __align__(16) int32_t ctab[];
   __shared__ int32_t bufs[2][kConfigWords];
   __shared__ uint4 trow[kMemoSets * 16];  // the row's table (256 bytes per set)
-  __shared__ uint2 lrow[kLT];             // the row's boundary table
   __shared__ int32_t srow[kMemoSets];     // frame-list word of each interned set
   __shared__ int32_t ltrans[256];         // byte codes of the frame list of the row's set (if any)
   __shared__ int32_t lkey[BPD_PDA_FRAME_KEY_WORDS];  // and its key
@@ -2366,12 +2372,17 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   int32_t* x = bufs[0];
   int32_t* y = bufs[1];
   // the reads wave 0 needs after the table is staged -- the token, its
-  // offsets and first 64 bytes, the workspace stamps, the pool's set 0 --
-  // are issued before the staging loads, so their round trips overlap them
+  // offsets and record (length and first 12 bytes: one read after the token
+  // id, where the bytes themselves are one more), the workspace stamps, the
+  // pool's set 0 -- are issued before the staging loads, so their round
+  // trips overlap them
   const int64_t t = read_token(a.tokens, a.tok_dtype, b);
   const bool t_in = t >= 0 && t < a.vocab;
   const bool walk_tok = t_in && t != a.eos;
-  const int32_t s = walk_tok ? a.tok_off[t] : 0, e = walk_tok ? a.tok_off[t + 1] : 0;
+  const uint32_t hk0 = ws.header[2], hk1 = ws.header[3];
+  const bool w0 = threadIdx.x < kWave;
+  const int32_t s = walk_tok && w0 ? a.tok_off[t] : 0, e = walk_tok && w0 ? a.tok_off[t + 1] : 0;
+  const uint4 tr = walk_tok && w0 ? ws.trecs[t] : make_uint4(0u, 0u, 0u, 0u);
   int32_t meta[4] = {0, 0, 0, 0};
   uint32_t hdr = 0;
   int32_t p0[kSetLoads];
@@ -2389,17 +2400,15 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
       }
     }
   }
-  // the token's first 64 bytes, one per lane
-  const int32_t bl = threadIdx.x < kWave && s + lane < e ? int32_t(a.tok_bytes[s + lane]) : 0;
   const TableSlice tsl = InLds ? table_slice(a.g, int(threadIdx.x)) : TableSlice{0, 0, 0, 0, 0, 0, 0, 0};
   {
+    // T rows of the first 16 sets, then (once the row's set count is read)
+    // those of the others the mask interned; the boundary table is probed
+    // where it lies (a commit rarely meets a boundary entry)
+    static_assert(kCommitThreads == 16 * 16, "one 16-byte piece of the first 16 T rows per thread");
     const uint4* src = reinterpret_cast<const uint4*>(ws.table + b * (kMemoSets * 64));
-    uint4 v[kMemoSets * 16 / kCommitThreads];
-#pragma unroll
-    for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) v[q] = src[q * kCommitThreads + threadIdx.x];
-    uint2 lv[kLT / kCommitThreads];
-#pragma unroll
-    for (int q = 0; q < kLT / kCommitThreads; ++q) lv[q] = ws.lt[b * kLT + q * kCommitThreads + threadIdx.x];
+    const uint4 v = src[threadIdx.x];
+    const int32_t pcm = ws.meta[b * 4];
     const int32_t sv = threadIdx.x < kMemoSets ? ws.slist[b * kMemoSets + threadIdx.x] : -1;
     // the list of the row's set (set 0 of the pool), its byte codes and key:
     // the walk's list steps and the composed set mostly use that list
@@ -2409,10 +2418,9 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
     const int32_t lkv = l0 >= 0 && threadIdx.x < BPD_PDA_FRAME_KEY_WORDS
                             ? a.frames.keys[int64_t(l0) * BPD_PDA_FRAME_KEY_WORDS + threadIdx.x]
                             : 0;
-#pragma unroll
-    for (int q = 0; q < kMemoSets * 16 / kCommitThreads; ++q) trow[q * kCommitThreads + threadIdx.x] = v[q];
-#pragma unroll
-    for (int q = 0; q < kLT / kCommitThreads; ++q) lrow[q * kCommitThreads + threadIdx.x] = lv[q];
+    trow[threadIdx.x] = v;
+    const int pc = pcm < 0 ? 0 : (pcm > kMemoSets ? kMemoSets : pcm);
+    for (int q = kCommitThreads + threadIdx.x; q < pc * 16; q += kCommitThreads) trow[q] = src[q];
     if (threadIdx.x < kMemoSets) srow[threadIdx.x] = sv;
     ltrans[threadIdx.x] = ltv;
     if (threadIdx.x < BPD_PDA_FRAME_KEY_WORDS) lkey[threadIdx.x] = lkv;
@@ -2422,6 +2430,13 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
   __syncthreads();
   if (threadIdx.x >= kWave) return;
   const int own = row_l0;  // the list whose codes and key are staged
+  // the record holds the first 12 bytes when the workspace's records are of
+  // these tables at this row count (its stamp) and its length is the
+  // token's; the bytes past them (all, without it) one per lane, read only
+  // for a token that has any
+  const int32_t nrec = hk0 == uint32_t(pkey) && hk1 == uint32_t(pkey >> 32) && int32_t(tr.x) == e - s ? 12 : 0;
+  int32_t bl = 0;
+  if (walk_tok && e - s > nrec) bl = s + lane < e ? int32_t(a.tok_bytes[s + lane]) : 0;
   bool ok;
   if (!t_in) {
     if (lane == 0 && a.err) atomicOr(a.err, BPD_FLAG_TOKEN_RANGE);
@@ -2435,7 +2450,12 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
     ok = true;
     if (s < e) {
       auto byte_at = [&](int32_t i) -> int {
-        return i - s < kWave ? __shfl(bl, int(i - s)) : int(a.tok_bytes[i]);
+        const int32_t r = i - s;
+        if (r < nrec) {
+          const uint32_t w = r < 4 ? tr.y : (r < 8 ? tr.z : tr.w);
+          return int((w >> ((r & 3) * 8)) & 0xFFu);
+        }
+        return r < kWave ? __shfl(bl, int(r)) : int(a.tok_bytes[i]);
       };
       // walk the mask's tables while they have the entries, as the mask's
       // walk does: T for interned sets; for a set in a frame list whose T
@@ -2450,7 +2470,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
       bool exact = false;
       int32_t i = s;
       bool same0 = false;
-      if (pool && meta[0] == 1 && meta[1] == int32_t(uint32_t(tag)) && meta[2] == int32_t(uint32_t(tag >> 32)) &&
+      if (pool && meta[0] >= 1 && meta[1] == int32_t(uint32_t(tag)) && meta[2] == int32_t(uint32_t(tag >> 32)) &&
           uint32_t(meta[3]) == hdr) {
         // set 0 of the pool against the row's set (coop_same with the pool's
         // words already in registers)
@@ -2500,7 +2520,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
           const uint32_t h = lt_hash(key);
           int r = -1;
           for (int p = 0; p < kLT; ++p) {
-            const uint2 v = lrow[(h + uint32_t(p)) & uint32_t(kLT - 1)];
+            const uint2 v = ws.lt[b * kLT + ((h + uint32_t(p)) & uint32_t(kLT - 1))];
             if (v.x == key) {
               r = int(v.y);
               break;
@@ -2766,7 +2786,7 @@ static int launch_pda_mask(const BpdPdaTable* g, const BpdTokenBytes* toks, cons
       // at most one block per CU
       const int64_t pack_blocks = std::min<int64_t>((int64_t(toks->vocab_size) + 255) / 256, 256);
       pack_tokens_kernel<<<unsigned(pack_blocks), 256, 0, as_stream(stream)>>>(
-          toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta, ws.header, pkey);
+          toks->offsets, toks->bytes, toks->order, toks->vocab_size, ws.recs, ws.tmeta, ws.trecs, ws.header, pkey);
       BPD_LAUNCHED();
     }
     // BPD_PDA_MEMO_SETS lowers the interned-set limit (tests of the overflow path)
@@ -2877,10 +2897,10 @@ extern "C" int bpd_pda_advance(const BpdPdaTable* g, const BpdTokenBytes* toks, 
     if (int rc = lds_room(reinterpret_cast<const void*>(&pda_memo_advance_kernel<true>), 1, &room)) return rc;
     if (tab_bytes <= room)
       pda_memo_advance_kernel<true><<<unsigned(rows), kCommitThreads, tab_bytes, as_stream(stream)>>>(
-          a, ws, memo_tag(g, toks, rows));
+          a, ws, memo_tag(g, toks, rows), pack_key(toks, rows));
     else
       pda_memo_advance_kernel<false><<<unsigned(rows), kCommitThreads, 0, as_stream(stream)>>>(
-          a, ws, memo_tag(g, toks, rows));
+          a, ws, memo_tag(g, toks, rows), pack_key(toks, rows));
     BPD_LAUNCHED();
     return BPD_OK;
   }
