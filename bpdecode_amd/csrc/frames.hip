@@ -70,8 +70,10 @@ bool add(List& l, const Suffix& x) {
 
 // Closure and compaction of a suffix list: kBoundary when a config pops into
 // the common stack or pushes past kSuffix frames, kDead when none is left,
-// else 0 with the list in `l`; `sat` gets whether a config was dropped.
-int32_t close_list(const Tables& t, List& l, bool& sat) {
+// else 0 with the list in `l`; `sat` gets whether a config was dropped at
+// the cap, `pruned` whether the compaction dropped one (a set stepped so
+// keeps that config's words in slots past its last).
+int32_t close_list(const Tables& t, List& l, bool& sat, bool& pruned) {
   const BpdPdaTable& g = t.g;
   for (int i = 0; i < l.n; ++i) {
     const Suffix sfx = l.s[i];
@@ -101,11 +103,12 @@ int32_t close_list(const Tables& t, List& l, bool& sat) {
   int out = 0;
   for (int i = 0; i < l.n; ++i)
     if (t.live(l.s[i].f[l.s[i].len - 1])) l.s[out++] = l.s[i];
+  pruned = out < l.n;
   l.n = out;
   return out > 0 ? 0 : kDead;
 }
 
-int32_t step_list(const Tables& t, const List& src, int byte, List& out, bool& sat) {
+int32_t step_list(const Tables& t, const List& src, int byte, List& out, bool& sat, bool& pruned) {
   const BpdPdaTable& g = t.g;
   out.n = 0;
   sat = false;
@@ -119,7 +122,7 @@ int32_t step_list(const Tables& t, const List& src, int byte, List& out, bool& s
       sat = !add(out, x) || sat;
     }
   }
-  return close_list(t, out, sat);
+  return close_list(t, out, sat, pruned);
 }
 
 uint32_t mix32(uint32_t x) {
@@ -236,8 +239,8 @@ int frame_lists_impl(const BpdPdaTable* g, int32_t max_lists, int32_t* keys, int
     l.n = 1;
     l.s[0].len = 1;
     l.s[0].f[0] = s;
-    bool sat = false;
-    if (close_list(t, l, sat) == 0) intern(l);
+    bool sat = false, pruned = false;
+    if (close_list(t, l, sat, pruned) == 0) intern(l);
   }
   std::vector<int32_t> rows;
   for (size_t head = 0; head < lists.size(); ++head) {
@@ -257,11 +260,11 @@ int frame_lists_impl(const BpdPdaTable* g, int32_t max_lists, int32_t* keys, int
         continue;
       }
       List nx;
-      bool sat = false;
-      int32_t code = step_list(t, src, byte, nx, sat);
+      bool sat = false, pruned = false;
+      int32_t code = step_list(t, src, byte, nx, sat, pruned);
       if (code == 0) {
         const int32_t id = intern(nx);
-        code = id < 0 ? kBoundary : (id | (sat ? BPD_PDA_FRAME_SAT : 0));
+        code = id < 0 ? kBoundary : (id | (sat ? BPD_PDA_FRAME_SAT : 0) | (pruned ? 0 : BPD_PDA_FRAME_RAW));
       }
       memo.emplace(sig, code);
       rows.push_back(code);

@@ -315,7 +315,7 @@ extern "C" int bpd_host_build_reachability(const int32_t* trans, int32_t num_sta
 
 // Every (frame list, token) walk of the PDA mask's frame lists, split over
 // `threads` host threads by list.  trans[l][c]: the list byte c leads to
-// (or-ed with the saturation flag), -1 when the step empties the set, -2 at
+// (or-ed with the saturation and raw-words flags), -1 when the step empties the set, -2 at
 // a boundary.  A token is inside list l when every byte leads to a list;
 // its bit in allowed[l] is set unless it is EOS or empty.  The seeds of l are
 // the walk positions whose token meets a boundary, or is EOS or empty.
@@ -330,7 +330,7 @@ extern "C" int bpd_host_frame_classify(const int32_t* trans, int32_t num_lists, 
   for (int64_t i = 0; i < int64_t(num_lists) * 256; ++i) {
     const int32_t c = trans[i];
     BPD_REQUIRE(c == -1 || c == -2 || (c >= 0 && (c & (BPD_PDA_FRAME_SAT - 1)) < num_lists &&
-                                       (c & ~(BPD_PDA_FRAME_SAT | (BPD_PDA_FRAME_SAT - 1))) == 0),
+                                       (c & ~(BPD_PDA_FRAME_RAW | BPD_PDA_FRAME_SAT | (BPD_PDA_FRAME_SAT - 1))) == 0),
                 "frame transition %d out of range", c);
   }
   BPD_REQUIRE(tok_offsets[0] == 0, "token offsets start at %d", tok_offsets[0]);

@@ -1433,7 +1433,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
                                       : frame_list_of(wdst, a.frames, fslots, lane, &lbase);
           if (lane == 0) {
             cand_list[r] = lst >= 0 ? (lst | (wdst[1] != 0 ? BPD_PDA_FRAME_SAT : 0) | (lbase << kListBase)) : -1;
-            cand_comp[r] = code >= 0 ? 1 : 0;
+            cand_comp[r] = code >= 0 && (code & BPD_PDA_FRAME_RAW) == 0 ? 1 : 0;
           }
           if (found == -2 && !in_work) {
             int32_t* out = cand + r * kConfigWords;
@@ -1442,7 +1442,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           if (lane == 0) {
             cand_hash[r] = h;
             cand_res[r] = found;
-            cand_exact[r] = found >= 0 && raw && code < 0 ? 1 : 0;
+            cand_exact[r] = found >= 0 && raw && (code < 0 || (code & BPD_PDA_FRAME_RAW) != 0) ? 1 : 0;
           }
         }
         wave_sync();
@@ -2512,7 +2512,7 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
           if (code >= 0) {
             prev = cur;
             cur = (cur & ~0xFFF) | ((code & BPD_PDA_FRAME_SAT) != 0 ? 1 << 12 : 0) | (code & 0xFFF);
-            exact = false;
+            exact = (code & BPD_PDA_FRAME_RAW) != 0;
             continue;
           }
           // a boundary byte: the mask's LT entry, if it has one
@@ -2541,6 +2541,17 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
         ok = false;
       } else if (cur >= 0 && cur < kListState && i == e && exact) {
         for (int k = lane; k < kConfigWords; k += kWave) cfg[k] = pool[cur * kConfigWords + k];
+      } else if (cur >= kListState && i == e && exact) {
+        // the last byte is a list step whose compaction drops no config: the
+        // stepped set is, word for word, the one composed from the anchor's
+        // common stack and the list's key
+        const int anchor = (cur >> 13) & (kMemoSets - 1);
+        if (anchor > 0) {
+          for (int k = lane; k < kConfigWords; k += kWave) x[k] = pool[anchor * kConfigWords + k];
+          wave_sync();
+        }
+        compose_list_set(x, cfg, (cur & 0xFFF) == own ? lkey : a.frames.keys + int64_t(cur & 0xFFF) * BPD_PDA_FRAME_KEY_WORDS,
+                         srow[anchor] >> kListBase, (cur >> 12) & 1, lane);
       } else {
         if (cur >= 0 && i == e) {
           cur = prev;  // every byte had its entry: step the last one again

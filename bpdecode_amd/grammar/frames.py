@@ -40,6 +40,7 @@ SLOTS = 2048  # hash-table slots (staged in LDS by the mask kernel)
 MAX_LISTS = 1400  # at most 0.7 * SLOTS keys
 KEY_WORDS = 56  # n, 8 suffix lengths, 8 x MAX_SUFFIX frames, padding
 SAT = 0x10000  # transition flag: the step dropped a config at the 8-config cap
+RAW = 0x20000  # transition flag: the compaction dropped none (stepped words = composed words)
 EMPTY = 0xFFFFFFFF
 _CAP = 8  # configs per set
 _MAXD = 32  # frames per config
@@ -49,7 +50,7 @@ _MAXD = 32  # frames per config
 class FrameLists:
     """The lists on the tables' device: ``keys`` int32 [L, KEY_WORDS],
     ``slots`` int32 [SLOTS] (uint32 words: list id | fingerprint << 12, or
-    EMPTY), ``trans`` int32 [L, 256] (list reached | SAT, -1 empty, -2
+    EMPTY), ``trans`` int32 [L, 256] (list reached | SAT | RAW, -1 empty, -2
     boundary), ``allowed`` int32 [L, ceil(V/32)] (uint32 words), ``seed_off``
     int32 [L + 1] and ``seeds`` int32 walk positions."""
 

@@ -270,7 +270,10 @@ typedef struct BpdPdaTable {
  * positions seeds[seed_off[l] .. seed_off[l + 1]) (the tokens that meet a
  * boundary, EOS and the empty tokens; every other token not in allowed[l]
  * is rejected).  trans[l][c] is the list byte c leads to (or-ed with
- * BPD_PDA_FRAME_SAT when the step drops a config at the 8-config cap), -1
+ * BPD_PDA_FRAME_SAT when the step drops a config at the 8-config cap, and
+ * with BPD_PDA_FRAME_RAW when its compaction drops none: a set stepped by
+ * the byte then holds exactly the words composed from the list's key, every
+ * word past the configs' frames 0), -1
  * when it empties the set, -2 at a boundary: the device fills the
  * transition-table row of every such set it meets (a byte that keeps the
  * list and the saturation flag leads back to the set, a byte that empties
@@ -287,6 +290,7 @@ typedef struct BpdPdaTable {
 #define BPD_PDA_FRAME_SUFFIX 5
 #define BPD_PDA_FRAME_KEY_WORDS 56
 #define BPD_PDA_FRAME_SAT 0x10000
+#define BPD_PDA_FRAME_RAW 0x20000
 #define BPD_PDA_FRAME_EMPTY 0xFFFFFFFFu
 typedef struct BpdPdaFrames {
   int32_t num_lists;       /* 0 .. BPD_PDA_MAX_FRAME_LISTS */

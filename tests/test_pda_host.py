@@ -364,6 +364,10 @@ def _check_list(t, fl, order_np, cfg, l, base, vsize, what):
             sat = int(cfg[1]) | (1 if code & 0x10000 else 0)
             exp = _compose(fl["keys"][code & 0xFFFF], stack, sat)
             assert _meaningful(nxt) == _meaningful(exp), (what, byte)
+            # the raw flag: the oracle's stepped set is the composed one in
+            # every word exactly when the step's compaction dropped no config
+            # (a dropped config leaves its depth word past the last)
+            assert bool(code & 0x20000) == np.array_equal(nxt, exp), (what, byte)
 
 
 def test_frame_lists_against_the_oracle():
