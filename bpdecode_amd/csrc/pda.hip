@@ -533,6 +533,9 @@ __device__ inline bool coop_append(int32_t* dst, const int32_t* src, int i, int 
 // Lane i's value of v for a wave-uniform i with every lane active: a scalar
 // read of the register (no LDS round trip, unlike a shuffle).
 __device__ __forceinline__ int lane_value(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
+// v of the first active lane, for a v every active lane holds alike: the
+// compiler then keeps it in a scalar register and branches on it as such.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Sum of v over the wave, in every lane (every lane active): DPP exchanges
 // within each row of 16 lanes (lane ^ 1, lane ^ 2, then the half-row and row
@@ -2484,12 +2487,14 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
         same0 = coop_same(x, p0l, lane);
       }
       if (same0) {
+        // every lane walks alike: the values the walk branches on are made
+        // wave-uniform (scalar lane reads), so its control flow is scalar
         const uint8_t* T = reinterpret_cast<const uint8_t*>(trow);
         cur = 0;
         for (; i < e; ++i) {
-          const int byte = byte_at(i);
+          const int byte = uniform(byte_at(i));
           if (cur < kListState) {
-            const uint8_t nx = T[cur * 256 + byte];
+            const int nx = uniform(T[cur * 256 + byte]);
             if (nx == kTDead) {
               cur = -2;
               break;
@@ -2500,11 +2505,11 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
               exact = (nx & kTExact) != 0;
               continue;
             }
-            const int sl = a.frames.num_lists > 0 ? srow[cur] : -1;
+            const int sl = a.frames.num_lists > 0 ? uniform(srow[cur]) : -1;
             if (sl < 0) break;  // not resolved by the mask: step from here
             cur = list_state(cur, sl);
           }
-          const int code = (cur & 0xFFF) == own ? ltrans[byte] : a.frames.trans[(cur & 0xFFF) * 256 + byte];
+          const int code = uniform((cur & 0xFFF) == own ? ltrans[byte] : a.frames.trans[(cur & 0xFFF) * 256 + byte]);
           if (code == -1) {
             cur = -2;
             break;
@@ -2521,11 +2526,11 @@ __global__ __launch_bounds__(kCommitThreads) void pda_memo_advance_kernel(Advanc
           int r = -1;
           for (int p = 0; p < kLT; ++p) {
             const uint2 v = ws.lt[b * kLT + ((h + uint32_t(p)) & uint32_t(kLT - 1))];
-            if (v.x == key) {
-              r = int(v.y);
+            if (uniform(int(v.x)) == int(key)) {
+              r = uniform(int(v.y));
               break;
             }
-            if (v.x == kLTEmpty) break;
+            if (uniform(int(v.x)) == int(kLTEmpty)) break;
           }
           if (r == kTDead) {
             cur = -2;
