@@ -324,9 +324,13 @@ typedef struct BpdTokenBytes {
   const BpdPdaFrames* frames;
   /* optional (0 = none): a tag that identifies the contents of offsets,
    * bytes and order.  The device mask packs the token records into its
-   * workspace on every call unless the workspace header already carries
-   * this tag for the same row count (a workspace keeps them between calls;
-   * zero the first 256 bytes of a newly allocated workspace). */
+   * workspace unless the workspace header already carries this tag for the
+   * same row count (a workspace keeps them between calls): by a launch of
+   * its own the first time the process masks with the tag on the
+   * workspace, inside the mask after that.  Zero the first 256 bytes of a
+   * newly allocated workspace: the header also holds the mask's finish
+   * count and deferred-write slots, and a slot is trusted when it carries
+   * the launch's generation (never 0). */
   uint64_t pack_tag;
 } BpdTokenBytes;
 
