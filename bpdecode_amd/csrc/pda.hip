@@ -835,9 +835,11 @@ __device__ __forceinline__ uint32_t frame_mix(uint32_t x) {
 // slot table (`slots`, staged in LDS) 64 slots at a time up to the first
 // empty slot and compares the keys of fingerprint matches lane-parallel.
 // Called by the 64 lanes of a wave; every lane gets the answer (and, in
-// base_out, the depth of P).
+// base_out, the depth of P).  With `codes` (4 per lane), the byte codes of
+// the list found are read beside its key: lane l gets those of bytes l,
+// 64 + l, 128 + l and 192 + l.
 __device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const uint32_t* slots, int lane,
-                              int* base_out = nullptr) {
+                              int* base_out = nullptr, int32_t* codes = nullptr) {
   if (f.num_lists <= 0) return -1;
   const int n = c[0];
   if (n < 1 || n > kMaxConfigs) return -1;
@@ -889,6 +891,10 @@ __device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const uint
         m &= m - 1;
         const int id = int(uint32_t(lane_value(int(e), k)) & 0xFFFu);
         if (id < f.num_lists) {
+          if (codes) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) codes[q] = f.trans[id * 256 + q * kWave + lane];
+          }
           const bool diff = lane < BPD_PDA_FRAME_KEY_WORDS && f.keys[id * BPD_PDA_FRAME_KEY_WORDS + lane] != want;
           if (__ballot(diff) == 0u) {
             if (base_out) *base_out = base;
@@ -906,16 +912,17 @@ __device__ int frame_list_of(const int32_t* c, const BpdPdaFrames& f, const uint
 // keeps the list (and, unless the set is already saturated, drops nothing)
 // leads back to the set, a byte whose step empties it is dead; the other
 // entries stay unknown until a walk requests them.  One wave.
+__device__ inline void frame_fill_entry(int32_t code, int l, bool sat, int id, uint8_t* trow, int c) {
+  if (code == -1) {
+    trow[c] = kTDead;
+  } else if (code >= 0 && (code & (BPD_PDA_FRAME_SAT - 1)) == l && (sat || (code & BPD_PDA_FRAME_SAT) == 0)) {
+    trow[c] = uint8_t(id);
+  }
+}
+
 __device__ void frame_fill_row(const BpdPdaFrames& f, int l, bool sat, int id, uint8_t* trow, int lane) {
   const int32_t* tr = f.trans + l * 256;
-  for (int c = lane; c < 256; c += kWave) {
-    const int32_t code = tr[c];
-    if (code == -1) {
-      trow[c] = kTDead;
-    } else if (code >= 0 && (code & (BPD_PDA_FRAME_SAT - 1)) == l && (sat || (code & BPD_PDA_FRAME_SAT) == 0)) {
-      trow[c] = uint8_t(id);
-    }
-  }
+  for (int c = lane; c < 256; c += kWave) frame_fill_entry(tr[c], l, sat, id, trow, c);
 }
 
 // The meaningful words of the set of list `key` over the common stack that
@@ -1211,7 +1218,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     const int lane = tid - kWave;
     const bool dead = (a.broken != nullptr && a.broken[row] != 0) || !config_ok(row_cfg, a.g.num_states, lane);
     int base0 = 0;
-    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, lane, &base0);
+    int32_t codes[4] = {-2, -2, -2, -2};
+    const int l0 = dead ? -1 : frame_list_of(row_cfg, a.frames, fslots, lane, &base0, codes);
     if (lane == 0) {
       row_list = l0;
       const int sl0 = l0 >= 0 ? (l0 | (row_cfg[1] != 0 ? BPD_PDA_FRAME_SAT : 0) | (base0 << kListBase)) : -1;
@@ -1219,8 +1227,15 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       set_ls[0] = sl0 >= 0 ? list_state(0, sl0) : -1;
     }
     if (l0 >= 0) {
+      // T row 0 from the list's codes (read beside its key), which also
+      // fill the list's entries of the byte-table cache
       wave_sync();
-      frame_fill_row(a.frames, l0, row_cfg[1] != 0, 0, T, lane);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = q * kWave + lane;
+        frame_fill_entry(codes[q], l0, row_cfg[1] != 0, 0, T, c);
+        lcache[lc_slot(l0, c)] = lc_entry(l0, c, codes[q]);
+      }
     }
   }
   if (tid < kWave) {
@@ -1783,12 +1798,14 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       // byte 0; of a set in a frame list only the boundary intervals (the
       // others are walked as its list state or were filled from the list)
       // (wave 0: lane l takes bytes l, 64 + l, 128 + l, 192 + l, the list's
-      // codes for them read at once; four ballots are the eight request
-      // words, each stored by the thread that collects it)
+      // codes for them from the byte-table cache, which the prologue filled;
+      // four ballots are the eight request words, each stored by the thread
+      // that collects it)
       if (tid < kWave) {
         int code[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) code[q] = row_list >= 0 ? a.frames.trans[row_list * 256 + q * kWave + tid] : -2;
+        for (int q = 0; q < 4; ++q)
+          code[q] = row_list >= 0 ? list_code(a.frames, lcache, row_list, q * kWave + tid) : -2;
         uint64_t m[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1801,12 +1818,6 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         if (tid < 8) {
           const uint64_t mq = tid < 2 ? m[0] : (tid < 4 ? m[1] : (tid < 6 ? m[2] : m[3]));
           req[tid] = uint32_t(mq >> (32 * (tid & 1)));
-        }
-        // the same codes fill the list's entries of the byte-table cache
-        // (read by the walks after the round's barriers)
-        if (row_list >= 0) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) lcache[lc_slot(row_list, q * kWave + tid)] = lc_entry(row_list, q * kWave + tid, code[q]);
         }
       }
       resolve();
