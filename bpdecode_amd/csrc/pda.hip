@@ -1159,6 +1159,11 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   __shared__ int32_t grp_pre[258];    // runs: exclusive prefix of the live runs' lengths, then the total
   __shared__ int32_t grp_start[257];  // runs: first walk position of each live run
   __shared__ int pass_mode, pass_list, pass_total, pass_base, run_n, run_top;
+  // the first round's idle waves prepare the first pass of a row in a frame
+  // list (pre_round: this is that round; pre_pass: they did, pre_s0/pre_s1
+  // the list's seed bounds they read)
+  __shared__ int pre_round, pre_pass, pre_s0, pre_s1;
+  __shared__ uint32_t warm_sink;
   uint8_t* T = reinterpret_cast<uint8_t*>(T32);
 
   const int tid = threadIdx.x;
@@ -1204,6 +1209,8 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
   for (int q = 0; q < BPD_PDA_FRAME_SLOTS / kMemoThreads; ++q) fslots[q * kMemoThreads + tid] = fsv[q];
   const PdaTableView g = InLds ? stage_tables(a.g, tab, tsl, tid, kMemoThreads) : a.g;
   if (tid == 0) {
+    pre_round = 0;
+    pre_pass = 0;
     pool_count = 1;
     overflowed = 0;
     walk_lists = row_mode != 0 ? 1 : 0;
@@ -1465,6 +1472,28 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
         }
         wave_sync();
         r = r_next;
+      }
+      // in the first round of a row in a frame list the waves without a
+      // request read the list's verdict bitmap into vbits and its seed
+      // bounds, and read the first tile's seed entries and their records
+      // once, so that the first pass finds them in L2
+      if (pre_round && n < kMemoThreads / kWave && wave >= n) {
+        const int idle = kMemoThreads / kWave - n, w = wave - n;
+        const int l = row_list;
+        const uint32_t* al = a.frames.allowed + int64_t(l) * a.frames.words;
+        for (int i = w * kWave + lane; i < vwords; i += idle * kWave) vbits[i] = al[i];
+        const int32_t s0 = a.frames.seed_off[l], s1 = a.frames.seed_off[l + 1];
+        if (w == 0 && lane == 0) {
+          pre_s0 = s0;
+          pre_s1 = s1;
+          pre_pass = 1;
+        }
+        uint32_t acc = 0u;
+        for (int i = w * kWave + lane; i < kMemoThreads && s0 + i < s1; i += idle * kWave) {
+          const int32_t k = a.frames.seeds[s0 + i];
+          if (k >= 0 && k < V) acc ^= ws.recs[k].x ^ uint32_t(ws.tmeta[k].x);
+        }
+        if (acc == 0x9E3779B9u) atomicOr(&warm_sink, 1u);  // (keeps the reads)
       }
     }
     __syncthreads();
@@ -1819,8 +1848,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
           const uint64_t mq = tid < 2 ? m[0] : (tid < 4 ? m[1] : (tid < 6 ? m[2] : m[3]));
           req[tid] = uint32_t(mq >> (32 * (tid & 1)));
         }
+        if (tid == 0) pre_round = row_list >= 0 ? 1 : 0;
       }
       resolve();
+      if (tid == 0) pre_round = 0;
     }
     if (tid == 0) {
       qcount = 0;
@@ -1843,7 +1874,7 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     // state, EOS and the empty tokens).
     if (tid == 0 && !dead_row && !overflowed && row_list >= 0) {
       const int l = row_list;
-      const int32_t s0 = a.frames.seed_off[l], s1 = a.frames.seed_off[l + 1];
+      const int32_t s0 = pre_pass ? pre_s0 : a.frames.seed_off[l], s1 = pre_pass ? pre_s1 : a.frames.seed_off[l + 1];
       pass_list = l;
       pass_mode = 2;
       pass_base = s0;
@@ -1851,8 +1882,10 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     }
     __syncthreads();
     if (pass_list >= 0) {  // (pass_mode is written below; pass_list is not)
-      const uint32_t* al = a.frames.allowed + int64_t(pass_list) * a.frames.words;
-      for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = al[i];
+      if (!pre_pass) {
+        const uint32_t* al = a.frames.allowed + int64_t(pass_list) * a.frames.words;
+        for (int i = tid; i < vwords; i += kMemoThreads) vbits[i] = al[i];
+      }
     } else if (a.runs && !dead_row && !overflowed && tid < kWave) {
       // first-byte runs: the run of byte c is walked unless the byte
       // empties set 0 (T[0][c] dead); lane l owns runs 4l..4l+3, lane 63
