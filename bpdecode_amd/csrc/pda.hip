@@ -1861,26 +1861,25 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
       pass_list = -1;
       pass_total = dead_row ? 0 : int(V);  // a dead row rejects every token: nothing to walk
       pass_base = 0;
+      // Frame lists: a row whose configs share one stack below their tops
+      // (depth >= 2) and whose ordered tops are a list's key takes the
+      // tokens that stay inside the tops' call-free rule from the list's
+      // bitmap and walks only the list's seeds (the tokens that reach the
+      // rule's accept state, EOS and the empty tokens).
+      if (!dead_row && !overflowed && row_list >= 0) {
+        const int l = row_list;
+        const int32_t s0 = pre_pass ? pre_s0 : a.frames.seed_off[l], s1 = pre_pass ? pre_s1 : a.frames.seed_off[l + 1];
+        pass_list = l;
+        pass_mode = 2;
+        pass_base = s0;
+        pass_total = s1 > s0 ? s1 - s0 : 0;
+      }
     }
     __syncthreads();
     if (tid < 256) {
       loop0[tid] = T[tid] == 0 ? 1 : 0;
       if (T[tid] == 0) atomicAdd(&loop_n, 1);
     }
-    // Frame lists: a row whose configs share one stack below their tops
-    // (depth >= 2) and whose ordered tops are a list's key takes the tokens
-    // that stay inside the tops' call-free rule from the list's bitmap and
-    // walks only the list's seeds (the tokens that reach the rule's accept
-    // state, EOS and the empty tokens).
-    if (tid == 0 && !dead_row && !overflowed && row_list >= 0) {
-      const int l = row_list;
-      const int32_t s0 = pre_pass ? pre_s0 : a.frames.seed_off[l], s1 = pre_pass ? pre_s1 : a.frames.seed_off[l + 1];
-      pass_list = l;
-      pass_mode = 2;
-      pass_base = s0;
-      pass_total = s1 > s0 ? s1 - s0 : 0;
-    }
-    __syncthreads();
     if (pass_list >= 0) {  // (pass_mode is written below; pass_list is not)
       if (!pre_pass) {
         const uint32_t* al = a.frames.allowed + int64_t(pass_list) * a.frames.words;
