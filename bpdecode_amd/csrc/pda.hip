@@ -2171,9 +2171,12 @@ __global__ __launch_bounds__(kMemoThreads) void pda_memo_mask_kernel(MaskArgs a,
     tile += int64_t(kMemoThreads) * kMemoTok;
   }
   __syncthreads();
-  // keep the transition table for the commit of this step
+  // keep the transition table for the commit of this step (the rows of the
+  // interned sets: the commit reads no other, their count is in the row's
+  // metadata)
   uint32_t* tout = ws.table + b * (kMemoSets * 64);
-  for (int i = tid; i < kMemoSets * 64; i += kMemoThreads) {
+  const int t_rows = pool_count < max_sets ? pool_count : max_sets;
+  for (int i = tid; i < t_rows * 64; i += kMemoThreads) {
     const uint32_t v = T32[i];
     const int c = (i & 63) * 4;
     const uint32_t nib = (texact[(i >> 6) * 8 + (c >> 5)] >> (c & 31)) & 0xFu;
