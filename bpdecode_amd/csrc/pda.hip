@@ -299,8 +299,8 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 // own.  The slots carry the launch's generation and the finish count runs
 // on (the launch after a mask copies it as the next launch's base), so no
 // launch has to clear them.
-constexpr int kDefer = 8;
-constexpr int kDeferBlocks = 64;
+constexpr int kDefer = 4;
+constexpr int kDeferBlocks = 128;
 constexpr int kFinishWord = 8;
 constexpr int kDeferWord = 16;
 static_assert(kDeferWord + 2 * kDefer <= 64, "deferred slots in the workspace header");

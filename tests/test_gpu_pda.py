@@ -722,7 +722,7 @@ def test_token_records_repacked_when_workspace_overwritten(dev, json_case):
     and key already packed by this process, so the mask checks the stamp
     itself, finds garbage and packs the records in every block before
     walking; the third takes them as they are.  Bits and fp32 logits at
-    B=16, V=151,936 (the last eight rows to finish leave their logits to the
+    B=16, V=151,936 (the last four rows to finish leave their logits to the
     launch after the mask), each call against the oracle."""
     from bpdecode_amd._lib import DTYPE_F32, check, lib, ptr
 
