@@ -723,8 +723,12 @@ def test_token_records_repacked_when_workspace_overwritten(dev, json_case):
     itself, finds garbage and packs the records in every block before
     walking; the third takes them as they are.  Bits and fp32 logits at
     B=16, V=151,936 (the last four rows to finish leave their logits to the
-    launch after the mask), each call against the oracle."""
-    from bpdecode_amd._lib import DTYPE_F32, check, lib, ptr
+    launch after the mask), each call against the oracle.  After each logits
+    mask a commit on the same workspace (whose transition rows past the
+    interned sets still hold the 0xAB fill after the overwrite) advances a
+    copy of the config-sets by an allowed token per row (token 0 where none
+    is), raw words and ok flags against the oracle."""
+    from bpdecode_amd._lib import DTYPE_F32, check, index_code, lib, ptr
 
     vocab, g, t = json_case
     gd = g.to(dev)
@@ -754,3 +758,17 @@ def test_token_records_repacked_when_workspace_overwritten(dev, json_case):
                 ref = lg.numpy().copy()
                 OP.apply_mask(t, cfgs.numpy(), ref)
                 assert np.array_equal(got.cpu().numpy(), ref), call
+                allowed = np.unpackbits(want_bits.view(np.uint8), axis=1, bitorder="little")[:, :V]
+                pick = np.random.default_rng(13)
+                toks = np.array([pick.choice(np.flatnonzero(r)) if r.any() else 0 for r in allowed], dtype=np.int32)
+                adv = pool.clone()
+                tk = torch.from_numpy(toks).to(dev)
+                ok = torch.empty(B, dtype=torch.uint8, device=dev)
+                status = torch.empty(B, dtype=torch.int32, device=dev)
+                check(lib().bpd_pda_advance(gd.c_table(), gd.c_tokens(), ptr(adv), None, ptr(tk),
+                                            index_code(torch.int32), B, ptr(ok), None, ptr(status), None,
+                                            ptr(ws), need, stream))
+                mirror = cfgs.numpy().copy()
+                ok_o = OP.advance(t, mirror, toks)
+                assert ok.cpu().numpy().tolist() == ok_o.tolist(), call
+                assert np.array_equal(adv.cpu().numpy(), mirror), call
